@@ -1,0 +1,140 @@
+/* mxfp4_hip.h -- C ABI of the MI355X (gfx950) MXFP4 MoE hot path.
+ *
+ * Plain C: device pointers, sizes and a HIP stream passed as void*
+ * (a hipStream_t; NULL = the default stream).  No torch types.  Every entry
+ * point validates its arguments on the host, launches asynchronously on the
+ * given stream, and returns MXFP4_OK (0), MXFP4_EINVAL (-1, see
+ * mxfp4_last_error()) or a positive hipError_t from the launch.
+ *
+ * Data formats (unchanged from the reference, quant/quantize_mxfp4.py:110-160):
+ *   packed MXFP4 rows  u8 (rows, Kp/2): two E2M1 nibbles per byte, element 2j
+ *                      in the low nibble (quant/fp4_format.py:126-137);
+ *   scale codes        u8 (rows, Kp/32): E8M0, value 2^(code-127);
+ *   Kp = ceil(K/32)*32, padding elements are zero.
+ * Quantization is bit-exact to quant/fp4_format.py (E2M1 ties to the larger
+ * magnitude; smallest power-of-two scale with amax/scale <= 6).
+ */
+#ifndef MXFP4_HIP_H
+#define MXFP4_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MXFP4_HIP_ABI_VERSION 1
+
+enum {
+    MXFP4_OK = 0,
+    MXFP4_EINVAL = -1,   /* argument check failed; message in mxfp4_last_error() */
+    MXFP4_ETIMEOUT = -2  /* a fused kernel's bounded wait expired (see mxfp4_decode_status) */
+};
+
+/* Activation dtypes accepted by the quantizers. */
+enum { MXFP4_DT_BF16 = 0, MXFP4_DT_F16 = 1, MXFP4_DT_F32 = 2 };
+
+/* Largest pointer table passed by value to one grouped launch; longer tables
+ * are processed in several launches. */
+#define MXFP4_MAX_TABLE 160
+
+int mxfp4_abi_version(void);
+/* Message of the last MXFP4_EINVAL on the calling thread ("" if none). */
+const char* mxfp4_last_error(void);
+
+/* ---------------------------------------------------------------------
+ * Activation quantizer.
+ * Replaces mxfp4v2::launch_prequant_v2 (src/ext/mxfp4_decode.cu:304-309),
+ * bound as `prequant` (src/ext/mxfp4_decode_binding.cpp:65-81).
+ * x: bf16 (M, K) with row stride ldx elements; writes every byte of
+ * xq (M, Kp/2) and xsc (M, Kp/32).  Kp must be a multiple of 32 and >= K.
+ * Unlike src/ext/mxfp4_decode.cu:46 the last element of an odd K is packed
+ * (quant/fp4_format.py contract).
+ */
+int mxfp4_prequant(const void* x, int64_t ldx, int M, int K, int Kp,
+                   uint8_t* xq, uint8_t* xsc, void* stream);
+
+/* Same quantizer for bf16 / fp16 / fp32 rows (src_dtype = MXFP4_DT_*).
+ * With round_to_f16 != 0 each element is first rounded to fp16, as the
+ * reference's `forward` does (src/ext/mxfp4_binding.cpp:31). */
+int mxfp4_quantize_rows(const void* x, int src_dtype, int round_to_f16, int64_t ldx,
+                        int M, int K, int Kp, uint8_t* q, uint8_t* s, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Block-scaled GEMM on pre-quantized activations: y (M, N) fp32 = A_q * W_q^T.
+ * Replaces mxfp4v2::launch_lin_pq_v2 (src/ext/mxfp4_decode.cu:311-318),
+ * bound as `lin_pq` (src/ext/mxfp4_decode_binding.cpp:84-98).
+ * xq (M, Kp/2), xsc (M, Kp/32), wp (N, Kp/2), wsc (N, Kp/32).  The sum runs
+ * over all Kp (activation padding must be zero nibbles, as prequant writes).
+ */
+int mxfp4_lin_pq(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp,
+                 const uint8_t* wsc, float* y, int M, int N, int K, int Kp,
+                 void* stream);
+
+/* ---------------------------------------------------------------------
+ * Linear with on-the-fly activation quantization: y (M, N) fp32.
+ * Replaces mxfp4::launch_mxfp4_linear (src/ext/mxfp4_linear.cu:200-206),
+ * bound as `forward` (src/ext/mxfp4_binding.cpp:21-45).
+ * x (M, K) bf16 or fp16 (x_dtype), contiguous.  Activations are rounded to
+ * fp16 first (src/ext/mxfp4_binding.cpp:31), then quantized per 32-block over
+ * the weight's Kp into `workspace` (>= mxfp4_linear_workspace_size bytes,
+ * device memory), then multiplied.
+ */
+size_t mxfp4_linear_workspace_size(int M, int Kp);
+int mxfp4_linear_forward(const void* x, int x_dtype, const uint8_t* wp,
+                         const uint8_t* wsc, float* y, int M, int N, int K, int Kp,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Grouped gate/up projection over a token-major pointer table.
+ * Replaces mxfp4v2::launch_gateup_v2 (src/ext/mxfp4_decode.cu:320-328),
+ * bound as `moe_gateup` (src/ext/mxfp4_decode_binding.cpp:101-120).
+ * Table entry t = m*2E + proj*E + e (runtime/model_runner_v2.py:279-286)
+ * holds the weight (N, Kp/2) + scales (N, Kp/32) applied to activation row
+ * m of xq/xsc; the result goes to gu[(m*E+e)*2N + proj*N + n] (fp32,
+ * (M*E, 2N)).  Entries with identical weight pointers share one pass over
+ * the weight.  The tables are host arrays of 2*E*M device pointers; they are
+ * passed by value in kernel arguments (no host-blocking copy, unlike
+ * src/ext/mxfp4_decode_binding.cpp:44-60).
+ */
+int mxfp4_moe_gateup(const uint8_t* xq, const uint8_t* xsc,
+                     const uint8_t* const* wp_tab, const uint8_t* const* wsc_tab,
+                     float* gu, int E, int M, int N, int K, int Kp, void* stream);
+
+/* As mxfp4_moe_gateup with the tables in device memory (int64 pointers),
+ * bound as `moe_gateup_tab` (src/ext/mxfp4_decode_binding.cpp:177-192). */
+int mxfp4_moe_gateup_devtab(const uint8_t* xq, const uint8_t* xsc,
+                            const int64_t* wp_tab, const int64_t* wsc_tab,
+                            float* gu, int E, int M, int N, int K, int Kp, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Fused SiLU-gate + MXFP4 re-quantization + down projection.
+ * Replaces mxfp4v2::launch_down_silu_v2 (src/ext/mxfp4_decode.cu:330-338),
+ * bound as `moe_down` (src/ext/mxfp4_decode_binding.cpp:123-142).
+ * For row z = m*E+e of gu (M*E, 2K): h = g/(1+exp(-g))*u in fp32 with
+ * g = gu[z, 0:K], u = gu[z, K:2K]; h is quantized per 32-block (zero past
+ * K) and multiplied with table entry z (N, Kp/2); yd (M*E, N) fp32.
+ */
+int mxfp4_moe_down(const float* gu, const uint8_t* const* wp_tab,
+                   const uint8_t* const* wsc_tab, float* yd, int E, int M, int N,
+                   int K, int Kp, void* stream);
+
+/* As mxfp4_moe_down with device tables, bound as `moe_down_tab`
+ * (src/ext/mxfp4_decode_binding.cpp:194-209). */
+int mxfp4_moe_down_devtab(const float* gu, const int64_t* wp_tab, const int64_t* wsc_tab,
+                          float* yd, int E, int M, int N, int K, int Kp, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Weighted top-k combine: out[m, c] = sum_{e < min(E, 8)} w[m, e] * yd[m*E+e, c].
+ * Replaces mxfp4v2::launch_combine_v2 (src/ext/mxfp4_decode.cu:340-344),
+ * bound as `moe_combine` (src/ext/mxfp4_decode_binding.cpp:145-158).  Slots
+ * past 8 are ignored exactly as the reference does (src/ext/mxfp4_decode.cu:296).
+ */
+int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
+                      float* out, int M, int N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MXFP4_HIP_H */

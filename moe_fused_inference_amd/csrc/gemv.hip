@@ -1,0 +1,446 @@
+// gemv.hip -- grouped small-M block-scaled MFMA GEMV for gfx950.
+//
+// Serves the reference's decode operators on token-major pointer tables:
+//   moe_gateup  (src/ext/mxfp4_decode.cu:177-212)  A = pre-quantized MXFP4 rows
+//   moe_down    (src/ext/mxfp4_decode.cu:218-279)  A = MXFP4(silu(g)*u), built in LDS
+//   lin_pq, M <= 16 rows (src/ext/mxfp4_decode.cu:135-170)
+// and the weighted combine (src/ext/mxfp4_decode.cu:285-299).
+//
+// Design (MI355X-first rather than a translation of the sm_120a kernels):
+// * One v_mfma_scale_f32_16x16x128_f8f6f4 consumes packed E2M1 + E8M0 for 16
+//   weight rows x 128 K straight from registers: no nibble unpacking, no
+//   dequant VALU work.  The activation rows (tokens) form the A operand, so a
+//   weight row is read once for every token routed to it.
+// * Table entries whose weight pointers are equal are grouped inside the
+//   kernel (first occurrence owns the group, others exit): at M=9 speculative
+//   verify an expert shared by several tokens is streamed from HBM once,
+//   where the reference re-reads it per token.
+// * Each lane streams 16 contiguous bytes per MFMA step and its lane group
+//   (l/16) owns a contiguous run of 32-blocks of the row (block permutation
+//   is free because A and B lanes pair on the same K set), so scale bytes and
+//   data are contiguous per lane.  Weight loads for a K segment are issued
+//   before the MFMAs of the previous segment (software prefetch).
+// * The pointer tables travel by value in the kernel arguments, replacing the
+//   reference's host-blocking H2D table copy (src/ext/mxfp4_decode_binding.cpp:58).
+#include "mx_device.h"
+#include "mx_host.h"
+
+namespace {
+
+constexpr int kMaxT = MXFP4_MAX_TABLE;
+constexpr int kSeg = 8;  // MFMA K-steps (1024 K) per prefetch segment
+
+struct HostTable {
+    const uint8_t* wp[kMaxT];
+    const uint8_t* ws[kMaxT];
+    __device__ __forceinline__ const uint8_t* w(int i) const { return wp[i]; }
+    __device__ __forceinline__ const uint8_t* s(int i) const { return ws[i]; }
+};
+struct DevTable {
+    const int64_t* wp;
+    const int64_t* ws;
+    __device__ __forceinline__ const uint8_t* w(int i) const { return reinterpret_cast<const uint8_t*>(wp[i]); }
+    __device__ __forceinline__ const uint8_t* s(int i) const { return reinterpret_cast<const uint8_t*>(ws[i]); }
+};
+
+enum { MAP_PLAIN = 0, MAP_GATEUP = 1 };
+enum { A_FP4 = 0, A_SILU = 1 };
+
+struct GemvArgs {
+    int T;     // entries in this launch
+    int t0;    // global table index of local entry 0
+    int E;     // slots per token (token-major mapping)
+    int map;   // MAP_*
+    int N;     // weight rows
+    int K;     // logical K (A_SILU: gu row stride is 2K)
+    int Kp;    // padded K of weights and activations
+    const uint8_t* aq;  // A_FP4: (rows, Kp/2)
+    const uint8_t* as;  // A_FP4: (rows, Kp/32)
+    const float* gu;    // A_SILU: (rows, 2K)
+    float* out;
+    int64_t ld_out;
+};
+
+struct EntryMap {
+    int src, dst, col;
+};
+
+__device__ __forceinline__ EntryMap map_entry(const GemvArgs& a, int tg) {
+    EntryMap r;
+    if (a.map == MAP_GATEUP) {
+        // t = m*2E + proj*E + e  (src/ext/mxfp4_decode.cu:187-195)
+        const int m = tg / (2 * a.E);
+        const int rem = tg - m * 2 * a.E;
+        const int proj = rem / a.E;
+        const int e = rem - proj * a.E;
+        r.src = m;
+        r.dst = m * a.E + e;
+        r.col = proj * a.N;
+    } else {
+        r.src = tg;
+        r.dst = tg;
+        r.col = 0;
+    }
+    return r;
+}
+
+// One prefetch segment of kSeg MFMA K-steps: weight (B) data + scales, and
+// for A_FP4 the activation (A) data + scales.  Separate named buffers keep
+// all register indices static.
+struct SegBuf {
+    uint4 b[kSeg];
+    uint32_t bs[kSeg];
+    uint4 a[kSeg];
+    uint32_t as[kSeg];
+};
+
+struct SegCtx {
+    const uint8_t* wrow;   // this lane's weight row
+    const uint8_t* srow;   // its scale row
+    const uint8_t* arow;   // A_FP4: activation row
+    const uint8_t* asrow;  // A_FP4: activation scale row
+    const uint8_t* lq;     // A_SILU: LDS row of quantized h
+    const uint8_t* lsc;    // A_SILU: LDS scale row
+    int cbase, steps, nch;
+    bool arow_ok;
+};
+
+template <int AMODE>
+__device__ __forceinline__ void load_seg(SegBuf& sb, const SegCtx& cx, int s0) {
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+        const int s = s0 + j;
+        const int c = cx.cbase + s;
+        const bool ok = (s < cx.steps) && (c < cx.nch);
+        sb.b[j] = ok ? *reinterpret_cast<const uint4*>(cx.wrow + c * 16) : make_uint4(0, 0, 0, 0);
+        sb.bs[j] = ok ? (uint32_t)cx.srow[c] : 127u;
+        if (AMODE == A_FP4) {
+            const bool aok = ok && cx.arow_ok;
+            sb.a[j] = aok ? *reinterpret_cast<const uint4*>(cx.arow + c * 16) : make_uint4(0, 0, 0, 0);
+            sb.as[j] = aok ? (uint32_t)cx.asrow[c] : 127u;
+        }
+    }
+}
+
+template <int AMODE>
+__device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& cx, int s0, mx::v4f acc) {
+#pragma unroll
+    for (int j = 0; j < kSeg; ++j) {
+        const int s = s0 + j;
+        if (s < cx.steps) {
+            uint4 aq;
+            uint32_t asc;
+            if (AMODE == A_FP4) {
+                aq = sb.a[j];
+                asc = sb.as[j];
+            } else {
+                const int c = cx.cbase + s;
+                const bool ok = c < cx.nch;
+                aq = ok ? *reinterpret_cast<const uint4*>(cx.lq + c * 16) : make_uint4(0, 0, 0, 0);
+                asc = ok ? (uint32_t)cx.lsc[c] : 127u;
+            }
+            acc = mx::mfma16_fp4(aq, sb.b[j], acc, asc, sb.bs[j]);
+        }
+    }
+    return acc;
+}
+
+template <class Tab, int AMODE>
+__global__ __launch_bounds__(256) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
+    extern __shared__ __align__(16) uint8_t s_dyn[];  // A_SILU: 16 rows of quantized h
+    __shared__ int s_rows[kMaxT];
+    __shared__ int s_cnt, s_first;
+
+    const int t = blockIdx.y;
+    if (t >= a.T) return;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const uint8_t* wp = tab.w(t);
+    const uint8_t* ws = tab.s(t);
+
+    // ---- grouping: the first entry with this weight owns all of its rows
+    if (wave == 0) {
+        bool dup = false;
+        for (int j = lane; j < t; j += 64) dup |= (tab.w(j) == wp) && (tab.s(j) == ws);
+        const bool any = __ballot(dup) != 0ull;
+        int cnt = 0;
+        if (!any) {
+            for (int j0 = t; j0 < a.T; j0 += 64) {
+                const int j = j0 + lane;
+                const bool m = (j < a.T) && (tab.w(j) == wp) && (tab.s(j) == ws);
+                const unsigned long long b = __ballot(m);
+                if (m) s_rows[cnt + __popcll(b & ((1ull << lane) - 1ull))] = j;
+                cnt += __popcll(b);
+            }
+        }
+        if (lane == 0) {
+            s_first = any ? 0 : 1;
+            s_cnt = cnt;
+        }
+    }
+    __syncthreads();
+    if (!s_first) return;
+    const int cnt = s_cnt;
+
+    const int nch = a.Kp >> 5;            // 32-blocks per row
+    const int steps = (nch + 3) >> 2;     // MFMA K-steps; lane group g owns blocks [g*steps, g*steps+steps)
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = blockIdx.x * 64 + wave * 16;
+    const int nrow = min(n0 + r, a.N - 1);
+    const uint8_t* wrow = wp + (int64_t)nrow * (a.Kp >> 1);
+    const uint8_t* srow = ws + (int64_t)nrow * nch;
+    const int cbase = g * steps;
+
+    uint8_t* sq = s_dyn;                              // [16][Kp/2]
+    uint8_t* ssc = s_dyn + 16 * (a.Kp >> 1);          // [16][nch]
+
+    for (int rt = 0; rt < cnt; rt += 16) {
+        if (AMODE == A_SILU) {
+            // Build the 16-row A tile: h = silu(g)*u (fp32) quantized per
+            // 32-block with the bit-exact rule; rows past the group are zero.
+            const int upr = a.Kp >> 3;
+            for (int u = threadIdx.x; u < 16 * upr; u += 256) {
+                const int rr = u / upr;
+                const int uu = u - rr * upr;
+                const int k0 = uu * 8;
+                float h[8];
+                if (rt + rr < cnt) {
+                    const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
+                    const float* grow = a.gu + (int64_t)em.src * 2 * a.K;
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) {
+                        const int k = k0 + i;
+                        h[i] = (k < a.K) ? mx::silu_mul(grow[k], grow[a.K + k]) : 0.0f;
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) h[i] = 0.0f;
+                }
+                float am = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(h[i]));
+                am = fmaxf(am, __shfl_xor(am, 1));
+                am = fmaxf(am, __shfl_xor(am, 2));
+                const uint32_t code = mx::e8m0_code(am);
+                *reinterpret_cast<uint32_t*>(sq + rr * (a.Kp >> 1) + uu * 4) =
+                    mx::e2m1_pack8(h, mx::e8m0_inv_scale(code));
+                if ((uu & 3) == 0) ssc[rr * nch + (uu >> 2)] = (uint8_t)code;
+            }
+            __syncthreads();
+        }
+
+        // A-operand source row of this lane (row r of the tile)
+        const bool arow_ok = (rt + r) < cnt;
+        int asrc = 0;
+        if (AMODE == A_FP4 && arow_ok) asrc = map_entry(a, a.t0 + s_rows[rt + r]).src;
+        const uint8_t* arow = a.aq + (int64_t)asrc * (a.Kp >> 1);
+        const uint8_t* asrow = a.as + (int64_t)asrc * nch;
+
+        mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+        SegBuf s0buf, s1buf;
+        const SegCtx cx{wrow, srow, arow, asrow, sq + r * (a.Kp >> 1), ssc + r * nch,
+                        cbase, steps, nch, arow_ok};
+        load_seg<AMODE>(s0buf, cx, 0);
+        for (int s0 = 0; s0 < steps; s0 += 2 * kSeg) {
+            if (s0 + kSeg < steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
+            acc = compute_seg<AMODE>(s0buf, cx, s0, acc);
+            if (s0 + kSeg >= steps) break;
+            if (s0 + 2 * kSeg < steps) load_seg<AMODE>(s0buf, cx, s0 + 2 * kSeg);
+            acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
+        }
+
+        // D[4*(l/16)+i][l%16]: token row, weight row
+        const int col = n0 + r;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int rr = 4 * g + i;
+            if (rt + rr < cnt && col < a.N) {
+                const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
+                a.out[(int64_t)em.dst * a.ld_out + em.col + col] = acc[i];
+            }
+        }
+        if (AMODE == A_SILU) __syncthreads();  // LDS tile reused by the next row tile
+    }
+}
+
+__global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ yd, int ystride,
+                                                      const float* __restrict__ w, int E,
+                                                      float* __restrict__ out, int M, int N) {
+    const int m = blockIdx.y;
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= N) return;
+    const float* yb = yd + (int64_t)m * E * ystride;
+    const float* wb = w + (int64_t)m * E;
+    float acc = 0.0f;
+    const int ee = E < 8 ? E : 8;  // src/ext/mxfp4_decode.cu:296 caps at 8 slots
+    for (int e = 0; e < ee; ++e) acc = fmaf(wb[e], yb[(int64_t)e * ystride + c], acc);
+    out[(int64_t)m * N + c] = acc;
+}
+
+size_t silu_lds_bytes(int Kp) { return (size_t)16 * ((Kp >> 1) + (Kp >> 5)); }
+
+template <class Tab>
+int launch_gemv(const Tab& tab, const GemvArgs& a, int amode, hipStream_t st) {
+    dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.T);
+    if (amode == A_FP4) {
+        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4>), grid, dim3(256), 0, st, tab, a);
+    } else {
+        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU>), grid, dim3(256), silu_lds_bytes(a.Kp), st, tab, a);
+    }
+    return mxh::launch_status("grouped_gemv");
+}
+
+// Runs a host table of T entries in launches of at most kMaxT entries.
+int run_host_table(const uint8_t* const* wp_tab, const uint8_t* const* ws_tab, int T, GemvArgs a,
+                   int amode, hipStream_t st) {
+    for (int c0 = 0; c0 < T; c0 += kMaxT) {
+        HostTable tab;
+        const int n = (T - c0) < kMaxT ? (T - c0) : kMaxT;
+        for (int i = 0; i < kMaxT; ++i) {
+            tab.wp[i] = i < n ? wp_tab[c0 + i] : nullptr;
+            tab.ws[i] = i < n ? ws_tab[c0 + i] : nullptr;
+        }
+        for (int i = 0; i < n; ++i)
+            MXH_REQUIRE(tab.wp[i] && tab.ws[i], "pointer table entry %d is null", c0 + i);
+        a.T = n;
+        a.t0 = c0;
+        const int rc = launch_gemv(tab, a, amode, st);
+        if (rc != MXFP4_OK) return rc;
+    }
+    return MXFP4_OK;
+}
+
+int run_dev_table(const int64_t* wp_tab, const int64_t* ws_tab, int T, GemvArgs a, int amode,
+                  hipStream_t st) {
+    for (int c0 = 0; c0 < T; c0 += kMaxT) {
+        DevTable tab{wp_tab + c0, ws_tab + c0};
+        a.T = (T - c0) < kMaxT ? (T - c0) : kMaxT;
+        a.t0 = c0;
+        const int rc = launch_gemv(tab, a, amode, st);
+        if (rc != MXFP4_OK) return rc;
+    }
+    return MXFP4_OK;
+}
+
+int check_common(int E, int M, int N, int K, int Kp, const char* op) {
+    MXH_REQUIRE(E > 0 && M > 0 && N > 0 && K > 0, "%s: sizes must be positive (E=%d M=%d N=%d K=%d)", op, E, M, N, K);
+    MXH_REQUIRE(Kp % 32 == 0 && Kp >= K, "%s: Kp=%d must be a multiple of 32 and >= K=%d", op, Kp, K);
+    return MXFP4_OK;
+}
+
+}  // namespace
+
+namespace mxh {
+// Small-M lin_pq through the grouped GEMV (one group of M rows).
+int lin_pq_gemv(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc,
+                float* y, int M, int N, int K, int Kp, hipStream_t st) {
+    GemvArgs a{};
+    a.E = 1;
+    a.map = MAP_PLAIN;
+    a.N = N;
+    a.K = K;
+    a.Kp = Kp;
+    a.aq = xq;
+    a.as = xsc;
+    a.out = y;
+    a.ld_out = N;
+    for (int c0 = 0; c0 < M; c0 += kMaxT) {
+        HostTable tab;
+        const int n = (M - c0) < kMaxT ? (M - c0) : kMaxT;
+        for (int i = 0; i < kMaxT; ++i) {
+            tab.wp[i] = wp;
+            tab.ws[i] = wsc;
+        }
+        a.T = n;
+        a.t0 = c0;
+        const int rc = launch_gemv(tab, a, A_FP4, st);
+        if (rc != MXFP4_OK) return rc;
+    }
+    return MXFP4_OK;
+}
+}  // namespace mxh
+
+extern "C" int mxfp4_moe_gateup(const uint8_t* xq, const uint8_t* xsc, const uint8_t* const* wp_tab,
+                                const uint8_t* const* wsc_tab, float* gu, int E, int M, int N, int K,
+                                int Kp, void* stream) {
+    int rc = check_common(E, M, N, K, Kp, "moe_gateup");
+    if (rc) return rc;
+    MXH_REQUIRE(xq && xsc && wp_tab && wsc_tab && gu, "moe_gateup: null pointer");
+    GemvArgs a{};
+    a.E = E;
+    a.map = MAP_GATEUP;
+    a.N = N;
+    a.K = K;
+    a.Kp = Kp;
+    a.aq = xq;
+    a.as = xsc;
+    a.out = gu;
+    a.ld_out = 2 * (int64_t)N;
+    return run_host_table(wp_tab, wsc_tab, 2 * E * M, a, A_FP4, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_gateup_devtab(const uint8_t* xq, const uint8_t* xsc, const int64_t* wp_tab,
+                                       const int64_t* wsc_tab, float* gu, int E, int M, int N, int K,
+                                       int Kp, void* stream) {
+    int rc = check_common(E, M, N, K, Kp, "moe_gateup_tab");
+    if (rc) return rc;
+    MXH_REQUIRE(xq && xsc && wp_tab && wsc_tab && gu, "moe_gateup_tab: null pointer");
+    GemvArgs a{};
+    a.E = E;
+    a.map = MAP_GATEUP;
+    a.N = N;
+    a.K = K;
+    a.Kp = Kp;
+    a.aq = xq;
+    a.as = xsc;
+    a.out = gu;
+    a.ld_out = 2 * (int64_t)N;
+    return run_dev_table(wp_tab, wsc_tab, 2 * E * M, a, A_FP4, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_down(const float* gu, const uint8_t* const* wp_tab, const uint8_t* const* wsc_tab,
+                              float* yd, int E, int M, int N, int K, int Kp, void* stream) {
+    int rc = check_common(E, M, N, K, Kp, "moe_down");
+    if (rc) return rc;
+    MXH_REQUIRE(gu && wp_tab && wsc_tab && yd, "moe_down: null pointer");
+    MXH_REQUIRE(Kp <= 4096, "moe_down: Kp=%d exceeds the 4096 supported by the LDS tile", Kp);
+    GemvArgs a{};
+    a.E = E;
+    a.map = MAP_PLAIN;
+    a.N = N;
+    a.K = K;
+    a.Kp = Kp;
+    a.gu = gu;
+    a.out = yd;
+    a.ld_out = N;
+    return run_host_table(wp_tab, wsc_tab, E * M, a, A_SILU, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_down_devtab(const float* gu, const int64_t* wp_tab, const int64_t* wsc_tab,
+                                     float* yd, int E, int M, int N, int K, int Kp, void* stream) {
+    int rc = check_common(E, M, N, K, Kp, "moe_down_tab");
+    if (rc) return rc;
+    MXH_REQUIRE(gu && wp_tab && wsc_tab && yd, "moe_down_tab: null pointer");
+    MXH_REQUIRE(Kp <= 4096, "moe_down_tab: Kp=%d exceeds the 4096 supported by the LDS tile", Kp);
+    GemvArgs a{};
+    a.E = E;
+    a.map = MAP_PLAIN;
+    a.N = N;
+    a.K = K;
+    a.Kp = Kp;
+    a.gu = gu;
+    a.out = yd;
+    a.ld_out = N;
+    return run_dev_table(wp_tab, wsc_tab, E * M, a, A_SILU, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E, float* out, int M,
+                                 int N, void* stream) {
+    MXH_REQUIRE(yd && w && out, "moe_combine: null pointer");
+    MXH_REQUIRE(M > 0 && E > 0 && N > 0, "moe_combine: sizes must be positive (M=%d E=%d N=%d)", M, E, N);
+    MXH_REQUIRE(ystride >= N, "moe_combine: ystride %d < N %d", ystride, N);
+    dim3 grid((unsigned)((N + 255) / 256), (unsigned)M);
+    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, mxh::as_stream(stream), yd, ystride, w, E, out, M, N);
+    return mxh::launch_status("moe_combine");
+}

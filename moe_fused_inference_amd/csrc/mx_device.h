@@ -1,0 +1,134 @@
+// mx_device.h -- gfx950 device primitives for the MXFP4 MoE path.
+//
+// * Bit-exact MXFP4 quantizer (contract: quant/fp4_format.py:21-148).
+//   E8M0: smallest 2^e with amax <= 6*2^e, clamp [-127,127], 0 -> 127, decided
+//   from the fp32 exponent/mantissa fields.  This equals the reference's
+//   frexp(amax/6) for every normal amax and also covers amax/6 underflow,
+//   where src/ext/mxfp4_common.cuh:42-50 would return 127.
+//   E2M1: nearest magnitude, ties toward the larger one, sign = (x < 0).
+//   The hardware converts (v_cvt_scalef32_pk_fp4_*) round ties to even and are
+//   therefore NOT used for the bit-exact path.
+// * CDNA4 block-scaled MFMA wrappers (v_mfma_scale_f32_{16x16x128,32x32x64}_f8f6f4).
+//   Operand layouts, measured on MI355X with a random-input probe:
+//     16x16x128, FP4 A and B: lane l holds row (A) / column (B) l%16 and the
+//       32 K-values 32*(l/16) .. +31 of the 128-K chunk as 16 bytes, nibble t
+//       of the chunk at byte t/2 (low nibble first); the lane's own E8M0 scale
+//       (byte 0 of the scale VGPR with op_sel 0) covers exactly those 32 values.
+//     16x16x128, FP8 (E4M3) A: lane l holds row l%16, bytes 0..15 = K
+//       16g..16g+15 and bytes 16..31 = K 64+16g..64+16g+15 (g = l/16); the
+//       scale of row r, 32-block b is read from lane r+16b.
+//     16x16 accumulator: lane l, element i = D[4*(l/16)+i][l%16].
+//     32x32x64, FP4: lane l holds row/column l%32, K 32*(l/32)..+31;
+//       accumulator element i of lane l = D[8*(i/4)+4*(l/32)+i%4][l%32].
+//   Because A and B of the same lane pair always cover the same K set, any
+//   permutation of whole 32-element blocks applied to both operands leaves the
+//   product unchanged; the kernels use that freedom to give each lane
+//   contiguous memory.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mx {
+
+typedef int v8i __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+typedef short v2s __attribute__((ext_vector_type(2)));
+
+constexpr int kBlock = 32;
+
+// ---------------------------------------------------------------- quantizer
+// E8M0 code of the smallest 2^e with amax <= 6*2^e (quant/fp4_format.py:73-88).
+__device__ __forceinline__ uint32_t e8m0_code(float amax) {
+    if (!(amax > 0.0f)) return 127u;
+    uint32_t bits = __float_as_uint(amax);
+    int ex = (int)(bits >> 23);
+    uint32_t frac = bits & 0x7FFFFFu;
+    int x;
+    if (ex == 0) {  // denormal amax: renormalise
+        int p = 31 - __clz((int)frac);
+        x = p - 149;
+        frac = (frac << (23 - p)) & 0x7FFFFFu;
+    } else {
+        x = ex - 127;
+    }
+    // amax = (1+f)*2^x <= 1.5*2^(e+2)  <=>  e = x-2 if (1+f) <= 1.5 else x-1
+    int e = (frac <= 0x400000u) ? x - 2 : x - 1;
+    e = e < -127 ? -127 : (e > 127 ? 127 : e);
+    return (uint32_t)(e + 127);
+}
+
+// 2^(127-code) as fp32: the reciprocal of the block scale.  Exact; for finite
+// amax the code never exceeds 253 so the result is a normal number.
+__device__ __forceinline__ float e8m0_inv_scale(uint32_t code) {
+    return code < 254u ? __uint_as_float((254u - code) << 23) : __uint_as_float(0x00400000u >> (code - 254u));
+}
+
+// E2M1 code of x = v / scale: nearest magnitude, ties up, clamp at 6,
+// sign bit from (x < 0) (quant/fp4_format.py:24-46).
+__device__ __forceinline__ uint32_t e2m1_code(float x) {
+    float a = __builtin_fabsf(x);
+    uint32_t m = (uint32_t)(a >= 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a >= 1.25f) +
+                 (uint32_t)(a >= 1.75f) + (uint32_t)(a >= 2.5f) + (uint32_t)(a >= 3.5f) +
+                 (uint32_t)(a >= 5.0f);
+    return m | (x < 0.0f ? 8u : 0u);
+}
+
+// Quantize 8 consecutive values of a 32-block whose scale code is known:
+// returns the 8 nibbles packed LSB-first into 32 bits.
+__device__ __forceinline__ uint32_t e2m1_pack8(const float v[8], float inv) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) r |= e2m1_code(v[i] * inv) << (4 * i);
+    return r;
+}
+
+// ---------------------------------------------------------------- FP4 decode
+// E2M1 nibble -> fp32 (used by reference-style epilogues and tests only).
+__device__ __forceinline__ float e2m1_value(uint32_t c) {
+    const float mag[8] = {0.f, 0.5f, 1.f, 1.5f, 2.f, 3.f, 4.f, 6.f};
+    float v = mag[c & 7u];
+    return (c & 8u) ? -v : v;
+}
+
+// ---------------------------------------------------------------- MFMA
+__device__ __forceinline__ v4f mfma16_fp4(uint4 a, uint4 b, v4f c, uint32_t sa, uint32_t sb) {
+    v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    v8i bv = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, c, 4, 4, 0, (int)sa, 0, (int)sb);
+}
+
+// A = E4M3 (32 bytes per lane), B = FP4.
+__device__ __forceinline__ v4f mfma16_fp8a_fp4b(v8i a, uint4 b, v4f c, uint32_t sa, uint32_t sb) {
+    v8i bv = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, bv, c, 0, 4, 0, (int)sa, 0, (int)sb);
+}
+
+__device__ __forceinline__ v16f mfma32_fp4(uint4 a, uint4 b, v16f c, uint32_t sa, uint32_t sb) {
+    v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    v8i bv = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 4, 4, 0, (int)sa, 0, (int)sb);
+}
+
+// ---------------------------------------------------------------- misc
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+// fp32 -> nearest fp16 (RNE, overflow to inf) -> fp32: the rounding torch's
+// .to(torch.half) applies.
+__device__ __forceinline__ float round_to_f16(float f) { return (float)(_Float16)f; }
+
+// fp32 -> bf16 bits, round to nearest even (finite inputs).
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
+    uint32_t u = __float_as_uint(f);
+    u += 0x7FFFu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float silu_mul(float g, float u) {
+    // h = g / (1 + exp(-g)) * u, fp32 (src/ext/mxfp4_decode.cu:258)
+    return (g / (1.0f + expf(-g))) * u;
+}
+
+}  // namespace mx

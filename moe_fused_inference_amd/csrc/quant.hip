@@ -1,0 +1,140 @@
+// quant.hip -- bit-exact activation -> MXFP4 quantizer for gfx950.
+//
+// Contract: quant/fp4_format.py (E2M1 ties-up, smallest power-of-two E8M0
+// scale, LSB-first nibbles), applied per 32-block of each row exactly as
+// quant/quantize_mxfp4.py:124-147 does for weights and as the reference's
+// prequant kernel does for activations (src/ext/mxfp4_decode.cu:24-50).
+//
+// Layout of the work: four consecutive lanes own one 32-block, eight
+// consecutive elements each.  A wave therefore reads 64 x 16 contiguous bytes
+// of bf16 input (fully coalesced), reduces the block amax with two xor
+// shuffles inside each lane quad, and each lane writes the 4 bytes holding
+// its 8 nibbles -- again contiguous across the wave.  The lane with quad index
+// 0 writes the block's scale byte.  HBM-bound: 2 B read + 0.53 B written per
+// element for bf16 input.
+#include "mx_device.h"
+#include "mx_host.h"
+
+namespace {
+
+template <int SRC>
+__device__ __forceinline__ float load_elem(const void* x, int64_t idx) {
+    if (SRC == MXFP4_DT_BF16) return mx::bf16_to_f32(static_cast<const uint16_t*>(x)[idx]);
+    if (SRC == MXFP4_DT_F16) return mx::f16_to_f32(static_cast<const uint16_t*>(x)[idx]);
+    return static_cast<const float*>(x)[idx];
+}
+
+// Loads 8 consecutive elements starting at row offset k0 (16-byte aligned
+// vector path when `vec` holds, element path with zero fill otherwise).
+template <int SRC>
+__device__ __forceinline__ void load8(const void* x, int64_t base, int k0, int K, bool vec,
+                                      float v[8]) {
+    if (vec && k0 + 8 <= K) {
+        if (SRC == MXFP4_DT_F32) {
+            const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(x) + base + k0);
+            float4 a = p[0], b = p[1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        } else {
+            const uint4 q = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + base + k0);
+            const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint16_t lo = (uint16_t)(w[i] & 0xFFFFu), hi = (uint16_t)(w[i] >> 16);
+                if (SRC == MXFP4_DT_BF16) {
+                    v[2 * i] = mx::bf16_to_f32(lo);
+                    v[2 * i + 1] = mx::bf16_to_f32(hi);
+                } else {
+                    v[2 * i] = mx::f16_to_f32(lo);
+                    v[2 * i + 1] = mx::f16_to_f32(hi);
+                }
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = (k0 + i < K) ? load_elem<SRC>(x, base + k0 + i) : 0.0f;
+    }
+}
+
+template <int SRC, bool ROUND_F16>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int64_t ldx,
+                                                            int M, int K, int Kp, int vec,
+                                                            uint8_t* __restrict__ q,
+                                                            uint8_t* __restrict__ s) {
+    const int upr = Kp >> 3;  // 8-element units per row
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = gid / upr;
+    const int u = (int)(gid - row * upr);
+    const bool valid = row < M;
+    const int k0 = u * 8;
+    float v[8];
+    if (valid) {
+        load8<SRC>(x, row * ldx, k0, K, vec != 0, v);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    if (ROUND_F16) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = mx::round_to_f16(v[i]);
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
+    am = fmaxf(am, __shfl_xor(am, 1));
+    am = fmaxf(am, __shfl_xor(am, 2));
+    const uint32_t code = mx::e8m0_code(am);
+    const uint32_t packed = mx::e2m1_pack8(v, mx::e8m0_inv_scale(code));
+    if (valid) {
+        *reinterpret_cast<uint32_t*>(q + row * (int64_t)(Kp >> 1) + (u << 2)) = packed;
+        if ((u & 3) == 0) s[row * (int64_t)(Kp >> 5) + (u >> 2)] = (uint8_t)code;
+    }
+}
+
+template <int SRC, bool R16>
+void launch_quant(const void* x, int64_t ldx, int M, int K, int Kp, int vec, uint8_t* q, uint8_t* s,
+                  hipStream_t st) {
+    const int64_t units = (int64_t)M * (Kp >> 3);
+    const int64_t blocks = (units + 255) / 256;
+    hipLaunchKernelGGL((quantize_rows_kernel<SRC, R16>), dim3((unsigned)blocks), dim3(256), 0, st,
+                       x, ldx, M, K, Kp, vec, q, s);
+}
+
+}  // namespace
+
+namespace mxh {
+// Shared by mxfp4_linear_forward.
+int quantize_rows_impl(const void* x, int src_dtype, int round_to_f16, int64_t ldx, int M, int K,
+                       int Kp, uint8_t* q, uint8_t* s, hipStream_t st) {
+    MXH_REQUIRE(x && q && s, "quantize: null pointer");
+    MXH_REQUIRE(M >= 0 && K >= 0, "quantize: negative size (M=%d K=%d)", M, K);
+    MXH_REQUIRE(Kp % 32 == 0 && Kp >= K, "quantize: Kp=%d must be a multiple of 32 and >= K=%d", Kp, K);
+    MXH_REQUIRE(ldx >= K, "quantize: row stride %lld < K=%d", (long long)ldx, K);
+    MXH_REQUIRE(src_dtype >= MXFP4_DT_BF16 && src_dtype <= MXFP4_DT_F32, "quantize: bad dtype %d", src_dtype);
+    MXH_REQUIRE(((uintptr_t)q & 3) == 0, "quantize: packed output must be 4-byte aligned");
+    if (M == 0 || Kp == 0) return MXFP4_OK;
+    const int esz = src_dtype == MXFP4_DT_F32 ? 4 : 2;
+    const int vec = (((uintptr_t)x & 15) == 0) && ((ldx * esz) % 16 == 0);
+    const bool r16 = round_to_f16 != 0;
+    if (src_dtype == MXFP4_DT_BF16) {
+        if (r16) launch_quant<MXFP4_DT_BF16, true>(x, ldx, M, K, Kp, vec, q, s, st);
+        else launch_quant<MXFP4_DT_BF16, false>(x, ldx, M, K, Kp, vec, q, s, st);
+    } else if (src_dtype == MXFP4_DT_F16) {
+        launch_quant<MXFP4_DT_F16, false>(x, ldx, M, K, Kp, vec, q, s, st);
+    } else {
+        if (r16) launch_quant<MXFP4_DT_F32, true>(x, ldx, M, K, Kp, vec, q, s, st);
+        else launch_quant<MXFP4_DT_F32, false>(x, ldx, M, K, Kp, vec, q, s, st);
+    }
+    return launch_status("quantize_rows");
+}
+}  // namespace mxh
+
+extern "C" int mxfp4_quantize_rows(const void* x, int src_dtype, int round_to_f16, int64_t ldx, int M,
+                                   int K, int Kp, uint8_t* q, uint8_t* s, void* stream) {
+    return mxh::quantize_rows_impl(x, src_dtype, round_to_f16, ldx, M, K, Kp, q, s, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_prequant(const void* x, int64_t ldx, int M, int K, int Kp, uint8_t* xq,
+                              uint8_t* xsc, void* stream) {
+    return mxh::quantize_rows_impl(x, MXFP4_DT_BF16, 0, ldx, M, K, Kp, xq, xsc, mxh::as_stream(stream));
+}

@@ -1,0 +1,188 @@
+"""Drop-in counterpart of the reference's extension loader (runtime/fp4_ext.py).
+
+``get_ext()`` returns the ``mxfp4_linear_ext`` surface (``forward``) and
+``get_decode_ext()`` the ``mxfp4_decode_ext`` surface (``prequant``,
+``lin_pq``, ``moe_gateup``, ``moe_down``, ``moe_combine``, ``moe_gateup_tab``,
+``moe_down_tab``; ``attn_decode`` / ``kv_write`` are not built yet and raise).
+Names, argument order, argument meaning, output shapes/dtypes and the
+argument checks (RuntimeError with the reference's messages) follow the
+pybind bindings src/ext/mxfp4_binding.cpp:21-50 and
+src/ext/mxfp4_decode_binding.cpp:44-243.  Underneath, every op is one or
+two calls into the C ABI of include/mxfp4_hip.h (libmxfp4_hip.so, gfx950),
+launched on torch's current HIP stream; outputs are allocated with torch's
+caching allocator on the input's device, as the reference does.
+"""
+import torch
+
+from . import _lib
+
+_DT = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+
+
+def _stream(t):
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond, msg):
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _ptr_table(ts):
+    """Host pointer table (src/ext/mxfp4_decode_binding.cpp:44-60 checks)."""
+    _require(len(ts) > 0, "empty pointer table")
+    ptrs = []
+    for t in ts:
+        _require(t.is_cuda and t.dtype == torch.uint8, "ptr table entries must be cuda uint8")
+        ptrs.append(t.data_ptr())
+    return _lib.ptr_array(ptrs)
+
+
+class LinearExt:
+    """``mxfp4_linear_ext`` (src/ext/mxfp4_binding.cpp:47-50)."""
+
+    __name__ = "mxfp4_linear_ext"
+
+    def __init__(self):
+        self._lib = _lib.load()
+
+    def forward(self, x, wp, wsc):
+        """x (M,K) half|bf16, wp (N,Kp/2) u8, wsc (N,Kp/32) u8 -> f32 (M,N).
+        Activations are rounded to fp16 then MXFP4-quantized per 32-block
+        (src/ext/mxfp4_binding.cpp:21-45)."""
+        _require(x.is_cuda, "x must be cuda")
+        _require(wp.is_cuda and wsc.is_cuda, "weights must be cuda")
+        _require(wp.dtype == torch.uint8 and wsc.dtype == torch.uint8, "weight tensors must be uint8")
+        xh = x if x.dtype in (torch.float16, torch.bfloat16) else x.to(torch.float16)
+        xh = xh.contiguous()
+        wp = wp.contiguous()
+        wsc = wsc.contiguous()
+        M, K = x.shape[0], x.shape[1]
+        N, Kp = wp.shape[0], wp.shape[1] * 2
+        y = torch.empty((M, N), dtype=torch.float32, device=x.device)
+        if M == 0 or N == 0:
+            return y
+        wsb = self._lib.mxfp4_linear_workspace_size(M, Kp)
+        ws = torch.empty(wsb + 256, dtype=torch.uint8, device=x.device)
+        base = ws.data_ptr()
+        aligned = (base + 255) & ~255
+        _lib.check(self._lib.mxfp4_linear_forward(
+            xh.data_ptr(), _DT[xh.dtype], wp.data_ptr(), wsc.data_ptr(), y.data_ptr(),
+            M, N, K, Kp, aligned, wsb, _stream(x)), "forward")
+        return y
+
+
+class DecodeExt:
+    """``mxfp4_decode_ext`` (src/ext/mxfp4_decode_binding.cpp:232-243)."""
+
+    __name__ = "mxfp4_decode_ext"
+
+    def __init__(self):
+        self._lib = _lib.load()
+
+    def prequant(self, x):
+        """x (M,K) bf16 cuda -> [xq (M,Kp/2) u8, xsc (M,Kp/32) u8], Kp = ceil32(K)."""
+        _require(x.is_cuda, "x must be cuda")
+        _require(x.dtype == torch.bfloat16, "x must be bfloat16")
+        x = x.contiguous()
+        M, K = int(x.shape[0]), int(x.shape[1])
+        Kp = (K + 31) // 32 * 32
+        xq = torch.empty((M, Kp // 2), dtype=torch.uint8, device=x.device)
+        xsc = torch.empty((M, Kp // 32), dtype=torch.uint8, device=x.device)
+        if M and Kp:
+            _lib.check(self._lib.mxfp4_prequant(x.data_ptr(), K, M, K, Kp, xq.data_ptr(),
+                                                xsc.data_ptr(), _stream(x)), "prequant")
+        return [xq, xsc]
+
+    def lin_pq(self, xq, xsc, wp, wsc, M, N, K):
+        """Pre-quantized static linear -> f32 (M,N); Kp = 2*wp.size(1)."""
+        xq, xsc, wp, wsc = xq.contiguous(), xsc.contiguous(), wp.contiguous(), wsc.contiguous()
+        M, N, K = int(M), int(N), int(K)
+        Kp = int(wp.shape[1]) * 2
+        y = torch.empty((M, N), dtype=torch.float32, device=xq.device)
+        _lib.check(self._lib.mxfp4_lin_pq(xq.data_ptr(), xsc.data_ptr(), wp.data_ptr(), wsc.data_ptr(),
+                                          y.data_ptr(), M, N, K, Kp, _stream(xq)), "lin_pq")
+        return y
+
+    def moe_gateup(self, xq, xsc, wps, wscs, E, M, N, K):
+        """Grouped gate+up over a token-major table of 2E*M weights -> f32 (M*E, 2N)."""
+        E, M, N, K = int(E), int(M), int(N), int(K)
+        _require(len(wps) == 2 * E * M, "wps must be 2E*M")
+        _require(len(wscs) == 2 * E * M, "wscs must be 2E*M")
+        Kp = int(wps[0].shape[1]) * 2
+        tw, ts = _ptr_table(wps), _ptr_table(wscs)
+        gu = torch.empty((M * E, 2 * N), dtype=torch.float32, device=xq.device)
+        _lib.check(self._lib.mxfp4_moe_gateup(xq.data_ptr(), xsc.data_ptr(), tw, ts, gu.data_ptr(),
+                                              E, M, N, K, Kp, _stream(xq)), "moe_gateup")
+        return gu
+
+    def moe_down(self, gu, wps, wscs, E, M, N, K):
+        """Fused silu(gate)*up -> MXFP4 -> down over E*M weights -> f32 (M*E, N)."""
+        E, M, N, K = int(E), int(M), int(N), int(K)
+        _require(len(wps) == E * M, "wps must be E*M")
+        Kp = int(wps[0].shape[1]) * 2
+        _require(gu.shape[0] == M * E and gu.shape[1] == 2 * K, "gu (M*E,2K)")
+        tw, ts = _ptr_table(wps), _ptr_table(wscs)
+        gu = gu.contiguous()
+        yd = torch.empty((M * E, N), dtype=gu.dtype, device=gu.device)
+        _lib.check(self._lib.mxfp4_moe_down(gu.data_ptr(), tw, ts, yd.data_ptr(), E, M, N, K, Kp,
+                                            _stream(gu)), "moe_down")
+        return yd
+
+    def moe_combine(self, yd, w, M):
+        """out[m,c] = sum_{e<min(E,8)} w[m,e]*yd[m*E+e,c] -> f32 (M,N); E = w.numel()/M."""
+        yd, w = yd.contiguous(), w.contiguous()
+        M = int(M)
+        E = int(w.numel()) // M
+        N = int(yd.shape[1])
+        _require(M * E == w.numel(), "w (M,E)")
+        _require(yd.shape[0] == M * E, "yd (M*E,N)")
+        out = torch.empty((M, N), dtype=yd.dtype, device=yd.device)
+        _lib.check(self._lib.mxfp4_moe_combine(yd.data_ptr(), N, w.data_ptr(), E, out.data_ptr(), M, N,
+                                               _stream(yd)), "moe_combine")
+        return out
+
+    def moe_gateup_tab(self, xq, xsc, wps_tab, wscs_tab, E, M, N, K):
+        """moe_gateup with device int64 pointer tables; Kp = 2*xq.size(1)."""
+        E, M, N, K = int(E), int(M), int(N), int(K)
+        Kp = int(xq.shape[1]) * 2
+        gu = torch.empty((M * E, 2 * N), dtype=torch.float32, device=xq.device)
+        _lib.check(self._lib.mxfp4_moe_gateup_devtab(xq.data_ptr(), xsc.data_ptr(), wps_tab.data_ptr(),
+                                                     wscs_tab.data_ptr(), gu.data_ptr(), E, M, N, K, Kp,
+                                                     _stream(xq)), "moe_gateup_tab")
+        return gu
+
+    def moe_down_tab(self, gu, wps_tab, wscs_tab, E, M, N, K):
+        """moe_down with device int64 pointer tables; Kp = ceil32(gu.size(1)/2)."""
+        E, M, N, K = int(E), int(M), int(N), int(K)
+        Kp = ((int(gu.shape[1]) // 2) + 31) // 32 * 32
+        yd = torch.empty((M * E, N), dtype=gu.dtype, device=gu.device)
+        _lib.check(self._lib.mxfp4_moe_down_devtab(gu.data_ptr(), wps_tab.data_ptr(), wscs_tab.data_ptr(),
+                                                   yd.data_ptr(), E, M, N, K, Kp, _stream(gu)), "moe_down_tab")
+        return yd
+
+    def attn_decode(self, q, kvk, kvv, dpos, sc, M):
+        raise NotImplementedError("attn_decode (FP8 KV decode attention) is not part of this build yet")
+
+    def kv_write(self, k, v, kvk, kvv, dpos, M):
+        raise NotImplementedError("kv_write (FP8 KV write) is not part of this build yet")
+
+
+_ext = None
+_dext = None
+
+
+def get_ext():
+    """Counterpart of runtime/fp4_ext.py:21-39 (module ``mxfp4_linear_ext``)."""
+    global _ext
+    if _ext is None:
+        _ext = LinearExt()
+    return _ext
+
+
+def get_decode_ext():
+    """Counterpart of runtime/fp4_ext.py:46-62 (module ``mxfp4_decode_ext``)."""
+    global _dext
+    if _dext is None:
+        _dext = DecodeExt()
+    return _dext

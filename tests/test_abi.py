@@ -1,0 +1,94 @@
+"""The C-ABI library loads and exports exactly what include/mxfp4_hip.h
+declares; host-side argument checks reject bad calls before any launch.
+No GPU is needed: every call here fails validation on the host."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from moe_fused_inference_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mxfp4_hip.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(mxfp4_[a-z0-9_]+)\s*\(", txt)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(_lib.LIB_PATH):
+        from moe_fused_inference_amd import build
+        build.build()
+    return _lib.load()
+
+
+def test_header_declares_the_bound_signatures():
+    decl = _declared()
+    assert decl, "no declarations parsed"
+    assert set(decl) == set(_lib.SIGNATURES) | set(_lib.OPTIONAL_SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.mxfp4_abi_version() == 1
+
+
+def test_workspace_size(lib):
+    assert lib.mxfp4_linear_workspace_size(4, 2048) == 4096 + 256
+    assert lib.mxfp4_linear_workspace_size(0, 2048) == 0
+
+
+@pytest.mark.parametrize("call,msg", [
+    (lambda L: L.mxfp4_prequant(None, 64, 1, 64, 64, None, None, None), "null pointer"),
+    (lambda L: L.mxfp4_prequant(16, 64, 1, 64, 48, 16, 16, None), "multiple of 32"),
+    (lambda L: L.mxfp4_prequant(16, 32, 1, 64, 64, 16, 16, None), "row stride"),
+    (lambda L: L.mxfp4_lin_pq(16, 16, 16, 16, 16, 0, 8, 64, 64, None), "positive"),
+    (lambda L: L.mxfp4_lin_pq(16, 16, 16, 16, 16, 1, 8, 100, 64, None), "exceeds"),
+    (lambda L: L.mxfp4_moe_down(16, _lib.ptr_array([16]), _lib.ptr_array([16]), 16, 1, 1, 8, 768, 8192,
+                                None), "LDS"),
+    (lambda L: L.mxfp4_moe_combine(16, 4, 16, 2, 16, 1, 8, None), "ystride"),
+    (lambda L: L.mxfp4_linear_forward(16, 0, 16, 16, 16, 2, 8, 64, 64, 256, 1, None), "workspace"),
+    (lambda L: L.mxfp4_moe_gateup(16, 16, _lib.ptr_array([16, 0]), _lib.ptr_array([16, 16]), 16,
+                                  1, 1, 8, 64, 64, None), "null"),
+])
+def test_argument_checks_fail_on_host(lib, call, msg):
+    rc = call(lib)
+    assert rc == -1
+    assert msg in lib.mxfp4_last_error().decode()
+
+
+def test_python_surface_checks_mirror_reference(lib):
+    """RuntimeError messages of src/ext/*_binding.cpp, raised before launch."""
+    from moe_fused_inference_amd import get_decode_ext, get_ext
+    d, l = get_decode_ext(), get_ext()
+    x = torch.zeros(1, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="x must be cuda"):
+        d.prequant(x)
+    with pytest.raises(RuntimeError, match="x must be cuda"):
+        l.forward(x, torch.zeros(8, 32, dtype=torch.uint8), torch.zeros(8, 2, dtype=torch.uint8))
+    with pytest.raises(RuntimeError, match="wps must be 2E\\*M"):
+        d.moe_gateup(x, x, [x] * 3, [x] * 4, 2, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="wscs must be 2E\\*M"):
+        d.moe_gateup(x, x, [x] * 4, [x] * 3, 2, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="wps must be E\\*M"):
+        d.moe_down(torch.zeros(2, 128), [x] * 3, [x] * 3, 2, 1, 8, 64)
+    w8 = torch.zeros(8, 32, dtype=torch.uint8)
+    with pytest.raises(RuntimeError, match="gu \\(M\\*E,2K\\)"):
+        d.moe_down(torch.zeros(2, 100), [w8] * 2, [w8] * 2, 2, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="ptr table entries must be cuda uint8"):
+        d.moe_down(torch.zeros(2, 128), [w8] * 2, [w8] * 2, 2, 1, 8, 64)
+    with pytest.raises(RuntimeError, match="w \\(M,E\\)"):
+        d.moe_combine(torch.zeros(4, 8), torch.zeros(5), 2)
+    with pytest.raises(RuntimeError, match="yd \\(M\\*E,N\\)"):
+        d.moe_combine(torch.zeros(5, 8), torch.zeros(4), 2)
+    with pytest.raises(TypeError):
+        d.moe_down(torch.zeros(2, 128), [w8] * 2, [w8] * 2, 2, 8, 64)  # stale 6-arg call
+    with pytest.raises(NotImplementedError):
+        d.attn_decode(None, None, None, None, None, 1)

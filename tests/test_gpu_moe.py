@@ -1,0 +1,193 @@
+"""GPU parity of the grouped decode MoE operators against the oracle.
+
+moe_gateup  src/ext/mxfp4_decode.cu:177-212   token-major table, FP4 activations
+moe_down    src/ext/mxfp4_decode.cu:218-279   fp32 SiLU*up -> MXFP4 -> down
+moe_combine src/ext/mxfp4_decode.cu:285-299   weighted sum over <= 8 slots
+Tables are built exactly as runtime/model_runner_v2.py:197-206 (decode) and
+:279-286 (batch) build them.  Shapes: H=2048, Mi=768 (Qwen3-30B-A3B).
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import mxfp4 as fmt
+from oracle import ops
+from tests.gpu_helpers import DEV, assert_close, log, np_, rand_weight
+
+pytestmark = pytest.mark.gpu
+H, MI = 2048, 768
+
+
+class Experts:
+    """Seeded bf16 N(0, 0.02) experts quantized by the bit-exact HIP quantizer;
+    dequantized copies (float64) for the oracle are made lazily."""
+
+    def __init__(self, dext, ids, seed0=100):
+        self.w = {}
+        self._deq = {}
+        for e in ids:
+            self.w[e] = {
+                "gate": rand_weight(dext, MI, H, seed0 + 3 * e),
+                "up": rand_weight(dext, MI, H, seed0 + 3 * e + 1),
+                "down": rand_weight(dext, H, MI, seed0 + 3 * e + 2),
+            }
+
+    def deq(self, e, p):
+        if (e, p) not in self._deq:
+            q, s = self.w[e][p]
+            self._deq[(e, p)] = fmt.dequant_rows(np_(q), np_(s)).astype(np.float64)
+        return self._deq[(e, p)]
+
+
+def _tables(ex, topi, M, E):
+    ids = topi.reshape(-1).tolist()
+    gu_w, gu_s, dn_w, dn_s = [], [], [], []
+    for m in range(M):
+        row = ids[m * E:(m + 1) * E]
+        gu_w += [ex.w[e]["gate"][0] for e in row] + [ex.w[e]["up"][0] for e in row]
+        gu_s += [ex.w[e]["gate"][1] for e in row] + [ex.w[e]["up"][1] for e in row]
+        dn_w += [ex.w[e]["down"][0] for e in row]
+        dn_s += [ex.w[e]["down"][1] for e in row]
+    return gu_w, gu_s, dn_w, dn_s
+
+
+def _check_gateup(ex, gu, xq, xs, topi, M, E):
+    A = fmt.dequant_rows(np_(xq), np_(xs)).astype(np.float64)
+    ref = np.zeros((M * E, 2 * MI))
+    for m in range(M):
+        for s in range(E):
+            e = int(topi[m, s])
+            ref[m * E + s, :MI] = ex.deq(e, "gate") @ A[m]
+            ref[m * E + s, MI:] = ex.deq(e, "up") @ A[m]
+    assert_close(np_(gu), ref, what=f"moe_gateup M={M}")
+
+
+def _check_down(ex, yd, gu, topi, M, E):
+    h = ops.moe_down_h_ref(np_(gu), E, M, MI)
+    hq, hs = fmt.quantize_rows(h)
+    hd = fmt.dequant_rows(hq, hs).astype(np.float64)
+    ref = np.zeros((M * E, H))
+    for m in range(M):
+        for s in range(E):
+            ref[m * E + s] = ex.deq(int(topi[m, s]), "down") @ hd[m * E + s]
+    # h from the device's expf may differ by ulps and flip a nibble at a
+    # threshold: slightly looser than the per-op bound, far inside the north star
+    assert_close(np_(yd), ref, cos_min=0.9999, rel_max=2e-3, what=f"moe_down M={M}")
+
+
+def test_decode_m1_full_chain(dext):
+    E, M = 8, 1
+    rng = np.random.default_rng(2)
+    topi = rng.permutation(128)[:E][None]
+    ex = Experts(dext, topi[0].tolist())
+    g = torch.Generator(device=DEV)
+    g.manual_seed(0)
+    x = torch.randn((1, H), generator=g, device=DEV).bfloat16()
+    xq, xs = dext.prequant(x)
+    gw, gs, dw, ds = _tables(ex, topi, M, E)
+    gu = dext.moe_gateup(xq, xs, gw, gs, E, M, MI, H)
+    yd = dext.moe_down(gu, dw, ds, E, M, H, MI)
+    w = torch.softmax(torch.randn(E, generator=g, device=DEV), 0)
+    out = dext.moe_combine(yd, w.view(1, E).float(), 1)
+    torch.cuda.synchronize()
+    assert gu.shape == (E, 2 * MI) and yd.shape == (E, H) and out.shape == (1, H)
+    _check_gateup(ex, gu, xq, xs, topi, M, E)
+    _check_down(ex, yd, gu, topi, M, E)
+    ref = ops.moe_combine_ref(np_(yd), np_(w).reshape(1, E), 1)
+    assert_close(np_(out), ref, cos_min=0.999999, rel_max=1e-5, what="moe_combine")
+    # information: the faithful chain (quantized activations) against the
+    # un-quantized bf16 oracle -- the reference reports ~0.992 for this
+    experts = {e: (ex.w[e]["gate"], ex.w[e]["up"], ex.w[e]["down"]) for e in topi[0]}
+    experts = {e: tuple((np_(q), np_(s)) for q, s in v) for e, v in experts.items()}
+    full = ops.decode_layer_ref(np_(x.float()), topi, np_(w).reshape(1, E), experts)
+    log(f"  faithful chain vs bf16-activation oracle: cos={ops.cos_sim(np_(out), full):.6f}")
+
+
+def _zipf_topi(rng, M, E, n_exp, s=1.1, beta=1.0):
+    perm = rng.permutation(n_exp)
+    p = 1.0 / np.arange(1, n_exp + 1) ** s
+    logp = np.log(p / p.sum())
+    out = []
+    for _ in range(M):
+        lg = rng.standard_normal(n_exp) + beta * logp[np.argsort(perm)]
+        topi, _ = ops.route_ref(lg[None].astype(np.float32), k=E)
+        out.append(topi[0])
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("beta", [0.5, 1.5])
+def test_spec_verify_m9_grouped(dext, beta):
+    """M = 1 + 8 draft tokens, Zipf-biased routing: experts shared between
+    tokens are grouped inside the kernel; results per (token, slot) entry."""
+    E, M = 8, 9
+    rng = np.random.default_rng(int(beta * 10))
+    topi = _zipf_topi(rng, M, E, 48, beta=beta)
+    distinct = sorted(set(topi.reshape(-1).tolist()))
+    log(f"  beta={beta}: {len(distinct)} distinct experts over {M * E} slots")
+    ex = Experts(dext, distinct)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(1)
+    x = torch.randn((M, H), generator=g, device=DEV).bfloat16()
+    xq, xs = dext.prequant(x)
+    gw, gs, dw, ds = _tables(ex, topi, M, E)
+    gu = dext.moe_gateup(xq, xs, gw, gs, E, M, MI, H)
+    yd = dext.moe_down(gu, dw, ds, E, M, H, MI)
+    tv = torch.softmax(torch.randn((M, E), generator=g, device=DEV), -1)
+    out = dext.moe_combine(yd, tv, M)
+    torch.cuda.synchronize()
+    _check_gateup(ex, gu, xq, xs, topi, M, E)
+    _check_down(ex, yd, gu, topi, M, E)
+    assert_close(np_(out), ops.moe_combine_ref(np_(yd), np_(tv), M), cos_min=0.999999, rel_max=1e-5,
+                 what="moe_combine M=9")
+
+    # device-table variants (moe_gateup_tab / moe_down_tab) run the same kernels
+    def dtab(ts):
+        return torch.tensor([t.data_ptr() for t in ts], dtype=torch.int64, device=DEV)
+    gu2 = dext.moe_gateup_tab(xq, xs, dtab(gw), dtab(gs), E, M, MI, H)
+    yd2 = dext.moe_down_tab(gu, dtab(dw), dtab(ds), E, M, H, MI)
+    torch.cuda.synchronize()
+    assert torch.equal(gu, gu2) and torch.equal(yd, yd2)
+
+
+def test_generic_table_with_repeats_and_ragged_k(dext):
+    """Small ragged shapes (K = 100 -> Kp = 128, N = 40) with a table that
+    repeats weights across tokens and within a token."""
+    E, M, N, K = 3, 4, 40, 100
+    rng = np.random.default_rng(7)
+    mats = [fmt.quantize_rows(rng.standard_normal((N, K)).astype(np.float32)) for _ in range(4)]
+    dev = [(torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV)) for q, s in mats]
+    pick = rng.integers(0, 4, size=2 * E * M)
+    pick[1] = pick[0]
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(DEV).bfloat16()
+    xq, xs = dext.prequant(x)
+    gu = dext.moe_gateup(xq, xs, [dev[i][0] for i in pick], [dev[i][1] for i in pick], E, M, N, K)
+    torch.cuda.synchronize()
+    ref = ops.moe_gateup_ref(np_(xq), np_(xs), [mats[i][0] for i in pick], [mats[i][1] for i in pick],
+                             E, M, N)
+    assert_close(np_(gu), ref, what="gateup ragged/repeats")
+    # down over E*M entries with repeats; K_down = N (gu holds 2N columns)
+    dm = [fmt.quantize_rows(rng.standard_normal((24, N)).astype(np.float32)) for _ in range(3)]
+    ddev = [(torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV)) for q, s in dm]
+    dp = rng.integers(0, 3, size=E * M)
+    yd = dext.moe_down(gu, [ddev[i][0] for i in dp], [ddev[i][1] for i in dp], E, M, 24, N)
+    torch.cuda.synchronize()
+    ref = ops.moe_down_ref(np_(gu), [dm[i][0] for i in dp], [dm[i][1] for i in dp], E, M, 24, N)
+    assert_close(np_(yd), ref, cos_min=0.9999, rel_max=2e-3, what="down ragged/repeats")
+
+
+def test_combine_caps_at_eight_slots(dext):
+    M, E, N = 3, 9, 2048
+    g = torch.Generator(device=DEV)
+    g.manual_seed(4)
+    yd = torch.randn((M * E, N), generator=g, device=DEV)
+    w = torch.rand((M, E), generator=g, device=DEV)
+    out = dext.moe_combine(yd, w, M)
+    torch.cuda.synchronize()
+    ref = ops.moe_combine_ref(np_(yd), np_(w), M)
+    assert_close(np_(out), ref, cos_min=0.999999, rel_max=1e-5, what="combine E=9")
+    # the 9th slot must not contribute
+    yd2 = yd.clone().view(M, E, N)
+    yd2[:, 8] += 1000.0
+    out2 = dext.moe_combine(yd2.view(M * E, N), w, M)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2)
