@@ -1,0 +1,403 @@
+#!/usr/bin/env python3
+"""Benchmark of the MXFP4 MoE hot path on one MI355X.
+
+Headline (BASELINE.json metric "MoE-layer us + HBM GB/s (MXFP4 decode,
+top-8); prefill MXFP4 GEMM TFLOPS"), workload = config 2:
+  48 MoE layers with independent seeded weights (128 experts each, H=2048,
+  Mi=768, MXFP4 from bf16 N(0, 0.02), all 15.4 GB resident in HBM), batch-1
+  decode, top-8 routing from fresh N(0,1) router logits for every layer of
+  every step (softmax -> top-8 -> renorm), so expert choice is ~uniform and
+  the 256 MB MALL cannot hold a step's 962 MB working set.
+  One step = one decode token through all 48 layers (x_{L+1} = bf16(x_L + moe_L)).
+  Steps are HIP-graph replays of S_ROUTES distinct pre-drawn steps.
+
+value = algorithmic HBM bytes of one layer (8 experts x 2,506,752 B) / mean
+layer time, in GB/s.  Also reported: us/layer, tok/s, the roofline object of
+the fused decode kernel, the reference's dequant+BF16 CPU path timed on this
+host (cpu_baseline), the drop-in 4-launch path, the prefill GEMM shapes of
+config 3 (TFLOPS) and the M=9 speculative-verify grouped path (config 4).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--skip-extra] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-layer µs + HBM GB/s (MXFP4 decode, top-8); prefill MXFP4 GEMM TFLOPS"
+H, MI, N_EXP, TOPK, LAYERS = 2048, 768, 128, 8, 48
+EXPERT_BYTES = 3 * MI * (H // 2 + H // 32)          # 2,506,752 B (gate + up + down, data + scales)
+LAYER_BYTES = TOPK * EXPERT_BYTES                  # 20,054,016 B
+LAYER_FLOPS = 2 * TOPK * (2 * MI * H + H * MI)     # 75.5 MFLOP
+HBM_PEAK_GBS = 8000.0
+MXFP4_PEAK_TFLOPS = 10100.0                        # dense fp4 MFMA, MI355X
+S_ROUTES = 4                                       # distinct pre-drawn decode steps in the graph
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--profile-decode-only", action="store_true",
+                    help="run only the fused decode graph (for rocprofv3 runs)")
+    return ap.parse_args()
+
+
+# ----------------------------------------------------------------------------- weights
+def build_layers(torch, lib, dev, n_layers):
+    """Seeded bf16 N(0, 0.02) expert weights, quantized on the GPU by the
+    bit-exact quantizer (the same rule as quant/quantize_mxfp4.py), stacked per
+    layer: gate/up (128, Mi, H/2)+(128, Mi, H/32), down (128, H, Mi/2)+(128, H, Mi/32)."""
+    from moe_fused_inference_amd.moe_layer import StackedExperts
+    stream = torch.cuda.current_stream().cuda_stream
+    layers = []
+    chunk = 16
+    for L in range(n_layers):
+        g = torch.Generator(device=dev)
+        g.manual_seed(1000 + L)
+        t = {}
+        for nm, (n, k) in (("gate", (MI, H)), ("up", (MI, H)), ("down", (H, MI))):
+            wp = torch.empty((N_EXP, n, k // 2), dtype=torch.uint8, device=dev)
+            ws = torch.empty((N_EXP, n, k // 32), dtype=torch.uint8, device=dev)
+            for e0 in range(0, N_EXP, chunk):
+                w = (torch.randn((chunk * n, k), generator=g, device=dev) * 0.02).bfloat16()
+                rc = lib.mxfp4_prequant(w.data_ptr(), k, chunk * n, k, k, wp[e0].data_ptr(),
+                                        ws[e0].data_ptr(), stream)
+                assert rc == 0
+            t[nm + "_wp"], t[nm + "_ws"] = wp, ws
+        layers.append(StackedExperts(**t))
+        if (L + 1) % 12 == 0:
+            torch.cuda.synchronize()
+            log(f"  built {L + 1}/{n_layers} layers")
+    torch.cuda.synchronize()
+    return layers
+
+
+def draw_routes(torch, n_steps, n_layers, seed):
+    """Fresh N(0,1) router logits per (step, layer) -> softmax -> top-8 -> renorm
+    (runtime/model_runner_v2.py:189-192)."""
+    g = torch.Generator()
+    g.manual_seed(seed)
+    logits = torch.randn((n_steps, n_layers, N_EXP), generator=g)
+    p = torch.softmax(logits.float(), -1)
+    tv, ti = torch.topk(p, TOPK, dim=-1)
+    tv = tv / tv.sum(-1, keepdim=True)
+    return ti.int(), tv.float()
+
+
+# ----------------------------------------------------------------------------- decode
+def make_decode_graph(torch, layers, routes, x0, ws, outs, bufs):
+    from moe_fused_inference_amd.moe_layer import DecodeLayerCall
+    ti, tv = routes
+    calls = []
+    for s in range(ti.shape[0]):
+        src = x0
+        for L, lay in enumerate(layers):
+            calls.append(DecodeLayerCall(src, ti[s, L].tolist(), tv[s, L].tolist(), lay,
+                                         outs[L], bufs[L % 2], ws))
+            src = bufs[L % 2]
+    for c in calls:  # eager warm-up / validation of every call
+        c()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    return graph, calls
+
+
+def time_graph(torch, graph, steps, warmup):
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per replay
+
+
+def dropin_graph(torch, dext, layers, routes, x0):
+    """The drop-in operator path of runtime/model_runner_v2.py:185-208 (prequant,
+    moe_gateup, moe_down, moe_combine, residual add) for the same routing."""
+    ti, tv = routes
+
+    def step_fn():
+        x = x0.view(1, H)
+        for L, lay in enumerate(layers):
+            ids = ti[0, L].tolist()
+            xq, xs = dext.prequant(x)
+            gw = [lay.gate_wp[e] for e in ids] + [lay.up_wp[e] for e in ids]
+            gs = [lay.gate_ws[e] for e in ids] + [lay.up_ws[e] for e in ids]
+            gu = dext.moe_gateup(xq, xs, gw, gs, TOPK, 1, MI, H)
+            yd = dext.moe_down(gu, [lay.down_wp[e] for e in ids], [lay.down_ws[e] for e in ids],
+                               TOPK, 1, H, MI)
+            moe = dext.moe_combine(yd, w_dev[L], 1)[0]
+            x = x + moe.bfloat16().unsqueeze(0)
+        return x
+
+    w_dev = [tv[0, L].view(1, TOPK).cuda() for L in range(len(layers))]
+    step_fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        step_fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            step_fn()
+    torch.cuda.synchronize()
+    return graph
+
+
+# ----------------------------------------------------------------------------- prefill
+def bench_gemm(torch, lext, dext, M, N, K, reps=20):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(M + N + K)
+    x = torch.randn((M, K), generator=g, device="cuda").bfloat16()
+    w = (torch.randn((N, K), generator=g, device="cuda") * 0.02).bfloat16()
+    wp, wsc = dext.prequant(w)
+    xq, xs = dext.prequant(x)
+    res = {}
+    for name, fn in (("forward", lambda: lext.forward(x, wp, wsc)),
+                     ("lin_pq", lambda: dext.lin_pq(xq, xs, wp, wsc, M, N, K))):
+        fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(reps):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        ms = s.elapsed_time(e) / reps
+        flops = 2.0 * M * N * K
+        tflops = flops / (ms * 1e-3) / 1e12
+        byts = (M * K * 2 if name == "forward" else M * K // 2 + M * K // 32) + N * K // 2 + N * K // 32 + M * N * 4
+        t_roof = max(flops / (MXFP4_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9))
+        res[name] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
+                     "mfma_frac": round(tflops / MXFP4_PEAK_TFLOPS, 4),
+                     "roofline_frac": round(t_roof / (ms * 1e-3), 4), "bytes": byts}
+    return res
+
+
+def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
+    """Config 4: M=9 tokens, Zipf(1.1)-biased routing over 128 experts, grouped
+    drop-in path (moe_gateup + moe_down + moe_combine)."""
+    import numpy as np
+    M = 9
+    rng = np.random.default_rng(seed)
+    perm = rng.permutation(N_EXP)
+    p = 1.0 / np.arange(1, N_EXP + 1) ** 1.1
+    logp = np.log(p / p.sum())[np.argsort(perm)]
+    logits = torch.from_numpy((rng.standard_normal((M, N_EXP)) + beta * logp).astype(np.float32))
+    pr = torch.softmax(logits, -1)
+    tv, ti = torch.topk(pr, TOPK, -1)
+    tv = (tv / tv.sum(-1, keepdim=True)).cuda()
+    ids = ti.reshape(-1).tolist()
+    distinct = len(set(ids))
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    x = torch.randn((M, H), generator=g, device="cuda").bfloat16()
+    xq, xs = dext.prequant(x)
+    gw, gs, dw, ds = [], [], [], []
+    for m in range(M):
+        row = ids[m * TOPK:(m + 1) * TOPK]
+        gw += [lay.gate_wp[e] for e in row] + [lay.up_wp[e] for e in row]
+        gs += [lay.gate_ws[e] for e in row] + [lay.up_ws[e] for e in row]
+        dw += [lay.down_wp[e] for e in row]
+        ds += [lay.down_ws[e] for e in row]
+
+    def fn():
+        gu = dext.moe_gateup(xq, xs, gw, gs, TOPK, M, MI, H)
+        yd = dext.moe_down(gu, dw, ds, TOPK, M, H, MI)
+        return dext.moe_combine(yd, tv, M)
+
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            fn()
+    ms = time_graph(torch, graph, reps, 3)
+    byts = distinct * EXPERT_BYTES
+    return {"beta": beta, "distinct_experts": distinct, "us": round(ms * 1e3, 2),
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1), "bytes": byts}
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+def cpu_baseline(torch, layer0, routes):
+    """The reference's dequant + BF16 expert path (runtime/model_runner.py:
+    128-131, dequant runtime/weight_store.py:27-44) on this host's cores, for
+    one layer and one token (config 1) -- a reported baseline, not a target."""
+    import numpy as np
+    from oracle import ops
+    ncpu = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncpu)
+    ids = routes[0][0, 0].tolist()
+    w = routes[1][0, 0].numpy()
+    experts = {}
+    for e in ids:
+        experts[e] = tuple((getattr(layer0, p + "_wp")[e].cpu().numpy(), getattr(layer0, p + "_ws")[e].cpu().numpy())
+                           for p in ("gate", "up", "down"))
+    g = torch.Generator()
+    g.manual_seed(0)
+    x = torch.randn((1, H), generator=g).bfloat16()
+    topi = np.array([ids])
+    topv = w[None]
+
+    def run_full():
+        return ops.dequant_bf16_moe_layer_torch(x, topi, topv, experts=experts)
+
+    deq = {e: tuple(ops.dequant_bf16_torch(*experts[e][j]) for j in range(3)) for e in ids}
+
+    def run_nodeq():
+        return ops.dequant_bf16_moe_layer_torch(x, topi, topv, experts_deq_bf16=deq)
+
+    res = {}
+    for name, fn in (("with_dequant", run_full), ("without_dequant", run_nodeq)):
+        for _ in range(3):
+            fn()
+        ts = []
+        t_end = time.perf_counter() + 15.0
+        while len(ts) < 20 or (time.perf_counter() < t_end and len(ts) < 200):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+            if len(ts) >= 20 and time.perf_counter() > t_end:
+                break
+        res[name] = float(np.median(ts)) * 1e6
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(LAYER_BYTES / (res["with_dequant"] * 1e-6) / 1e9, 3), "unit": "GB/s",
+            "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "1 MoE layer x 1 token (config 1: 8 of 128 experts, H=2048, Mi=768), dequant + bf16 "
+                      "F.linear chain with torch-CPU, median of >=20 after 3 warm-ups",
+            "us_per_layer_with_dequant": round(res["with_dequant"], 1),
+            "us_per_layer_without_dequant": round(res["without_dequant"], 1),
+            "cpu_model": cpu_model, "affinity_cores": ncpu}
+
+
+# ----------------------------------------------------------------------------- main
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the multi-GPU "
+              "design is described in DESIGN.md but not run.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from moe_fused_inference_amd import _lib, get_decode_ext, get_ext
+    from moe_fused_inference_amd.moe_layer import layer_status, workspace
+    lib = _lib.load()
+    dext, lext = get_decode_ext(), get_ext()
+    dev = "cuda"
+    torch.cuda.set_device(0)
+    log(f"device: {torch.cuda.get_device_name(0)}")
+
+    t0 = time.time()
+    layers = build_layers(torch, lib, dev, LAYERS)
+    log(f"weights resident: {LAYERS * N_EXP * EXPERT_BYTES / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    routes = draw_routes(torch, S_ROUTES, LAYERS, seed=7)
+    g = torch.Generator(device=dev)
+    g.manual_seed(0)
+    x0 = torch.randn(H, generator=g, device=dev).bfloat16()
+    ws = workspace(TOPK, MI, dev)
+    outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
+    bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    graph, _ = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
+    log("decode graph captured")
+    ms_replay = time_graph(torch, graph, args.steps, args.warmup)
+    if layer_status(ws) != 0:
+        raise RuntimeError("fused decode layer reported an expired wait")
+    n_launch = S_ROUTES * LAYERS
+    us_layer = ms_replay * 1e3 / n_launch
+    gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
+    ms_step = us_layer * LAYERS / 1e3
+    log(f"fused decode: {us_layer:.3f} us/layer, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+    if args.profile_decode_only:
+        return
+
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "decode_layer_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    extra = {}
+    if not args.skip_extra:
+        dg = dropin_graph(torch, dext, layers, routes, x0)
+        ms_d = time_graph(torch, dg, max(3, args.steps // 2), 2)
+        us_d = ms_d * 1e3 / LAYERS
+        extra["dropin_path"] = {"us_per_layer": round(us_d, 3),
+                                "gbs": round(LAYER_BYTES / (us_d * 1e-6) / 1e9, 1),
+                                "launches_per_layer": 4,
+                                "note": "prequant + moe_gateup + moe_down + moe_combine + bf16 residual "
+                                        "(torch add), graph-captured, activations MXFP4 as the reference"}
+        log(f"drop-in path: {us_d:.3f} us/layer")
+        pre = {}
+        for (M, N, K) in ((512, 1536, 2048), (2048, 2048, 768), (4096, 4096, 2048)):
+            pre[f"{M}x{N}x{K}"] = bench_gemm(torch, lext, dext, M, N, K)
+            log(f"gemm {M}x{N}x{K}: {pre[f'{M}x{N}x{K}']}")
+        extra["prefill_gemm"] = pre
+        sv = [bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]
+        extra["spec_verify_m9"] = sv
+        log(f"spec verify: {sv}")
+
+    cpu = None
+    if not args.no_cpu:
+        t0 = time.time()
+        cpu = cpu_baseline(torch, layers[0], routes)
+        log(f"cpu baseline: {cpu} ({time.time() - t0:.1f}s)")
+
+    line = {
+        "metric": METRIC, "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "mxfp4(e2m1,e8m0) weights x e4m3x3 activations -> f32",
+        "data": "synthetic (seeded random-init weights and router logits)",
+        "config": {"workload": "config 2: decode MoE layer, batch 1, top-8 of 128 experts, H=2048, Mi=768, "
+                               "48 resident layers (15.4 GB), fresh routing per layer, fused one-launch kernel",
+                   "layers": LAYERS, "experts": N_EXP, "top_k": TOPK, "hidden": H, "moe_intermediate": MI,
+                   "graph_steps_per_replay": S_ROUTES},
+        "us_per_layer": round(us_layer, 3), "tok_per_s": round(1e3 / ms_step, 1),
+        "layer_bytes": LAYER_BYTES, "layer_flops": LAYER_FLOPS,
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "decode_layer_kernel<false>",
+                     "timing": "HIP events around graph replays; mean over all launches incl. gaps"},
+        "cpu_baseline": cpu,
+    }
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -134,6 +134,40 @@ int mxfp4_moe_down_devtab(const float* gu, const int64_t* wp_tab, const int64_t*
 int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
                       float* out, int M, int N, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Fused decode MoE layer, one launch per layer, batch 1.
+ * Replaces the per-layer sequence prequant -> moe_gateup -> moe_down ->
+ * moe_combine -> `x + moe.bfloat16()` of runtime/model_runner_v2.py:185-208
+ * for one token, computed on the UN-quantized bf16 activations (the
+ * dequant-to-BF16 path of runtime/model_runner.py:128-131 in fp32).
+ *   x          bf16 (H), 16-byte aligned
+ *   routing    E expert ids + E combine weights (runtime/model_runner_v2.py:
+ *              189-192), either by value from the host (ids_host/w_host,
+ *              ids_dev = w_dev = NULL) or in device memory (ids_dev/w_dev)
+ *   weights    per layer, the n_experts experts stacked back to back, each
+ *              in the reference layout: gate/up (Mi, H/2) + (Mi, H/32),
+ *              down (H, Mi/2) + (H, Mi/32)
+ *   out        fp32 (H): sum_e w_e * down_e(silu(gate_e x) * up_e x)
+ *   resid_out  optional bf16 (H): bf16(x + bf16(out)), or NULL
+ *   workspace  device memory of mxfp4_decode_layer_workspace_size(E, Mi)
+ *              bytes, 256-byte aligned, zero-initialised once (or
+ *              mxfp4_decode_layer_reset); launches that share a workspace
+ *              must be stream-ordered.
+ * Limits: E <= 8, H a multiple of 512 up to 2048, Mi a multiple of 32 up to
+ * 1024.  Returns MXFP4_OK or an error; a bounded internal wait that expired
+ * is reported by mxfp4_decode_layer_status.
+ */
+size_t mxfp4_decode_layer_workspace_size(int E, int Mi);
+int mxfp4_decode_layer_reset(void* workspace, void* stream);
+int mxfp4_decode_layer_status(const void* workspace, int* error_flag);
+int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* w_host,
+                           const int32_t* ids_dev, const float* w_dev,
+                           const uint8_t* gate_wp, const uint8_t* gate_ws,
+                           const uint8_t* up_wp, const uint8_t* up_ws,
+                           const uint8_t* down_wp, const uint8_t* down_ws,
+                           int n_experts, int E, int H, int Mi, float* out, void* resid_out,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -39,8 +39,10 @@ constexpr int kBlock = 32;
 
 // ---------------------------------------------------------------- quantizer
 // E8M0 code of the smallest 2^e with amax <= 6*2^e (quant/fp4_format.py:73-88).
+// amax <= 0 gives 127 (:78-79); so does an infinite amax, because the
+// reference's frexp(inf) yields exponent 0 (:81-88).
 __device__ __forceinline__ uint32_t e8m0_code(float amax) {
-    if (!(amax > 0.0f)) return 127u;
+    if (!(amax > 0.0f) || !(amax <= 3.402823466e38f)) return 127u;
     uint32_t bits = __float_as_uint(amax);
     int ex = (int)(bits >> 23);
     uint32_t frac = bits & 0x7FFFFFu;

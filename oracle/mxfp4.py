@@ -55,14 +55,16 @@ def e2m1_decode(codes):
 def e8m0_code(amax):
     """Block amax -> E8M0 code of the smallest 2^e with amax <= 6 * 2^e.
 
-    e is clamped to [-127, 127]; amax <= 0 gives 127 (scale 1.0).
-    quant/fp4_format.py:73-88.  Vectorised; amax is any float array.
+    e is clamped to [-127, 127]; amax <= 0 gives 127 (scale 1.0).  An infinite
+    amax also gives 127: the reference computes frexp(inf) = (inf, 0), i.e.
+    exponent 0.  quant/fp4_format.py:73-88.  Vectorised; amax is any float array.
     """
     a = np.asarray(amax, dtype=np.float64)
-    m, q = np.frexp(a)
+    with np.errstate(invalid="ignore"):
+        m, q = np.frexp(np.where(np.isfinite(a), a, 1.0))
     e = np.where(m <= 0.75, q - 3, q - 2)
     e = np.clip(e, -E8M0_BIAS, E8M0_BIAS)
-    return np.where(a > 0, e + E8M0_BIAS, E8M0_BIAS).astype(np.uint8)
+    return np.where((a > 0) & np.isfinite(a), e + E8M0_BIAS, E8M0_BIAS).astype(np.uint8)
 
 
 def e8m0_scale_f32(codes):

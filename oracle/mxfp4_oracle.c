@@ -18,7 +18,7 @@
 /* Smallest e with amax <= 6 * 2^e, clamped to [-127, 127]; code e + 127;
  * amax <= 0 -> 127.  quant/fp4_format.py:73-88. */
 uint8_t mxo_e8m0_code(float amax) {
-    if (!(amax > 0.0f)) return 127;
+    if (!(amax > 0.0f) || isinf(amax)) return 127; /* frexp(inf) -> exponent 0 */
     uint32_t bits;
     memcpy(&bits, &amax, 4);
     int32_t ex = (int32_t)((bits >> 23) & 0xFF);
@@ -43,6 +43,7 @@ uint8_t mxo_e8m0_code(float amax) {
  * mxo_e8m0_code. */
 uint8_t mxo_e8m0_code_frexp(float amax) {
     if (!(amax > 0.0f)) return 127;
+    if (isinf(amax)) return 127;
     int e;
     double m = frexp((double)amax / 6.0, &e);
     int ep = (m == 0.5) ? e - 1 : e;

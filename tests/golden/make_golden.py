@@ -58,9 +58,13 @@ def edge_rows():
     r[0] = 96.0
     r[1:8] = -np.float32(2.0 ** -20)
     r[33] = np.float32(3.0) * np.float32(2.0 ** -126)   # denormal-range amax block
-    r[34] = -np.float32(2.0 ** -140)
+    r[34] = -np.float32(2.0 ** -133)                    # smallest bf16 denormal
+    r[40] = np.float32(np.inf)                          # inf amax -> scale code 127
+    r[41] = np.float32(-7.5)
     rows.append(r)
-    return np.stack(rows)
+    out = np.stack(rows)
+    assert np.array_equal(fmt.bf16_round(out), out), "edge rows must be bf16-exact"
+    return out
 
 
 def vectors():

@@ -55,6 +55,16 @@ def test_reference_kat_points():
         assert amax / scale <= 6.0
 
 
+def test_infinite_amax_gives_scale_one():
+    # quant/fp4_format.py:81-88: math.frexp(inf) == (inf, 0) -> e = 0 -> code 127
+    assert math.frexp(float("inf"))[1] == 0
+    assert int(fmt.e8m0_code(np.float32(np.inf))) == 127
+    assert int(cbuild.lib().mxo_e8m0_code(float("inf"))) == 127
+    q, s = fmt.quantize_rows(np.array([[np.inf, -7.5, 1.0] + [0.0] * 29], np.float32))
+    assert s[0, 0] == 127
+    assert (q[0, 0] & 0xF) == 7 and (q[0, 0] >> 4) == 15 and (q[0, 1] & 0xF) == 2
+
+
 def test_reference_kat_pack():
     k = _kat()["pack"]
     packed, pad = fmt.pack_nibbles(np.array(k["codes"], np.uint8))
