@@ -49,8 +49,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--profile-decode-only", action="store_true",
-                    help="run only the fused decode graph (for rocprofv3 runs)")
+    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec"], default=None,
+                    help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
 
 
@@ -306,6 +306,19 @@ def cpu_baseline(torch, layer0, routes):
             "cpu_model": cpu_model, "affinity_cores": ncpu}
 
 
+def only_extra(args, torch, dext, lext, layers, routes, x0):
+    """Single measurements for profiling runs."""
+    if args.only == "dropin":
+        dg = dropin_graph(torch, dext, layers, routes, x0)
+        ms_d = time_graph(torch, dg, args.steps, args.warmup)
+        log(f"drop-in path: {ms_d * 1e3 / LAYERS:.3f} us/layer")
+    elif args.only == "gemm":
+        for (M, N, K) in ((512, 1536, 2048), (2048, 2048, 768), (4096, 4096, 2048)):
+            log(f"gemm {M}x{N}x{K}: {bench_gemm(torch, lext, dext, M, N, K)}")
+    elif args.only == "spec":
+        log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
+
+
 # ----------------------------------------------------------------------------- main
 def main():
     args = parse()
@@ -324,7 +337,10 @@ def main():
 
     t0 = time.time()
     layers = build_layers(torch, lib, dev, LAYERS)
-    log(f"weights resident: {LAYERS * N_EXP * EXPERT_BYTES / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    torch.cuda.synchronize()
+    chk = float(layers[LAYERS - 1].down_wp[N_EXP - 1].float().mean())
+    log(f"weights resident: {LAYERS * N_EXP * EXPERT_BYTES / 1e9:.2f} GB in {time.time() - t0:.1f}s "
+        f"(allocated {torch.cuda.memory_allocated() / 1e9:.2f} GB, last-expert byte mean {chk:.2f})")
     routes = draw_routes(torch, S_ROUTES, LAYERS, seed=7)
     g = torch.Generator(device=dev)
     g.manual_seed(0)
@@ -332,8 +348,21 @@ def main():
     ws = workspace(TOPK, MI, dev)
     outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    graph, _ = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
+    if args.only in ("dropin", "gemm", "spec"):
+        return only_extra(args, torch, dext, lext, layers, routes, x0)
+    graph, calls = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
     log("decode graph captured")
+    # eager back-to-back launches of the same calls (no graph), for comparison
+    for c in calls[:LAYERS]:
+        c()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for c in calls:
+        c()
+    ev1.record()
+    torch.cuda.synchronize()
+    log(f"eager fused launches: {ev0.elapsed_time(ev1) * 1e3 / len(calls):.3f} us/layer")
     ms_replay = time_graph(torch, graph, args.steps, args.warmup)
     if layer_status(ws) != 0:
         raise RuntimeError("fused decode layer reported an expired wait")
@@ -342,7 +371,7 @@ def main():
     gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
     ms_step = us_layer * LAYERS / 1e3
     log(f"fused decode: {us_layer:.3f} us/layer, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
-    if args.profile_decode_only:
+    if args.only == "decode":
         return
 
     traffic = None

@@ -45,7 +45,7 @@ def routing(g, n_exp, E):
     return ti.int(), tv.float()
 
 
-@pytest.mark.parametrize("n_exp,E,H,Mi", [(16, 8, 2048, 768), (6, 4, 512, 256), (5, 3, 1024, 96)])
+@pytest.mark.parametrize("n_exp,E,H,Mi", [(16, 8, 2048, 768), (6, 4, 512, 256), (5, 3, 1024, 96), (4, 2, 1536, 160)])
 def test_decode_layer_vs_bf16_oracle(dext, n_exp, E, H, Mi):
     stack = make_stack(dext, n_exp, H, Mi, seed=500 + H)
     g = torch.Generator(device=DEV)
