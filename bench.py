@@ -345,7 +345,7 @@ def main():
     g = torch.Generator(device=dev)
     g.manual_seed(0)
     x0 = torch.randn(H, generator=g, device=dev).bfloat16()
-    ws = workspace(TOPK, MI, dev)
+    ws = workspace(TOPK, MI, H, dev)
     outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     if args.only in ("dropin", "gemm", "spec"):

@@ -29,7 +29,7 @@ extern "C" {
 enum {
     MXFP4_OK = 0,
     MXFP4_EINVAL = -1,   /* argument check failed; message in mxfp4_last_error() */
-    MXFP4_ETIMEOUT = -2  /* a fused kernel's bounded wait expired (see mxfp4_decode_status) */
+    MXFP4_ETIMEOUT = -2  /* a fused kernel's bounded wait expired (see mxfp4_decode_layer_status) */
 };
 
 /* Activation dtypes accepted by the quantizers. */
@@ -150,15 +150,17 @@ int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
  *   out        fp32 (H): sum_e w_e * down_e(silu(gate_e x) * up_e x)
  *   resid_out  optional bf16 (H): bf16(x + bf16(out)), or NULL
  *   workspace  device memory of mxfp4_decode_layer_workspace_size(E, Mi)
- *              bytes, 256-byte aligned, zero-initialised once (or
- *              mxfp4_decode_layer_reset); launches that share a workspace
- *              must be stream-ordered.
+ *              bytes, 256-byte aligned, initialised by
+ *              mxfp4_decode_layer_reset(workspace, E, H, Mi) for the (E, H, Mi)
+ *              every launch on it must use; launches sharing a workspace must
+ *              be stream-ordered (a launch with another shape sets the error
+ *              flag instead of waiting).
  * Limits: E <= 8, H a multiple of 512 up to 2048, Mi a multiple of 32 up to
  * 1024.  Returns MXFP4_OK or an error; a bounded internal wait that expired
- * is reported by mxfp4_decode_layer_status.
+ * (or a workspace/shape mismatch) is reported by mxfp4_decode_layer_status.
  */
 size_t mxfp4_decode_layer_workspace_size(int E, int Mi);
-int mxfp4_decode_layer_reset(void* workspace, void* stream);
+int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream);
 int mxfp4_decode_layer_status(const void* workspace, int* error_flag);
 int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* w_host,
                            const int32_t* ids_dev, const float* w_dev,

@@ -30,7 +30,7 @@ SIGNATURES = {
     "mxfp4_moe_down_devtab": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_moe_combine": (_c_i, [_c_p, _c_i, _c_p, _c_i, _c_p, _c_i, _c_i, _c_p]),
     "mxfp4_decode_layer_workspace_size": (_c_sz, [_c_i, _c_i]),
-    "mxfp4_decode_layer_reset": (_c_i, [_c_p, _c_p]),
+    "mxfp4_decode_layer_reset": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_decode_layer_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),
     "mxfp4_moe_decode_layer": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                       _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),

@@ -25,27 +25,31 @@
 // gate/up workgroup is resident or finished before any down workgroup waits:
 // the wait cannot deadlock.  It is still bounded (kSpinLimit polls); on expiry
 // the kernel sets an error flag, skips its work and exits normally.
-//   * Each gate/up workgroup publishes its 32 values of h with agent-scope
-//     atomic stores (write-through to the device coherence point), drains its
-//     store counter (s_waitcnt vmcnt(0)), then bumps the arrival counter of
-//     its slot -- one counter per slot, each in its own cache line, so the
-//     Mi/32 increments per slot do not all serialise on one address.  (A
-//     release/acquire fence pair would instead write back and invalidate a
-//     whole L2 per workgroup.)
-//   * Counters only ever grow.  Down workgroup b keeps, in the workspace, the
-//     count it expects for each slot ("memo"); it waits until every slot's
-//     counter reaches memo + Mi/32, reads h with agent-scope loads and stores
-//     the new memo.  All counters and memos advance by the same amount per
-//     launch, so no reset and no departure counter are needed between
-//     launches or graph replays.  A workspace is tied to one H (the set of
-//     down workgroups); mxfp4_decode_layer_reset zeroes it.
-//   * Within one launch every h line is written before any reader touches
-//     it, and each launch starts with the dispatch-level cache invalidation,
-//     so no reader can hold a stale copy.
+//   * h travels as tagged 64-bit words: 32 bits of payload (E4M3 bytes or the
+//     3 scale codes of a 32-block) and a 32-bit generation tag, written with
+//     agent-scope atomic stores (write-through to the device coherence
+//     point).  A down workgroup polls the very words it needs until every tag
+//     equals the current generation -- the data is the flag, so there is no
+//     store drain, no counter and no extra round trip between "ready" and
+//     "read".  (A release/acquire fence pair would instead write back and
+//     invalidate a whole L2 per workgroup.)
+//   * The generation is the number of launches on the workspace: every
+//     workgroup keeps its own count ("memo") in the workspace, reads it at
+//     start and stores count+1 at the end, so all counts advance together
+//     with no reset between launches or graph replays.  This requires every
+//     launch on a workspace to use the same (E, H, Mi); the workspace header
+//     records them (mxfp4_decode_layer_reset) and a mismatching launch sets
+//     the error flag instead of waiting.
+//   * Within one launch every h word is written once before it is consumed,
+//     and each launch starts with the dispatch-level cache invalidation, so
+//     no reader can hold a stale copy; a word from the previous launch
+//     carries the previous generation and is simply polled again.
 //
-// Registers are kept under 128 VGPRs (h is staged through LDS, the down
+// Registers are kept near 128 VGPRs (h is staged through LDS, the down
 // K-step count is a template bound) so that every workgroup of a layer is
-// resident from the start and all weight loads are in flight at once.
+// resident from the start and all weight loads are in flight at once.  The
+// MFMA loops read their operands with clamped, unconditional LDS loads so the
+// reads of a phase issue back to back ahead of the MFMA chain.
 //
 // Activations on the MFMA: there is no bf16 x FP4 MFMA, so the bf16 x (and the
 // fp32 h) is split into three E4M3 terms hi + mid + lo, each with its own E8M0
@@ -59,14 +63,17 @@
 
 namespace {
 
-constexpr int kSpinLimit = 1 << 22;   // polls of the arrival counters (~0.2 s)
+constexpr int kSpinLimit = 1 << 22;   // polls of one word (~0.2 s)
 constexpr int kTerms = 3;             // E4M3 terms per activation value
 constexpr int kMaxE = 8;
+constexpr int kRecWords = 25;         // tagged words per (slot, 32-block) record of h:
+                                      // 24 x 4 E4M3 bytes (3 terms x 32) + 1 word of scale codes
 // workspace layout (bytes)
-constexpr int kCtrOff = 0;            // int32 counter of slot s at kCtrOff + 128*s
-constexpr int kErrOff = 1024;         // int32 error flag
-constexpr int kMemoOff = 2048;        // int32 memo[H/16][8]
-constexpr int kHOff = 8192;           // h terms, then h scale codes
+constexpr int kCfgOff = 0;            // int32 config word written by reset
+constexpr int kErrOff = 256;          // int32 error flag
+constexpr int kMemoAOff = 1024;       // int32 generation of gate/up workgroup (s, jb): [8][32]
+constexpr int kMemoBOff = 2048;       // int32 generation of down workgroup cb: [128]
+constexpr int kHOff = 4096;           // h records: (E, Mi/32, kRecWords) uint64
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -83,12 +90,15 @@ struct LayerArgs {
     int32_t ids[kMaxE];       // by-value ids when ids_dev is null
     float w[kMaxE];           // by-value weights when w_dev is null
     int E, H, Mi;
+    int cfg;                  // expected workspace config word
     float* out;               // (H) fp32 moe output
     uint16_t* resid;          // (H) bf16 x + bf16(out), or null
     uint8_t* ws;              // workspace base
-    uint8_t* hs8;             // (E, kTerms, Mi) E4M3 terms of h
-    uint32_t* hsc;            // (E, Mi/32) scale codes of terms 0..2 in bytes 0..2
 };
+
+__host__ __device__ constexpr int layer_cfg(int E, int H, int Mi) {
+    return 0x5A000000 | (E << 16) | ((H / 512) << 12) | (Mi / 32);
+}
 
 // E8M0 code of the smallest 2^e with amax <= 448*2^e (E4M3 range), e in
 // [-127, 127]; zero blocks get 127.
@@ -165,8 +175,6 @@ __device__ __forceinline__ float pick_w(const LayerArgs& a, int s) {
     return w;
 }
 
-__device__ __forceinline__ void drain_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-
 // Unconditional load from an always-valid (clamped) address, value selected
 // afterwards: keeps every load of a phase in one basic block so the compiler
 // can wait for exactly the loads a computation needs.
@@ -176,15 +184,13 @@ __device__ __forceinline__ T ld_sel(const T* p, bool ok, T zero) {
     return ok ? v : zero;
 }
 
-// FP8-A operand of one MFMA K-step for lane (r = term row, g) when B lane
-// group gb holds 32-block phys(gb) of this step: bytes 0..15 <- logical K
-// 16g..16g+15 (B group g/2, elements 16*(g%2)..), bytes 16..31 <- logical K
-// 64+16g.. (B group 2+g/2).
-__device__ __forceinline__ mx::v8i fp8_operand(const uint8_t* row8, int blk_lo, int blk_hi, int g) {
-    const uint4 lo = *reinterpret_cast<const uint4*>(row8 + blk_lo * 32 + 16 * (g & 1));
-    const uint4 hi = *reinterpret_cast<const uint4*>(row8 + blk_hi * 32 + 16 * (g & 1));
+__device__ __forceinline__ mx::v8i cat8(uint4 lo, uint4 hi) {
     mx::v8i a = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     return a;
+}
+
+__device__ __forceinline__ void set_error(const LayerArgs& a) {
+    __hip_atomic_store(reinterpret_cast<int*>(a.ws + kErrOff), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 union Smem {
@@ -195,8 +201,8 @@ union Smem {
         float h[2][32];
     } a;
     struct {                                       // down workgroups
-        uint8_t h8[kMaxE * kTerms * 1024];         // E4M3 terms of h (Mi <= 1024)
-        uint32_t hsc[kMaxE * 32];
+        uint8_t h8[kMaxE * kTerms * 1024];         // E4M3 terms of h, [slot][term][Mi]
+        uint32_t hsc[kMaxE * 32];                  // [slot][32-block]: codes of terms 0..2
         float red[4][16];
         int abort;
     } b;
@@ -210,10 +216,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15;
     const int g = lane >> 4;
+    const int rr = r < kTerms ? r : 0;     // A-operand term row read by this lane (rows >= 3 are zero)
     const int nblk_mi = a.Mi >> 5;
     const int nA = a.E * nblk_mi;
     const int bid = blockIdx.x;
-    int* ctr = reinterpret_cast<int*>(a.ws + kCtrOff);
+    uint64_t* hrec = reinterpret_cast<uint64_t*>(a.ws + kHOff);
 
     if (bid < nA) {
         // ================================================= gate / up
@@ -229,6 +236,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int k0 = threadIdx.x * 8;
         uint4 xq = make_uint4(0, 0, 0, 0);
         if (k0 < H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
+        int* memo = reinterpret_cast<int*>(a.ws + kMemoAOff) + s * 32 + jb;
+        const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+        const int gen = *memo + 1;
 
         const int e = DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[s]) : pick_id(a, s);
         const uint8_t* gw = a.gate_wp + (int64_t)e * a.wp_stride_gu;
@@ -279,59 +289,73 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         }
         __syncthreads();
 
-        // MFMA: step i covers blocks {bpw*wave + sa*gb + i : gb = 0..3}
+        // MFMA: step i covers blocks {bpw*wave + sa*gb + i : gb = 0..3}.
+        // Operands first (clamped unconditional LDS reads), then the MFMAs.
+        mx::v8i av[4];
+        uint32_t asc[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int base = bpw * wave + min(i, sa - 1);
+            const mx::v8i v = cat8(*reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (g >> 1)) * 32 + 16 * (g & 1)]),
+                                   *reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (2 + (g >> 1))) * 32 + 16 * (g & 1)]));
+            const uint32_t c = sm.a.xsc[rr][base + sa * g];
+            const bool ok = r < kTerms && i < sa;
+            av[i] = ok ? v : (mx::v8i){0, 0, 0, 0, 0, 0, 0, 0};
+            asc[i] = ok ? c : 127u;
+        }
         mx::v4f acc[4];
 #pragma unroll
         for (int G = 0; G < 4; ++G) acc[G] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            if (i >= sa) break;
-            mx::v8i av = {0, 0, 0, 0, 0, 0, 0, 0};
-            uint32_t asc = 127u;
-            if (r < kTerms) {
-                const int base = bpw * wave + i;
-                av = fp8_operand(sm.a.x8[r], base + sa * (g >> 1), base + sa * (2 + (g >> 1)), g);
-                asc = sm.a.xsc[r][base + sa * g];
-            }
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int G = 0; G < 4; ++G)
-                acc[G] = mx::mfma16_fp8a_fp4b(av, bq[G][i], acc[G], asc, (bsc4[G] >> (8 * i)) & 0xFFu);
-        }
+                acc[G] = mx::mfma16_fp8a_fp4b(av[i], bq[G][i], acc[G], asc[i], (bsc4[G] >> (8 * i)) & 0xFFu);
+#pragma unroll
+        for (int G = 0; G < 4; ++G) mx::pin(acc[G]);   // complete the chain before the lane < 16 branch
         // rows 0..2 of D (the three terms) are elements 0..2 of lanes 0..15
         if (lane < 16) {
 #pragma unroll
             for (int G = 0; G < 4; ++G) sm.a.red[wave][G][lane] = acc[G][0] + acc[G][1] + acc[G][2];
         }
         __syncthreads();
-        if (threadIdx.x < 64) {
-            const int G = threadIdx.x >> 4;   // 0,1 gate halves; 2,3 up halves
-            const int n = threadIdx.x & 15;
-            sm.a.h[G >> 1][16 * (G & 1) + n] =
-                sm.a.red[0][G][n] + sm.a.red[1][G][n] + sm.a.red[2][G][n] + sm.a.red[3][G][n];
-        }
-        __syncthreads();
-        // h = silu(g) * u for the 32 rows, split into E4M3 terms, published
-        // with agent-scope stores; then the slot's arrival counter
-        if (threadIdx.x < 4) {
+        // h = silu(g) * u for the 32 rows (lanes 0..31 of wave 0), split into
+        // E4M3 terms by lane quads 0..3, published as tagged words by lanes 0..24
+        if (wave == 0) {
             float v[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
-                const int j = threadIdx.x * 8 + i;
-                v[i] = mx::silu_mul(sm.a.h[0][j], sm.a.h[1][j]);
+                const int j = (lane & 3) * 8 + i;
+                float gsum = 0.f, usum = 0.f;
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    gsum += sm.a.red[w][j >> 4][j & 15];
+                    usum += sm.a.red[w][2 + (j >> 4)][j & 15];
+                }
+                v[i] = mx::silu_mul(gsum, usum);
             }
             uint64_t w8[kTerms];
             uint32_t codes;
-            split8(v, w8, codes);
-#pragma unroll
-            for (int t = 0; t < kTerms; ++t) {
-                uint64_t* dst = reinterpret_cast<uint64_t*>(a.hs8 + ((int64_t)s * kTerms + t) * a.Mi + j0 + threadIdx.x * 8);
-                __hip_atomic_store(dst, w8[t], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            split8(v, w8, codes);  // lanes 0..3 hold the block (lanes 4.. repeat it)
+            // word w < 24: term w/8, bytes 4*(w%8).. of the 32-byte term block,
+            // held by lane (w%8)/2 in half (w%2) of its 8 bytes; word 24: codes
+            const int wi = lane;
+            const int src = (wi % 8) >> 1;
+            const int t = wi >> 3;
+            const uint64_t s0 = __shfl(w8[0], src), s1 = __shfl(w8[1], src), s2 = __shfl(w8[2], src);
+            const uint64_t sel = (t == 0) ? s0 : ((t == 1) ? s1 : s2);
+            const uint32_t codes0 = __shfl(codes, 0);
+            uint32_t payload = (wi & 1) ? (uint32_t)(sel >> 32) : (uint32_t)sel;
+            payload = (wi == 24) ? codes0 : payload;
+            const bool cfg_ok = cfg == a.cfg;
+            if (wi < kRecWords && cfg_ok)
+                __hip_atomic_store(hrec + ((int64_t)s * nblk_mi + jb) * kRecWords + wi,
+                                   (uint64_t)payload | ((uint64_t)(uint32_t)gen << 32), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+            if (lane == 0) {
+                *memo = gen;
+                if (!cfg_ok) set_error(a);
             }
-            if (threadIdx.x == 0)
-                __hip_atomic_store(a.hsc + (int64_t)s * nblk_mi + jb, codes, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            drain_stores();
-            if (threadIdx.x == 0)
-                __hip_atomic_fetch_add(ctr + 32 * s, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
         return;
     }
@@ -342,6 +366,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int Mi = a.Mi;
     const int kb = Mi >> 5;          // 32-blocks per down row (24)
     const int steps = (kb + 3) >> 2; // MFMA K-steps (6), <= MS
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoBOff) + cb;
+    const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+    const int gen = *memo + 1;
     // wave handles slots 2*wave, 2*wave+1; lane group g owns blocks
     // g*steps .. g*steps+steps-1 of its row
     int slot[2], eid[2];
@@ -385,52 +412,60 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         }
     }
 
-    // wait until every slot's counter reaches this workgroup's memo + Mi/32
-    int* memo = reinterpret_cast<int*>(a.ws + kMemoOff) + cb * kMaxE;
-    if (wave == 0) {
-        const bool mine = lane < a.E;
-        const int target = (mine ? memo[lane] : 0) + nblk_mi;
+    // poll the tagged h words of all slots until they carry this launch's
+    // generation, then stage them in LDS (thread t owns words t, t+256, ...)
+    const int nwords = a.E * nblk_mi * kRecWords;
+    const bool cfg_ok = cfg == a.cfg;
+    constexpr int kPer = (kMaxE * 4 * MS * kRecWords + 255) / 256;  // max words per thread
+    uint64_t wv[kPer];
+    bool ok = cfg_ok;
+    if (cfg_ok) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int wi = threadIdx.x + 256 * k;
+            wv[k] = __hip_atomic_load(hrec + min(wi, nwords - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         int spins = 0;
-        bool ok = true;
         while (true) {
-            const int c = mine ? __hip_atomic_load(ctr + 32 * lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : target;
-            if (__ballot(c - target < 0) == 0ull) break;
-            __builtin_amdgcn_s_sleep(2);
+            bool pending = false;
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int wi = threadIdx.x + 256 * k;
+                pending |= (wi < nwords) && ((uint32_t)(wv[k] >> 32) != (uint32_t)gen);
+            }
+            if (!pending) break;
             if (++spins >= kSpinLimit) {
                 ok = false;
                 break;
             }
+            __builtin_amdgcn_s_sleep(2);
+#pragma unroll
+            for (int k = 0; k < kPer; ++k) {
+                const int wi = threadIdx.x + 256 * k;
+                if (wi < nwords && (uint32_t)(wv[k] >> 32) != (uint32_t)gen)
+                    wv[k] = __hip_atomic_load(hrec + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
-        if (mine) memo[lane] = target;
-        if (lane == 0) {
-            if (!ok) __hip_atomic_store(reinterpret_cast<int*>(a.ws + kErrOff), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            sm.b.abort = ok ? 0 : 1;
+        // word wi of record (slot, block) -> LDS: term bytes or the codes word
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int wi = threadIdx.x + 256 * k;
+            if (wi < nwords) {
+                const int rec = wi / kRecWords;
+                const int w = wi - rec * kRecWords;
+                const int sl = rec / nblk_mi;
+                const int blk = rec - sl * nblk_mi;
+                const uint32_t payload = (uint32_t)wv[k];
+                if (w < 24)
+                    *reinterpret_cast<uint32_t*>(sm.b.h8 + (sl * kTerms + (w >> 3)) * Mi + blk * 32 + (w & 7) * 4) = payload;
+                else
+                    sm.b.hsc[sl * 32 + blk] = payload;
+            }
         }
     }
-    __syncthreads();
-    const bool abort = sm.b.abort != 0;
-
-    // stage h (all slots, agent-scope loads) in LDS
-    const int hbytes = a.E * kTerms * Mi;       // multiple of 96
-    if (!abort) {
-        uint64_t tmp[12];
-#pragma unroll
-        for (int k = 0; k < 12; ++k) {
-            const int off = (threadIdx.x + 256 * k) * 8;
-            tmp[k] = __hip_atomic_load(reinterpret_cast<const uint64_t*>(a.hs8 + min(off, hbytes - 8)),
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        const uint32_t hs = threadIdx.x < a.E * kb
-                                ? __hip_atomic_load(a.hsc + threadIdx.x, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                : 0u;
-#pragma unroll
-        for (int k = 0; k < 12; ++k) {
-            const int off = (threadIdx.x + 256 * k) * 8;
-            if (off < hbytes) *reinterpret_cast<uint64_t*>(sm.b.h8 + off) = tmp[k];
-        }
-        if (threadIdx.x < a.E * kb) sm.b.hsc[threadIdx.x] = hs;
-    }
-    __syncthreads();
+    if (!ok) set_error(a);
+    if (threadIdx.x == 0) *memo = gen;
+    const bool abort = __syncthreads_or(!ok);
 
     float part = 0.0f;  // this lane's (lane < 16) partial combine over its slots
     if (!abort) {
@@ -438,31 +473,34 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             if (slot[q] >= a.E) continue;
-            const uint8_t* h8 = sm.b.h8 + (slot[q] * kTerms + (r < kTerms ? r : 0)) * Mi;
-            const uint32_t* hsq = sm.b.hsc + slot[q] * kb;
-            mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+            const uint8_t* h8 = sm.b.h8 + (slot[q] * kTerms + rr) * Mi;
+            const uint32_t* hsq = sm.b.hsc + slot[q] * 32;
+            // operands of all steps first (clamped unconditional LDS reads)
+            mx::v8i av[MS];
+            uint32_t asc[MS];
 #pragma unroll
             for (int i = 0; i < MS; ++i) {
-                if (i >= steps) break;
                 // step i: B lane group gb holds block gb*steps + i
                 const int blo = (g >> 1) * steps + i;
                 const int bhi = (2 + (g >> 1)) * steps + i;
                 const int bown = g * steps + i;
-                mx::v8i av = {0, 0, 0, 0, 0, 0, 0, 0};
-                uint32_t asc = 127u;
-                if (r < kTerms) {
-                    const uint4 lo = blo < kb ? *reinterpret_cast<const uint4*>(h8 + blo * 32 + 16 * (g & 1))
-                                              : make_uint4(0, 0, 0, 0);
-                    const uint4 hi = bhi < kb ? *reinterpret_cast<const uint4*>(h8 + bhi * 32 + 16 * (g & 1))
-                                              : make_uint4(0, 0, 0, 0);
-                    av = (mx::v8i){(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
-                    asc = bown < kb ? (hsq[bown] >> (8 * r)) & 0xFFu : 127u;
-                }
+                const uint4 lo = *reinterpret_cast<const uint4*>(h8 + min(blo, kb - 1) * 32 + 16 * (g & 1));
+                const uint4 hi = *reinterpret_cast<const uint4*>(h8 + min(bhi, kb - 1) * 32 + 16 * (g & 1));
+                const uint32_t c = (hsq[min(bown, kb - 1)] >> (8 * rr)) & 0xFFu;
+                const bool rok = r < kTerms && i < steps;
+                av[i] = cat8(rok && blo < kb ? lo : make_uint4(0, 0, 0, 0), rok && bhi < kb ? hi : make_uint4(0, 0, 0, 0));
+                asc[i] = rok && bown < kb ? c : 127u;
+            }
+            mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < MS; ++i) {
                 // weight scale byte of block g*steps+i from the aligned dwords
+                // (blocks past the row carry zero data, so any scale is fine)
                 const int bi = g * steps + i - sb0;           // 0..10
                 const uint32_t wd = bi < 4 ? bsw[q][0] : (bi < 8 ? bsw[q][1] : bsw[q][2]);
-                acc = mx::mfma16_fp8a_fp4b(av, bq[q][i], acc, asc, (wd >> (8 * (bi & 3))) & 0xFFu);
+                acc = mx::mfma16_fp8a_fp4b(av[i], bq[q][i], acc, asc[i], (wd >> (8 * (bi & 3))) & 0xFFu);
             }
+            mx::pin(acc);
             part = fmaf(wgt[q], acc[0] + acc[1] + acc[2], part);
         }
     }
@@ -481,8 +519,10 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     }
 }
 
-__global__ void reset_workspace_kernel(int* ws, int n) {
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ws[i] = 0;
+__global__ void reset_workspace_kernel(int* ws, int cfg) {
+    for (int i = threadIdx.x; i < kHOff / 4; i += blockDim.x) ws[i] = 0;
+    __syncthreads();
+    if (threadIdx.x == 0) ws[kCfgOff / 4] = cfg;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -491,13 +531,13 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 extern "C" size_t mxfp4_decode_layer_workspace_size(int E, int Mi) {
     if (E <= 0 || Mi <= 0) return 0;
-    return kHOff + align256((size_t)E * kTerms * Mi) + align256((size_t)E * (Mi / 32) * 4);
+    return kHOff + align256((size_t)E * (Mi / 32) * kRecWords * 8);
 }
 
-extern "C" int mxfp4_decode_layer_reset(void* workspace, void* stream) {
+extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream) {
     MXH_REQUIRE(workspace, "decode_layer_reset: null workspace");
     hipLaunchKernelGGL(reset_workspace_kernel, dim3(1), dim3(256), 0, mxh::as_stream(stream),
-                       static_cast<int*>(workspace), kHOff / 4);
+                       static_cast<int*>(workspace), layer_cfg(E, H, Mi));
     return mxh::launch_status("decode_layer_reset");
 }
 
@@ -551,11 +591,10 @@ extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, co
     a.E = E;
     a.H = H;
     a.Mi = Mi;
+    a.cfg = layer_cfg(E, H, Mi);
     a.out = out;
     a.resid = static_cast<uint16_t*>(resid_out);
     a.ws = static_cast<uint8_t*>(workspace);
-    a.hs8 = a.ws + kHOff;
-    a.hsc = reinterpret_cast<uint32_t*>(a.hs8 + align256((size_t)E * kTerms * Mi));
     const int nA = E * (Mi / 32);
     const int nB = H / 16;
     const int steps = (Mi / 32 + 3) / 4;

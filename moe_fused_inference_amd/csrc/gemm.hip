@@ -173,6 +173,10 @@ __global__ __launch_bounds__(256, 2) void gemm_mxfp4_kernel(GemmArgs g) {
         __syncthreads();
     }
 
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
     // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32
 #pragma unroll
     for (int i = 0; i < 2; ++i)

@@ -250,6 +250,7 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(Tab tab, GemvArgs a) 
             acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
         }
 
+        mx::pin(acc);
         // D[4*(l/16)+i][l%16]: token row, weight row
         const int col = n0 + r;
 #pragma unroll

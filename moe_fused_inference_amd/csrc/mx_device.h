@@ -112,6 +112,16 @@ __device__ __forceinline__ v16f mfma32_fp4(uint4 a, uint4 b, v16f c, uint32_t sa
     return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 4, 4, 0, (int)sa, 0, (int)sb);
 }
 
+// Materialises an MFMA result at this point of wave-uniform control flow.
+// An MFMA reads the operands of all 64 lanes, but the compiler models it as a
+// per-lane operation: when only some lanes consume the result (`if (lane <
+// 16) store(acc)`), it may sink the MFMA chain -- and the per-lane selects
+// that build its operands -- into that branch, where the operands of the other
+// lanes are never written.  The empty volatile asm uses and redefines the
+// value, so the chain must complete before any lane-dependent branch.
+__device__ __forceinline__ void pin(v4f& v) { asm volatile("" : "+v"(v)); }
+__device__ __forceinline__ void pin(v16f& v) { asm volatile("" : "+v"(v)); }
+
 // ---------------------------------------------------------------- misc
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 

@@ -53,11 +53,15 @@ class StackedExperts:
                 raise RuntimeError(f"{k} must be a contiguous cuda uint8 tensor of shape {shp}")
 
 
-def workspace(E, Mi, device="cuda"):
-    """Zero-initialised workspace for decode_layer (one per stream)."""
+def workspace(E, Mi, H=2048, device="cuda"):
+    """Workspace for decode_layer launches of shape (E, H, Mi), initialised on
+    the current stream.  Launches sharing it must be stream-ordered."""
     lib = _lib.load()
     n = lib.mxfp4_decode_layer_workspace_size(E, Mi)
-    return torch.zeros(n, dtype=torch.uint8, device=device)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    _lib.check(lib.mxfp4_decode_layer_reset(ws.data_ptr(), E, H, Mi, torch.cuda.current_stream().cuda_stream),
+               "decode_layer_reset")
+    return ws
 
 
 class DecodeLayerCall:
@@ -107,7 +111,7 @@ def decode_layer(x, ids, w, experts, out=None, resid=None, ws=None):
     if out is None:
         out = torch.empty(experts.hidden, dtype=torch.float32, device=x.device)
     if ws is None:
-        ws = workspace(E, experts.inter, x.device)
+        ws = workspace(E, experts.inter, experts.hidden, x.device)
     DecodeLayerCall(x, ids, w, experts, out, resid, ws)()
     return out, resid
 

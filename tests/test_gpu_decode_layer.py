@@ -50,7 +50,7 @@ def test_decode_layer_vs_bf16_oracle(dext, n_exp, E, H, Mi):
     stack = make_stack(dext, n_exp, H, Mi, seed=500 + H)
     g = torch.Generator(device=DEV)
     g.manual_seed(H + Mi)
-    ws = moe_layer.workspace(E, Mi)
+    ws = moe_layer.workspace(E, Mi, H)
     for it in range(3):  # repeated launches on one workspace: counters reset themselves
         x = torch.randn((1, H), generator=g, device=DEV).bfloat16()
         ti, tv = routing(g, n_exp, E)
@@ -73,7 +73,7 @@ def test_device_routing_equals_host_routing(dext):
     g.manual_seed(3)
     x = torch.randn((1, H), generator=g, device=DEV).bfloat16()
     ti, tv = routing(g, n_exp, E)
-    ws = moe_layer.workspace(E, Mi)
+    ws = moe_layer.workspace(E, Mi, H)
     o1, _ = moe_layer.decode_layer(x, ti.tolist(), tv.tolist(), stack, ws=ws)
     o2, _ = moe_layer.decode_layer(x, ti.contiguous(), tv.contiguous(), stack, ws=ws)
     torch.cuda.synchronize()
@@ -90,7 +90,7 @@ def test_graph_replays_match_eager(dext):
     g.manual_seed(5)
     x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
     routes = [routing(g, n_exp, E) for _ in range(4)]
-    ws = moe_layer.workspace(E, Mi)
+    ws = moe_layer.workspace(E, Mi, H)
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=DEV) for _ in range(4)]
     outs = [torch.empty(H, dtype=torch.float32, device=DEV) for _ in range(4)]
     calls = []
