@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec"], default=None,
+    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy"], default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
 
@@ -306,6 +306,31 @@ def cpu_baseline(torch, layer0, routes):
             "cpu_model": cpu_model, "affinity_cores": ncpu}
 
 
+def copy_reference(torch, nbytes=1 << 30, reps=4):
+    """A plain device copy of known size: the yardstick that converts the
+    FETCH_SIZE / WRITE_SIZE counters of a profiling run into HBM bytes."""
+    torch.cuda.set_device(0)
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"copy reference: {reps} x {nbytes} B device-to-device")
+
+
+def read_traffic():
+    """HBM bytes per launch of the fused decode kernel from the committed
+    counter summary (key: value lines), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_layer_traffic.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    return None
+
+
 def only_extra(args, torch, dext, lext, layers, routes, x0):
     """Single measurements for profiling runs."""
     if args.only == "dropin":
@@ -323,10 +348,13 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the multi-GPU "
-              "design is described in DESIGN.md but not run.", file=sys.stderr)
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); the decode layer "
+              "would shard each expert's Mi across GPUs with one all-reduce of the 2048-float output per "
+              "layer, which is designed but not built or run here.", file=sys.stderr)
         sys.exit(2)
     import torch
+    if args.only == "copy":
+        return copy_reference(torch)
     from moe_fused_inference_amd import _lib, get_decode_ext, get_ext
     from moe_fused_inference_amd.moe_layer import layer_status, workspace
     lib = _lib.load()
@@ -374,11 +402,7 @@ def main():
     if args.only == "decode":
         return
 
-    traffic = None
-    tpath = os.path.join(ROOT, "profiles", "decode_layer_traffic.json")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+    traffic = read_traffic()
 
     extra = {}
     if not args.skip_extra:
@@ -421,7 +445,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "kernel": "decode_layer_kernel<false>",
-                     "timing": "HIP events around graph replays; mean over all launches incl. gaps"},
+                     "timing": "HIP events on the launching stream around the timed graph replays / launches; "
+                               "rocprofv3 kernel-trace average of the same kernel agrees (profiles/)"},
         "cpu_baseline": cpu,
     }
     line.update(extra)

@@ -14,10 +14,10 @@
 //   workgroups [0, nA)      gate/up: slot s, 32 intermediate rows j0..j0+31 of
 //                           both gate and up (64 rows x K=H), K split over the
 //                           4 waves; computes h = silu(g)*u in fp32 and
-//                           publishes it, then increments an arrival counter.
+//                           publishes it as generation-tagged words.
 //   workgroups [nA, nA+nB)  down + combine: 16 output columns for all E slots.
-//                           They load their down weights first, then wait on
-//                           the arrival counter (bounded), then run 2 slots per
+//                           They load their down weights first, then poll the
+//                           tagged h words (bounded wait), then run 2 slots per
 //                           wave and combine sum_e w_e*y_e in-workgroup, adding
 //                           the bf16 residual as the reference does.
 //
