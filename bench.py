@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy"], default=None,
+    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy", "prefill"], default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
 
@@ -246,6 +246,65 @@ def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
             "gbs": round(byts / (ms * 1e-3) / 1e9, 1), "bytes": byts}
 
 
+def bench_prefill_moe(torch, lext, lay, T=2048, reps=10, loop_reps=2):
+    """Config 3b: T tokens routed top-8 over the 128 experts of one layer
+    through the grouped path (mxfp4_moe_prefill: route, quantize, gate/up
+    GEMM + SiLU + MXFP4, down GEMM, combine), and the reference's per-expert
+    loop of `forward` calls (runtime/model_runner_v2.py:108-122) on the same
+    kernels library, for comparison."""
+    import torch.nn.functional as F
+    from moe_fused_inference_amd.moe_layer import moe_compute, prefill_workspace
+    g = torch.Generator(device="cuda")
+    g.manual_seed(77)
+    x = torch.randn((T, H), generator=g, device="cuda").bfloat16()
+    logits = torch.randn((T, N_EXP), generator=g, device="cuda")
+    p = torch.softmax(logits.float(), -1)
+    tv, ti = torch.topk(p, TOPK, dim=-1)
+    tv = (tv / tv.sum(-1, keepdim=True)).bfloat16()
+    ws = prefill_workspace(T, TOPK, N_EXP, H, MI)
+    out = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    moe_compute(x, ti, tv, lay, out=out, ws=ws)
+    torch.cuda.synchronize()
+    s_ev, e_ev = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s_ev.record()
+    for _ in range(reps):
+        moe_compute(x, ti, tv, lay, out=out, ws=ws)
+    e_ev.record()
+    torch.cuda.synchronize()
+    ms = s_ev.elapsed_time(e_ev) / reps
+    flops = 2.0 * T * TOPK * (2 * MI * H + H * MI)
+    byts = N_EXP * EXPERT_BYTES + T * H * 2 * 2
+    t_roof = max(flops / (MXFP4_PEAK_TFLOPS * 1e12), byts / (HBM_PEAK_GBS * 1e9))
+
+    def loop():   # the reference's moe_compute on the drop-in `forward`
+        o = torch.zeros_like(x)
+        for e in range(N_EXP):
+            idx, slots = torch.where(ti == e)
+            if idx.numel() == 0:
+                continue
+            xt = x[idx]
+            gg = lext.forward(xt, lay.gate_wp[e], lay.gate_ws[e])
+            uu = lext.forward(xt, lay.up_wp[e], lay.up_ws[e])
+            y = lext.forward(F.silu(gg) * uu, lay.down_wp[e], lay.down_ws[e]).to(o.dtype)
+            o.index_add_(0, idx, y * tv[idx, slots].unsqueeze(-1))
+        return o
+
+    ref_o = loop()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(loop_reps):
+        loop()
+    torch.cuda.synchronize()
+    ms_loop = (time.perf_counter() - t0) * 1e3 / loop_reps
+    rel = float((ref_o.float() - out.float()).abs().max() / ref_o.float().abs().max())
+    return {"tokens": T, "us": round(ms * 1e3, 1), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / MXFP4_PEAK_TFLOPS, 4),
+            "gbs": round(byts / (ms * 1e-3) / 1e9, 1), "roofline_frac": round(t_roof / (ms * 1e-3), 4),
+            "flops": flops, "bytes": byts,
+            "reference_loop_on_forward_us": round(ms_loop * 1e3, 1),
+            "max_rel_vs_reference_loop": round(rel, 5)}
+
+
 # ----------------------------------------------------------------------------- CPU baseline
 def cpu_baseline(torch, layer0, routes):
     """The reference's dequant + BF16 expert path (runtime/model_runner.py:
@@ -340,6 +399,8 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
     elif args.only == "gemm":
         for (M, N, K) in ((512, 1536, 2048), (2048, 2048, 768), (4096, 4096, 2048)):
             log(f"gemm {M}x{N}x{K}: {bench_gemm(torch, lext, dext, M, N, K)}")
+    elif args.only == "prefill":
+        log(f"prefill moe: {bench_prefill_moe(torch, lext, layers[2])}")
     elif args.only == "spec":
         log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
 
@@ -376,7 +437,7 @@ def main():
     ws = workspace(TOPK, MI, H, dev)
     outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    if args.only in ("dropin", "gemm", "spec"):
+    if args.only in ("dropin", "gemm", "spec", "prefill"):
         return only_extra(args, torch, dext, lext, layers, routes, x0)
     graph, calls = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
     log("decode graph captured")
@@ -423,6 +484,9 @@ def main():
         sv = [bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]
         extra["spec_verify_m9"] = sv
         log(f"spec verify: {sv}")
+        pf = bench_prefill_moe(torch, lext, layers[2])
+        extra["prefill_moe_3b"] = pf
+        log(f"prefill moe (config 3b): {pf}")
 
     cpu = None
     if not args.no_cpu:

@@ -170,6 +170,53 @@ int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* 
                            int n_experts, int E, int H, int Mi, float* out, void* resid_out,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------
+ * Token -> expert grouping (the bookkeeping of torch.where(topi == e) in
+ * runtime/model_runner_v2.py:111 and of the token-major tables :279-286).
+ * topi int64 (T, topk) device ids.  Writes counts[e] (pairs routed to e),
+ * offsets[e] (number of valid pairs with a smaller id) and pairs[offsets[e]
+ * + i] = t*topk + k for the i-th such pair in row-major order -- a stable sort
+ * of the pairs by expert id.  Ids outside [0, n_experts) are left out.
+ * counts/offsets hold n_experts ints, pairs T*topk ints; n_experts <= 1024.
+ */
+int mxfp4_moe_group(const int64_t* topi, int T, int topk, int n_experts, int* counts, int* offsets,
+                    int* pairs, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Grouped MoE over a batch of tokens (prefill, speculative verify).
+ * Replaces ModelRunnerV2.moe_compute (runtime/model_runner_v2.py:108-122):
+ * per expert e the rows of torch.where(topi == e) go through `forward` with
+ * gate_e and up_e (activations rounded to fp16, then MXFP4), h = silu(g)*u in
+ * fp32, `forward` with down_e (h rounded to fp16, then MXFP4), .to(bf16),
+ * times the bf16 score, accumulated into a bf16 output.
+ *   x        bf16 (T, H), 16-byte aligned
+ *   topi     int64 (T, topk) expert ids; ids outside [0, n_experts)
+ *            contribute nothing (as an id absent from the reference's
+ *            `experts` dict)
+ *   scores   bf16 (T, topk)
+ *   weights  stacked per layer exactly as for mxfp4_moe_decode_layer
+ *   out      bf16 (T, H), 16-byte aligned: the slots of a token are summed
+ *            in fp32 in slot order and rounded once (the reference adds in
+ *            bf16 in expert order)
+ *   workspace >= mxfp4_moe_prefill_workspace_size(T, topk, n_experts, H, Mi)
+ *            bytes, 256-byte aligned; no state is kept between calls.
+ * Limits: H, Mi multiples of 32; 0 < topk <= 32; n_experts <= 1024.
+ */
+size_t mxfp4_moe_prefill_workspace_size(int T, int topk, int n_experts, int H, int Mi);
+int mxfp4_moe_prefill(const void* x, const int64_t* topi, const uint16_t* scores,
+                      const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                      const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                      int n_experts, int T, int topk, int H, int Mi, void* out, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* As mxfp4_moe_prefill with the experts given by a device table of
+ * n_experts x 6 int64 pointers (gate wp, gate wsc, up wp, up wsc, down wp,
+ * down wsc) -- the per-expert spec dicts of runtime/weight_store.py:278-284.
+ * Every id that can occur must have non-null entries. */
+int mxfp4_moe_prefill_tab(const void* x, const int64_t* topi, const uint16_t* scores,
+                          const int64_t* expert_tab, int n_experts, int T, int topk, int H, int Mi,
+                          void* out, void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -34,6 +34,12 @@ SIGNATURES = {
     "mxfp4_decode_layer_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),
     "mxfp4_moe_decode_layer": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                       _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_moe_group": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
+    "mxfp4_moe_prefill_workspace_size": (_c_sz, [_c_i, _c_i, _c_i, _c_i, _c_i]),
+    "mxfp4_moe_prefill": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                 _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_moe_prefill_tab": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                     _c_p, _c_p, _c_sz, _c_p]),
 }
 
 # Optional exports added by later ABI versions are declared here as they land.

@@ -1,0 +1,579 @@
+// moe_prefill.hip -- grouped MoE for prefill / batched tokens on gfx950.
+//
+// Replaces the per-expert Python loop of ModelRunnerV2.moe_compute
+// (runtime/model_runner_v2.py:108-122):
+//     for e in experts:
+//         idx, slots = torch.where(topi == e)
+//         g = forward(h[idx], gate_e); u = forward(h[idx], up_e)    # x -> half -> MXFP4
+//         y = forward(silu(g) * u, down_e).to(bf16)                 # fp32 h -> half -> MXFP4
+//         out.index_add_(0, idx, y * scores[idx, slots])
+// which issues 3 launches per active expert and syncs on torch.where, with
+// five stream-ordered launches and no host synchronisation:
+//
+//   1. route_kernel       one workgroup per expert: counts of the ids equal
+//                         to / below the expert, then a stable ballot
+//                         compaction of the (token, slot) pairs routed to it
+//                         in row-major order -- exactly torch.where's order.
+//   2. quantize_rows      h (T, H) bf16 -> fp16-rounded -> MXFP4, once per
+//                         token (the per-row quantization does not depend on
+//                         which expert gathers the row).
+//   3. grouped GEMM, gate/up   workgroup (feature tile, expert): for every
+//                         128-token tile of the expert, A = gathered token
+//                         rows, W = 64 gate rows + the same 64 up rows; the
+//                         epilogue computes h = silu(g)*u in fp32, rounds it
+//                         to fp16 (the x.to(half) of the `forward` binding)
+//                         and quantizes it to MXFP4 in registers.
+//   4. grouped GEMM, down      workgroup (output tile, expert): A = the
+//                         expert's quantized h rows; the epilogue writes
+//                         bf16(bf16(y) * score) per (token, slot) pair.
+//   5. combine_kernel     out[t] = bf16(sum over the token's slots, fp32,
+//                         slot order).  Ids outside [0, n_experts) contribute
+//                         nothing, as an id missing from `experts` does in
+//                         the reference.
+//
+// MFMA tiling is that of the lin_pq GEMM (128x128 tiles, K step 256, LDS
+// double buffer, v_mfma_scale_f32_32x32x64_f8f6f4), with the operands
+// swapped: the weight tile is the MFMA's A operand, so each lane ends with
+// one token and 16 features of a 32-feature block.  The 32-block amax of h is
+// then one exchange with lane l^32, and the nibbles pack into 8-byte stores.
+#include <type_traits>
+
+#include "mx_device.h"
+#include "mx_host.h"
+
+namespace mxh {
+int quantize_rows_impl(const void* x, int src_dtype, int round_to_f16, int64_t ldx, int M, int K, int Kp,
+                       uint8_t* q, uint8_t* s, hipStream_t st);
+}
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 256;   // tokens, weight rows, K per step
+constexpr int ROWB = BK / 2;
+constexpr int LDSROW = ROWB + 16;
+constexpr int SCB = BK / 32;
+constexpr int TILE_BYTES = BM * LDSROW;
+constexpr int BUF_BYTES = 2 * TILE_BYTES + 2 * BM * SCB;
+constexpr int kMaxExperts = 1024;
+constexpr int kMaxTopk = 32;
+
+enum { MODE_GATEUP = 0, MODE_DOWN = 1 };
+
+// ------------------------------------------------------------------ routing
+// Workgroup E lists the pairs routed to expert E.  Each wave owns a
+// contiguous quarter of the row-major (token, slot) pairs: a first coalesced
+// pass counts its matches (ballot) and its valid ids below E; the waves
+// exchange the counts once through LDS; a second pass writes the matches in
+// order (ballot rank), so the result is a stable sort by expert id.
+__global__ __launch_bounds__(256) void route_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
+                                                    int* __restrict__ counts, int* __restrict__ offs,
+                                                    int* __restrict__ pairs) {
+    __shared__ int s_eq[4], s_lt[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int E = blockIdx.x;
+    const int per_wave = ((P + 255) / 256) * 64;
+    const int w0 = min(wave * per_wave, P);
+    const int w1 = min(w0 + per_wave, P);
+    constexpr int U = 8;   // chunks of 64 ids in flight per pass step
+    int n_eq = 0, n_lt = 0;
+    for (int b = w0; b < w1; b += 64 * U) {
+        int64_t id[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int p = b + 64 * u + lane;
+            id[u] = p < w1 ? topi[p] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            n_eq += __popcll(__ballot(id[u] == (int64_t)E));
+            n_lt += (id[u] >= 0 && id[u] < (int64_t)E) ? 1 : 0;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) n_lt += __shfl_xor(n_lt, o);
+    if (lane == 0) {
+        s_eq[wave] = n_eq;
+        s_lt[wave] = n_lt;
+    }
+    __syncthreads();
+    const int off = s_lt[0] + s_lt[1] + s_lt[2] + s_lt[3];
+    int pos = off;
+    for (int w = 0; w < wave; ++w) pos += s_eq[w];
+    for (int b = w0; b < w1; b += 64 * U) {
+        int64_t id[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int p = b + 64 * u + lane;
+            id[u] = p < w1 ? topi[p] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const bool m = id[u] == (int64_t)E;
+            const unsigned long long bal = __ballot(m);
+            if (m) pairs[pos + __popcll(bal & ((1ull << lane) - 1ull))] = b + 64 * u + lane;
+            pos += __popcll(bal);
+        }
+    }
+    if (threadIdx.x == 0) {
+        counts[E] = s_eq[0] + s_eq[1] + s_eq[2] + s_eq[3];
+        offs[E] = off;
+    }
+}
+
+// ------------------------------------------------------------------ weights
+struct StackedW {                // expert e of projection j at base[j] + e * stride
+    const uint8_t* wp[3];
+    const uint8_t* ws[3];
+    int64_t wp_stride[3], ws_stride[3];
+    __device__ const uint8_t* p(int e, int j) const { return wp[j] + (int64_t)e * wp_stride[j]; }
+    __device__ const uint8_t* s(int e, int j) const { return ws[j] + (int64_t)e * ws_stride[j]; }
+};
+struct TableW {                  // device table (n_experts, 6) int64: gate wp/ws, up wp/ws, down wp/ws
+    const int64_t* tab;
+    __device__ const uint8_t* p(int e, int j) const { return reinterpret_cast<const uint8_t*>(tab[e * 6 + 2 * j]); }
+    __device__ const uint8_t* s(int e, int j) const { return reinterpret_cast<const uint8_t*>(tab[e * 6 + 2 * j + 1]); }
+};
+
+struct GArgs {
+    const uint8_t* aq;       // GATEUP: token rows (T, H/2); DOWN: sorted h rows (P, Mi/2)
+    const uint8_t* as;       // matching scale rows
+    const int* counts;
+    const int* offs;
+    const int* pairs;
+    int topk;
+    int Kp;                  // K of this GEMM: H (gate/up) or Mi (down)
+    int Nw;                  // weight rows per projection: Mi (gate/up) or H (down)
+    uint8_t* hq;             // GATEUP out: (P, Mi/2) MXFP4 h in sorted order
+    uint8_t* hs;             //             (P, Mi/32)
+    uint16_t* yd;            // DOWN out: (P, H) bf16 at the pair's own index
+    const uint16_t* scores;  // DOWN: (P) bf16 routing weights
+};
+
+struct StageRegs {
+    uint4 a[4];
+    uint4 w[4];
+    uint2 sc;
+};
+
+// One K step: 4 x 16 B of A rows and of W rows per thread, 8 scale bytes of
+// one row (threads 0..127: A row, 128..255: W row).  Row base pointers are
+// resolved once per token tile (gathered tokens, gate/up interleave).
+__device__ __forceinline__ void load_stage(StageRegs& r, const uint8_t* const arow[4], const uint8_t* const wrow[4],
+                                           const uint8_t* srow, int Kp, int k0) {
+    const int tid = threadIdx.x;
+    const int nch = Kp >> 5;
+    const int kb0 = k0 >> 5;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int ch = tid & 7;
+        const bool kok = kb0 + ch < nch;
+        const int off = (k0 >> 1) + ch * 16;
+        r.a[i] = kok ? *reinterpret_cast<const uint4*>(arow[i] + off) : make_uint4(0, 0, 0, 0);
+        r.w[i] = kok ? *reinterpret_cast<const uint4*>(wrow[i] + off) : make_uint4(0, 0, 0, 0);
+    }
+    const uint8_t* sp = srow + kb0;
+    if (kb0 + SCB <= nch && (((uintptr_t)sp) & 7) == 0) {
+        r.sc = *reinterpret_cast<const uint2*>(sp);
+    } else {
+        uint32_t lo = 0, hi = 0;
+#pragma unroll
+        for (int j = 0; j < SCB; ++j) {
+            const uint32_t b = (kb0 + j < nch) ? (uint32_t)sp[j] : 127u;
+            if (j < 4) lo |= b << (8 * j);
+            else hi |= b << (8 * (j - 4));
+        }
+        r.sc = make_uint2(lo, hi);
+    }
+}
+
+__device__ __forceinline__ void store_stage(const StageRegs& r, uint8_t* buf) {
+    const int tid = threadIdx.x;
+    uint8_t* la = buf;
+    uint8_t* lw = buf + TILE_BYTES;
+    uint8_t* lsa = buf + 2 * TILE_BYTES;
+    uint8_t* lsw = lsa + BM * SCB;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int row = (tid >> 3) + 32 * i;
+        const int ch = tid & 7;
+        *reinterpret_cast<uint4*>(la + row * LDSROW + ch * 16) = r.a[i];
+        *reinterpret_cast<uint4*>(lw + row * LDSROW + ch * 16) = r.w[i];
+    }
+    const int row = tid & 127;
+    *reinterpret_cast<uint2*>((tid >= 128 ? lsw : lsa) + row * SCB) = r.sc;
+}
+
+__device__ __forceinline__ uint32_t scale_word(const uint8_t* srow, int h) {
+    const uint2 v = *reinterpret_cast<const uint2*>(srow);
+    return __builtin_amdgcn_perm(v.y, v.x, h ? 0x07050301u : 0x06040200u);
+}
+
+template <int OP>
+__device__ __forceinline__ mx::v16f mfma32(uint4 a, uint4 b, mx::v16f c, uint32_t sa, uint32_t sb) {
+    mx::v8i av = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+    mx::v8i bv = {(int)b.x, (int)b.y, (int)b.z, (int)b.w, 0, 0, 0, 0};
+    return __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(av, bv, c, 4, 4, OP, (int)sa, OP, (int)sb);
+}
+
+// Weight row of tile row rho (0..127).  Gate/up: rows [32b, 32b+32) hold
+// projection b&1 (0 gate, 1 up) of features f0 + 32*(b>>1) + 0..31, so a
+// wave's two 32-row blocks are the gate and up rows of the same features.
+template <int MODE>
+__device__ __forceinline__ int weight_row(int rho, int n0, int& proj) {
+    if (MODE == MODE_GATEUP) {
+        const int b = rho >> 5;
+        proj = b & 1;
+        return n0 + 32 * (b >> 1) + (rho & 31);
+    }
+    proj = 2;
+    return n0 + rho;
+}
+
+template <int MODE, class W>
+__global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GArgs g, W w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int e = blockIdx.y;
+    const int cnt = g.counts[e];
+    if (cnt == 0) return;
+    const int off = g.offs[e];
+    // gate/up: 64 features per workgroup; down: 128 output columns
+    const int n0 = blockIdx.x * (MODE == MODE_GATEUP ? BN / 2 : BN);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31;
+    const int h = lane >> 5;
+    const int cbytes = g.Kp >> 1;
+    const int nch = g.Kp >> 5;
+    const int nsteps = (g.Kp + BK - 1) / BK;
+
+    // weight rows of this thread (fixed for the whole workgroup)
+    const uint8_t* wrow[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        int proj;
+        const int rr = min(weight_row<MODE>((tid >> 3) + 32 * i, n0, proj), g.Nw - 1);
+        wrow[i] = w.p(e, proj) + (int64_t)rr * cbytes;
+    }
+    const uint8_t* wsrow;
+    {
+        int proj;
+        const int rr = min(weight_row<MODE>(tid & 127, n0, proj), g.Nw - 1);
+        wsrow = w.s(e, proj) + (int64_t)rr * nch;
+    }
+
+    for (int mt = 0; mt < cnt; mt += BM) {
+        const int mrows = min(BM, cnt - mt);
+        // token (A) rows of this thread, clamped to the tile's last valid row
+        const uint8_t* arow[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = min((tid >> 3) + 32 * i, mrows - 1);
+            const int src = MODE == MODE_GATEUP ? g.pairs[off + mt + r] / g.topk : off + mt + r;
+            arow[i] = g.aq + (int64_t)src * cbytes;
+        }
+        const uint8_t* srow = wsrow;
+        if (tid < 128) {
+            const int r = min(tid, mrows - 1);
+            const int src = MODE == MODE_GATEUP ? g.pairs[off + mt + r] / g.topk : off + mt + r;
+            srow = g.as + (int64_t)src * nch;
+        }
+
+        mx::v16f acc[2][2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+        StageRegs st;
+        load_stage(st, arow, wrow, srow, g.Kp, 0);
+        store_stage(st, smem);
+        __syncthreads();
+        for (int it = 0; it < nsteps; ++it) {
+            uint8_t* cur = smem + (it & 1) * BUF_BYTES;
+            const bool more = it + 1 < nsteps;
+            if (more) load_stage(st, arow, wrow, srow, g.Kp, (it + 1) * BK);
+            const uint8_t* la = cur;
+            const uint8_t* lw = cur + TILE_BYTES;
+            const uint8_t* lsa = cur + 2 * TILE_BYTES;
+            const uint8_t* lsw = lsa + BM * SCB;
+            uint32_t sa[2], sb[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                sa[i] = scale_word(lsa + (wm * 64 + i * 32 + lr) * SCB, h);
+                sb[i] = scale_word(lsw + (wn * 64 + i * 32 + lr) * SCB, h);
+            }
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                uint4 af[2], bf[2];
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    af[i] = *reinterpret_cast<const uint4*>(la + (wm * 64 + i * 32 + lr) * LDSROW + ks * 32 + h * 16);
+                    bf[i] = *reinterpret_cast<const uint4*>(lw + (wn * 64 + i * 32 + lr) * LDSROW + ks * 32 + h * 16);
+                }
+                // D[weight row][token]: the weight tile is the MFMA A operand
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        if (ks == 0) acc[i][j] = mfma32<0>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 1) acc[i][j] = mfma32<1>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 2) acc[i][j] = mfma32<2>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 3) acc[i][j] = mfma32<3>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
+                    }
+            }
+            if (more) store_stage(st, smem + ((it + 1) & 1) * BUF_BYTES);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
+
+        // acc[i][j] element q of lane l: token wm*64 + 32i + l%32, weight row
+        // wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
+        if (MODE == MODE_GATEUP) {
+            const int fb = n0 + 32 * wn;           // first feature of this wave's 32-block
+            const int Mi = g.Nw;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int rloc = wm * 64 + 32 * i + lr;
+                float v[16];
+                float amax = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    v[q] = mx::round_to_f16(mx::silu_mul(acc[i][0][q], acc[i][1][q]));
+                    amax = fmaxf(amax, fabsf(v[q]));
+                }
+                amax = fmaxf(amax, __shfl_xor(amax, 32));
+                const uint32_t code = mx::e8m0_code(amax);
+                const float inv = mx::e8m0_inv_scale(code);
+                uint32_t piece[4];
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    piece[q4] = 0;
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) piece[q4] |= mx::e2m1_code(v[4 * q4 + r] * inv) << (4 * r);
+                }
+                // lane h holds features 8*q4 + 4h + 0..3 -> bytes 4*q4 + 2h, +1
+                const uint32_t send = h ? (piece[0] | (piece[1] << 16)) : (piece[2] | (piece[3] << 16));
+                const uint32_t recv = __shfl_xor(send, 32);
+                uint2 d;
+                if (h == 0) {
+                    d.x = piece[0] | ((recv & 0xFFFFu) << 16);
+                    d.y = piece[1] | ((recv >> 16) << 16);
+                } else {
+                    d.x = (recv & 0xFFFFu) | (piece[2] << 16);
+                    d.y = (recv >> 16) | (piece[3] << 16);
+                }
+                if (rloc < mrows && fb < Mi) {
+                    const int64_t srow_i = off + mt + rloc;
+                    *reinterpret_cast<uint2*>(g.hq + srow_i * (Mi >> 1) + (fb >> 1) + 8 * h) = d;
+                    if (h == 0) g.hs[srow_i * (Mi >> 5) + (fb >> 5)] = (uint8_t)code;
+                }
+            }
+        } else {
+            const int H = g.Nw;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const int rloc = wm * 64 + 32 * i + lr;
+                if (rloc < mrows) {
+                    const int p = g.pairs[off + mt + rloc];
+                    const float sc = mx::bf16_to_f32(g.scores[p]);
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        const int cb = n0 + wn * 64 + 32 * j;   // 32-column block
+                        if (cb < H) {
+#pragma unroll
+                            for (int q4 = 0; q4 < 4; ++q4) {
+                                uint32_t b[4];
+#pragma unroll
+                                for (int r = 0; r < 4; ++r) {
+                                    const float y = mx::bf16_to_f32(mx::f32_to_bf16_rne(acc[i][j][4 * q4 + r]));
+                                    b[r] = mx::f32_to_bf16_rne(y * sc);
+                                }
+                                const uint2 d = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+                                *reinterpret_cast<uint2*>(g.yd + (int64_t)p * H + cb + 8 * q4 + 4 * h) = d;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+        __syncthreads();   // LDS buffers are refilled by the next token tile
+    }
+}
+
+// out[t, c] = bf16(sum_{k < topk, id valid} yd[t*topk + k, c]); 8 columns per thread
+__global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* __restrict__ yd,
+                                                              const int64_t* __restrict__ topi, int T, int topk,
+                                                              int H, int n_exp, uint16_t* __restrict__ out) {
+    const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int per_row = H >> 3;
+    if (gid >= (int64_t)T * per_row) return;
+    const int t = (int)(gid / per_row);
+    const int c = (int)(gid - (int64_t)t * per_row) * 8;
+    float s[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s[i] = 0.0f;
+    for (int k = 0; k < topk; ++k) {
+        const int64_t id = topi[(int64_t)t * topk + k];
+        if (id < 0 || id >= n_exp) continue;
+        const uint4 v = *reinterpret_cast<const uint4*>(yd + ((int64_t)t * topk + k) * H + c);
+        const uint32_t wv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            s[2 * i] += mx::bf16_to_f32((uint16_t)(wv[i] & 0xFFFFu));
+            s[2 * i + 1] += mx::bf16_to_f32((uint16_t)(wv[i] >> 16));
+        }
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        o[i] = (uint32_t)mx::f32_to_bf16_rne(s[2 * i]) | ((uint32_t)mx::f32_to_bf16_rne(s[2 * i + 1]) << 16);
+    *reinterpret_cast<uint4*>(out + (int64_t)t * H + c) = make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// ------------------------------------------------------------------ host
+struct WsLayout {
+    size_t counts, offs, pairs, xq, xs, hq, hs, yd, total;
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+WsLayout ws_layout(int T, int topk, int n_exp, int H, int Mi) {
+    const size_t P = (size_t)T * topk;
+    WsLayout L;
+    size_t o = 0;
+    L.counts = o; o = align256(o + sizeof(int) * n_exp);
+    L.offs = o;   o = align256(o + sizeof(int) * n_exp);
+    L.pairs = o;  o = align256(o + sizeof(int) * P);
+    L.xq = o;     o = align256(o + (size_t)T * (H / 2));
+    L.xs = o;     o = align256(o + (size_t)T * (H / 32));
+    L.hq = o;     o = align256(o + P * (Mi / 2));
+    L.hs = o;     o = align256(o + P * (Mi / 32));
+    L.yd = o;     o = align256(o + P * H * sizeof(uint16_t));
+    L.total = o;
+    return L;
+}
+
+template <class W>
+int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w, int n_exp, int T, int topk,
+                int H, int Mi, void* out, void* workspace, size_t ws_bytes, hipStream_t st) {
+    MXH_REQUIRE(x && topi && scores && out && workspace, "moe_prefill: null pointer");
+    MXH_REQUIRE(T > 0 && topk > 0 && topk <= kMaxTopk, "moe_prefill: T=%d topk=%d (need T > 0, 0 < topk <= %d)",
+                T, topk, kMaxTopk);
+    MXH_REQUIRE(n_exp > 0 && n_exp <= kMaxExperts, "moe_prefill: n_experts=%d (1..%d)", n_exp, kMaxExperts);
+    MXH_REQUIRE(H > 0 && H % 32 == 0 && Mi > 0 && Mi % 32 == 0,
+                "moe_prefill: H=%d and Mi=%d must be positive multiples of 32", H, Mi);
+    MXH_REQUIRE((int64_t)T * topk < (1ll << 31) / 2, "moe_prefill: T*topk too large");
+    MXH_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
+                "moe_prefill: x/out must be 16-byte and workspace 256-byte aligned");
+    const WsLayout L = ws_layout(T, topk, n_exp, H, Mi);
+    MXH_REQUIRE(ws_bytes >= L.total, "moe_prefill: workspace of %zu bytes < required %zu", ws_bytes, L.total);
+    static bool attr_set[2][2] = {{false, false}, {false, false}};
+    constexpr int tw = std::is_same<W, TableW>::value ? 1 : 0;
+    for (int m = 0; m < 2; ++m) {
+        if (attr_set[tw][m]) continue;
+        const void* fn = m == 0 ? reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_GATEUP, W>)
+                                : reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_DOWN, W>);
+        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * BUF_BYTES);
+        MXH_REQUIRE(e == hipSuccess, "moe_prefill: cannot reserve %d B of LDS: %s", 2 * BUF_BYTES,
+                    hipGetErrorString(e));
+        attr_set[tw][m] = true;
+    }
+    uint8_t* ws = static_cast<uint8_t*>(workspace);
+    int* counts = reinterpret_cast<int*>(ws + L.counts);
+    int* offs = reinterpret_cast<int*>(ws + L.offs);
+    int* pairs = reinterpret_cast<int*>(ws + L.pairs);
+    const int P = T * topk;
+
+    hipLaunchKernelGGL(route_kernel, dim3(n_exp), dim3(256), 0, st, topi, P, n_exp, counts, offs, pairs);
+    int rc = mxh::launch_status("moe_prefill route");
+    if (rc != MXFP4_OK) return rc;
+    rc = mxh::quantize_rows_impl(x, MXFP4_DT_BF16, 1, H, T, H, H, ws + L.xq, ws + L.xs, st);
+    if (rc != MXFP4_OK) return rc;
+
+    GArgs g{};
+    g.counts = counts;
+    g.offs = offs;
+    g.pairs = pairs;
+    g.topk = topk;
+    g.hq = ws + L.hq;
+    g.hs = ws + L.hs;
+    g.yd = reinterpret_cast<uint16_t*>(ws + L.yd);
+    g.scores = scores;
+
+    g.aq = ws + L.xq;
+    g.as = ws + L.xs;
+    g.Kp = H;
+    g.Nw = Mi;
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256), 2 * BUF_BYTES,
+                       st, g, w);
+    rc = mxh::launch_status("moe_prefill gate/up");
+    if (rc != MXFP4_OK) return rc;
+
+    g.aq = ws + L.hq;
+    g.as = ws + L.hs;
+    g.Kp = Mi;
+    g.Nw = H;
+    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256), 2 * BUF_BYTES,
+                       st, g, w);
+    rc = mxh::launch_status("moe_prefill down");
+    if (rc != MXFP4_OK) return rc;
+
+    const int64_t threads = (int64_t)T * (H / 8);
+    hipLaunchKernelGGL(prefill_combine_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                       reinterpret_cast<const uint16_t*>(ws + L.yd), topi, T, topk, H, n_exp,
+                       static_cast<uint16_t*>(out));
+    return mxh::launch_status("moe_prefill combine");
+}
+
+}  // namespace
+
+extern "C" int mxfp4_moe_group(const int64_t* topi, int T, int topk, int n_experts, int* counts, int* offsets,
+                               int* pairs, void* stream) {
+    MXH_REQUIRE(topi && counts && offsets && pairs, "moe_group: null pointer");
+    MXH_REQUIRE(T > 0 && topk > 0 && (int64_t)T * topk < (1ll << 30), "moe_group: T=%d topk=%d", T, topk);
+    MXH_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts, "moe_group: n_experts=%d (1..%d)", n_experts, kMaxExperts);
+    hipLaunchKernelGGL(route_kernel, dim3(n_experts), dim3(256), 0, mxh::as_stream(stream), topi, T * topk, n_experts,
+                       counts, offsets, pairs);
+    return mxh::launch_status("moe_group");
+}
+
+extern "C" size_t mxfp4_moe_prefill_workspace_size(int T, int topk, int n_experts, int H, int Mi) {
+    if (T <= 0 || topk <= 0 || n_experts <= 0 || H <= 0 || Mi <= 0) return 0;
+    return ws_layout(T, topk, n_experts, H, Mi).total;
+}
+
+extern "C" int mxfp4_moe_prefill(const void* x, const int64_t* topi, const uint16_t* scores,
+                                 const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                                 const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                                 int n_experts, int T, int topk, int H, int Mi, void* out, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(gate_wp && gate_ws && up_wp && up_ws && down_wp && down_ws, "moe_prefill: null weight pointer");
+    MXH_REQUIRE(((uintptr_t)gate_wp & 15) == 0 && ((uintptr_t)up_wp & 15) == 0 && ((uintptr_t)down_wp & 15) == 0,
+                "moe_prefill: packed weights must be 16-byte aligned");
+    StackedW w;
+    w.wp[0] = gate_wp; w.ws[0] = gate_ws;
+    w.wp[1] = up_wp;   w.ws[1] = up_ws;
+    w.wp[2] = down_wp; w.ws[2] = down_ws;
+    w.wp_stride[0] = w.wp_stride[1] = (int64_t)Mi * (H / 2);
+    w.ws_stride[0] = w.ws_stride[1] = (int64_t)Mi * (H / 32);
+    w.wp_stride[2] = (int64_t)H * (Mi / 2);
+    w.ws_stride[2] = (int64_t)H * (Mi / 32);
+    return run_prefill(x, topi, scores, w, n_experts, T, topk, H, Mi, out, workspace, workspace_bytes,
+                       mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_prefill_tab(const void* x, const int64_t* topi, const uint16_t* scores,
+                                     const int64_t* expert_tab, int n_experts, int T, int topk, int H, int Mi,
+                                     void* out, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(expert_tab, "moe_prefill_tab: null expert table");
+    TableW w{expert_tab};
+    return run_prefill(x, topi, scores, w, n_experts, T, topk, H, Mi, out, workspace, workspace_bytes,
+                       mxh::as_stream(stream));
+}

@@ -122,3 +122,102 @@ def layer_status(ws):
     flag = ctypes.c_int(0)
     _lib.check(lib.mxfp4_decode_layer_status(ws.data_ptr(), ctypes.byref(flag)), "decode_layer_status")
     return flag.value
+
+
+# ----------------------------------------------------------------------------- batched tokens
+def moe_group(topi, n_experts):
+    """GPU token->expert grouping (mxfp4_moe_group): topi (T, k) int64 ->
+    (counts (n,), offsets (n,), pairs (T*k,)) int32, pairs sorted stably by
+    expert id -- the order torch.where(topi == e) yields per expert
+    (runtime/model_runner_v2.py:111)."""
+    lib = _lib.load()
+    if topi.dim() != 2 or topi.dtype != torch.int64 or not topi.is_cuda:
+        raise RuntimeError("topi must be a 2-D cuda int64 tensor")
+    topi = topi.contiguous()
+    T, k = topi.shape
+    dev = topi.device
+    counts = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    offs = torch.empty(n_experts, dtype=torch.int32, device=dev)
+    pairs = torch.full((T * k,), -1, dtype=torch.int32, device=dev)
+    _lib.check(lib.mxfp4_moe_group(topi.data_ptr(), T, k, n_experts, counts.data_ptr(), offs.data_ptr(),
+                                   pairs.data_ptr(), torch.cuda.current_stream(dev).cuda_stream), "moe_group")
+    return counts, offs, pairs
+
+
+def prefill_workspace(T, topk, n_experts, H, Mi, device="cuda"):
+    """Scratch memory for one moe_compute call of this shape (reusable by
+    stream-ordered calls; nothing persists between calls)."""
+    lib = _lib.load()
+    n = lib.mxfp4_moe_prefill_workspace_size(T, topk, n_experts, H, Mi)
+    if n == 0:
+        raise RuntimeError(f"invalid prefill shape T={T} topk={topk} n_experts={n_experts} H={H} Mi={Mi}")
+    return torch.empty(n, dtype=torch.uint8, device=device)
+
+
+def _expert_table(experts, device):
+    """Reference spec dicts {e: {'gate': {'wp','wsc'}, 'up': ..., 'down': ...}}
+    -> (device table (n, 6) int64, n, H, Mi, present (n,) bool)."""
+    ids = sorted(int(e) for e in experts)
+    n = ids[-1] + 1
+    first = experts[ids[0]]
+    H = int(first["gate"]["wp"].shape[1]) * 2
+    Mi = int(first["gate"]["wp"].shape[0])
+    tab = torch.zeros((n, 6), dtype=torch.int64)
+    present = torch.zeros(n, dtype=torch.bool)
+    for e in ids:
+        spec = experts[e]
+        for j, nm in enumerate(("gate", "up", "down")):
+            wp, wsc = spec[nm]["wp"], spec[nm]["wsc"]
+            want = ((Mi, H // 2), (Mi, H // 32)) if nm != "down" else ((H, Mi // 2), (H, Mi // 32))
+            if (tuple(wp.shape), tuple(wsc.shape)) != want or wp.dtype != torch.uint8 or not wp.is_cuda \
+                    or not wp.is_contiguous() or not wsc.is_contiguous():
+                raise RuntimeError(f"expert {e} {nm}: expected contiguous cuda uint8 {want}")
+            tab[e, 2 * j] = wp.data_ptr()
+            tab[e, 2 * j + 1] = wsc.data_ptr()
+        present[e] = True
+    return tab.to(device), n, H, Mi, present.to(device)
+
+
+def moe_compute(h, topi, scores, experts, out=None, ws=None):
+    """Drop-in counterpart of ModelRunnerV2.moe_compute
+    (runtime/model_runner_v2.py:108-122): h (T, H) bf16, topi (T, k) int64,
+    scores (T, k) (used as bf16, as moe_route returns them), experts either a
+    StackedExperts or the reference's dict of per-expert spec dicts.  Returns
+    the bf16 (T, H) MoE output.  Five launches, no host synchronisation (the
+    dict form builds a small pointer table first)."""
+    lib = _lib.load()
+    if h.dim() != 2 or h.dtype != torch.bfloat16 or not h.is_cuda:
+        raise RuntimeError("h must be a 2-D cuda bfloat16 tensor")
+    if topi.shape != scores.shape or topi.dim() != 2 or topi.shape[0] != h.shape[0]:
+        raise RuntimeError("topi and scores must both be (T, k) with T = h.shape[0]")
+    h = h.contiguous()
+    topi = topi.to(torch.int64).contiguous()
+    sc = scores.to(torch.bfloat16).contiguous()
+    T, k = topi.shape
+    stream = torch.cuda.current_stream(h.device).cuda_stream
+    if isinstance(experts, StackedExperts):
+        experts.check()
+        n, H, Mi = experts.n_experts, experts.hidden, experts.inter
+    else:
+        tab, n, H, Mi, present = _expert_table(experts, h.device)
+        # ids absent from the dict contribute nothing, as in the reference loop
+        ok = (topi >= 0) & (topi < n)
+        topi = torch.where(ok & present[topi.clamp(0, n - 1)], topi, torch.full_like(topi, -1))
+    if h.shape[1] != H:
+        raise RuntimeError(f"h has {h.shape[1]} columns, experts expect H={H}")
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.bfloat16, device=h.device)
+    if ws is None:
+        ws = prefill_workspace(T, k, n, H, Mi, h.device)
+    if isinstance(experts, StackedExperts):
+        rc = lib.mxfp4_moe_prefill(h.data_ptr(), topi.data_ptr(), sc.data_ptr(),
+                                   experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
+                                   experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
+                                   experts.down_wp.data_ptr(), experts.down_ws.data_ptr(),
+                                   n, T, k, H, Mi, out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "moe_prefill")
+    else:
+        rc = lib.mxfp4_moe_prefill_tab(h.data_ptr(), topi.data_ptr(), sc.data_ptr(), tab.data_ptr(), n, T, k, H,
+                                       Mi, out.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "moe_prefill_tab")
+    return out

@@ -13,6 +13,7 @@ Reference operators restated:
   moe_down        src/ext/mxfp4_decode.cu:218-279, binding mxfp4_decode_binding.cpp:123-142
   moe_combine     src/ext/mxfp4_decode.cu:285-299, binding mxfp4_decode_binding.cpp:145-158
   routing         runtime/model_runner_v2.py:100-106,189-192,272-275
+  moe_compute     runtime/model_runner_v2.py:108-122 (prefill / batched grouped MoE)
   token-major tables  runtime/model_runner_v2.py:197-206,279-286
   dequant+BF16 layer  runtime/model_runner.py:99-132 (the CPU baseline)
 """
@@ -203,6 +204,77 @@ def decode_layer_ref(x, topi, topv, experts):
             acc = topv[m, s] * y if acc is None else acc + topv[m, s] * y
         rows.append(acc)
     return np.stack(rows)
+
+
+def moe_prefill_ref(x, topi, scores, experts, bf16_steps=True, ambiguous=None):
+    """ModelRunnerV2.moe_compute (runtime/model_runner_v2.py:108-122) on the
+    operands the op consumes, float64 accumulation:
+      for e in sorted(experts): idx, slots = where(topi == e)           (:111)
+        g, u = forward(x[idx], gate_e / up_e)   x -> fp16 -> MXFP4      (:116-117)
+        hh = silu(g) * u  (fp32)  -> forward(hh, down_e): fp16 -> MXFP4  (:118-119)
+        y = bf16(y); out[idx] += bf16(y * bf16(score))                  (:119-120)
+    experts: {e: ((gate_wp, gate_ws), (up_wp, up_ws), (down_wp, down_ws))}.
+    Ids absent from `experts` contribute nothing.  With bf16_steps the two
+    bf16 roundings of y and y*score are applied; the sum over slots is kept in
+    float64 (the reference's bf16 index_add_ order is not restated: parity of
+    that last rounding is by tolerance).  Returns float64 (T, H).
+
+    If `ambiguous` is a boolean array of shape (T,), tokens are flagged in it
+    whose MXFP4 h quantization is not robust: h * (1 +- 1e-5) quantizes to
+    other codes or scales than h.  Any fp32 implementation (the reference's
+    included) may legitimately round such an h the other way."""
+    x = np.asarray(x, np.float32)
+    topi = np.asarray(topi, np.int64)
+    scores = fmt.bf16_round(np.asarray(scores, np.float32))
+    T, H = x.shape
+    out = np.zeros((T, H), np.float64)
+    xq, xs = forward_act_quant_ref(x, H)
+    xd = fmt.dequant_rows(xq, xs).astype(np.float64)
+    for e in sorted(experts):
+        idx, slots = np.nonzero(topi == e)
+        if idx.size == 0:
+            continue
+        (gwp, gws), (uwp, uws), (dwp, dws) = experts[e]
+        g = (xd[idx] @ fmt.dequant_rows(gwp, gws).astype(np.float64).T).astype(np.float32)
+        u = (xd[idx] @ fmt.dequant_rows(uwp, uws).astype(np.float64).T).astype(np.float32)
+        hh = silu_mul_f32(g, u)
+        hq, hs = forward_act_quant_ref(hh, dwp.shape[1] * 2)
+        if ambiguous is not None:
+            for f in (1.0 + 1e-5, 1.0 - 1e-5):
+                q2, s2 = forward_act_quant_ref(hh * np.float32(f), dwp.shape[1] * 2)
+                bad = np.any(q2 != hq, axis=1) | np.any(s2 != hs, axis=1)
+                ambiguous[idx[bad]] = True
+        y = fmt.dequant_rows(hq, hs).astype(np.float64) @ fmt.dequant_rows(dwp, dws).astype(np.float64).T
+        s = scores[idx, slots].astype(np.float64)[:, None]
+        if bf16_steps:
+            contrib = fmt.bf16_round((fmt.bf16_round(y).astype(np.float64) * s).astype(np.float32))
+        else:
+            contrib = y * s
+        np.add.at(out, idx, contrib.astype(np.float64))
+    return out
+
+
+def moe_prefill_tokenwise_ref(x, topi, scores, experts):
+    """The same operator restated token by token (no grouping): for each
+    token t and slot k, y = forward(h(x_t)) with expert topi[t, k], summed
+    over k.  An independent loop structure to pin moe_prefill_ref's
+    idx/slot bookkeeping."""
+    x = np.asarray(x, np.float32)
+    topi = np.asarray(topi, np.int64)
+    scores = fmt.bf16_round(np.asarray(scores, np.float32))
+    T, H = x.shape
+    out = np.zeros((T, H), np.float64)
+    for t in range(T):
+        for k in range(topi.shape[1]):
+            e = int(topi[t, k])
+            if e not in experts:
+                continue
+            (gwp, gws), (uwp, uws), (dwp, dws) = experts[e]
+            g = forward_ref(x[t:t + 1], gwp, gws).astype(np.float32)
+            u = forward_ref(x[t:t + 1], uwp, uws).astype(np.float32)
+            y = forward_ref(silu_mul_f32(g, u), dwp, dws)[0]
+            out[t] += fmt.bf16_round((fmt.bf16_round(y).astype(np.float64) * scores[t, k]).astype(np.float32))
+    return out
 
 
 def dequant_bf16_moe_layer_torch(x, topi, topv, experts_deq_bf16=None, experts=None):

@@ -185,3 +185,50 @@ def test_cpu_baseline_close_to_fp32_oracle(M):
     ref = ops.decode_layer_ref(x, topi, topv, experts)
     got = ops.dequant_bf16_moe_layer_torch(torch.from_numpy(x).bfloat16(), topi, topv, experts=experts)
     assert ops.cos_sim(got.float().numpy(), ref) > 0.995
+
+
+def _rand_experts(rng, ids, H, Mi):
+    ex = {}
+    for e in ids:
+        parts = []
+        for n, k in ((Mi, H), (Mi, H), (H, Mi)):
+            parts.append(fmt.quantize_rows((rng.standard_normal((n, k)) * 0.05).astype(np.float32)))
+        ex[e] = tuple(parts)
+    return ex
+
+
+@pytest.mark.parametrize("skew", [False, True])
+def test_moe_prefill_ref_matches_tokenwise_loop(skew):
+    """Grouped restatement of moe_compute (where(topi == e) per expert) equals
+    an independent token-by-token restatement, including ids that are absent
+    from the expert dict (contribute nothing) and a skewed routing."""
+    rng = np.random.default_rng(11 if skew else 12)
+    T, k, n, H, Mi = 9, 3, 6, 64, 64
+    experts = _rand_experts(rng, [0, 1, 2, 4, 5], H, Mi)        # expert 3 absent
+    x = fmt.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    if skew:
+        topi = np.stack([rng.permutation(n)[:k] for _ in range(T)])
+        topi[:, 0] = 1                                            # every token hits expert 1
+    else:
+        topi = np.stack([rng.permutation(n)[:k] for _ in range(T)])
+    scores = rng.random((T, k)).astype(np.float32)
+    a = ops.moe_prefill_ref(x, topi, scores, experts)
+    b = ops.moe_prefill_tokenwise_ref(x, topi, scores, experts)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-9)
+    assert np.any(topi == 3)                                      # the absent id really occurs
+
+
+def test_moe_prefill_ref_single_expert_weight_one_is_forward_chain():
+    """One slot, one expert, score 1: the output is bf16 of the plain
+    forward -> silu*mul -> forward chain of the reference operators."""
+    rng = np.random.default_rng(5)
+    T, H, Mi = 4, 64, 96
+    experts = _rand_experts(rng, [0], H, Mi)
+    x = fmt.bf16_round(rng.standard_normal((T, H)).astype(np.float32))
+    topi = np.zeros((T, 1), np.int64)
+    out = ops.moe_prefill_ref(x, topi, np.ones((T, 1), np.float32), experts)
+    (gwp, gws), (uwp, uws), (dwp, dws) = experts[0]
+    g = ops.forward_ref(x, gwp, gws).astype(np.float32)
+    u = ops.forward_ref(x, uwp, uws).astype(np.float32)
+    y = ops.forward_ref(ops.silu_mul_f32(g, u), dwp, dws)
+    np.testing.assert_array_equal(out, fmt.bf16_round(fmt.bf16_round(y)).astype(np.float64))
