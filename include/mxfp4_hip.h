@@ -150,14 +150,17 @@ int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
  *   out        fp32 (H): sum_e w_e * down_e(silu(gate_e x) * up_e x)
  *   resid_out  optional bf16 (H): bf16(x + bf16(out)), or NULL
  *   workspace  device memory of mxfp4_decode_layer_workspace_size(E, Mi)
- *              bytes, 256-byte aligned, initialised by
- *              mxfp4_decode_layer_reset(workspace, E, H, Mi) for the (E, H, Mi)
- *              every launch on it must use; launches sharing a workspace must
- *              be stream-ordered (a launch with another shape sets the error
- *              flag instead of waiting).
+ *              bytes (~53 KB at E=8, Mi=768), 256-byte aligned, initialised
+ *              once by mxfp4_decode_layer_reset(workspace, E, H, Mi); every
+ *              launch leaves it ready for the next one, so it needs no reset
+ *              between launches or HIP graph replays.  Every launch on it
+ *              must use that (E, H, Mi) (a launch with another shape sets the
+ *              error flag instead of waiting); launches sharing a workspace
+ *              must be stream-ordered.
  * Limits: E <= 8, H a multiple of 512 up to 2048, Mi a multiple of 32 up to
  * 1024.  Returns MXFP4_OK or an error; a bounded internal wait that expired
- * (or a workspace/shape mismatch) is reported by mxfp4_decode_layer_status.
+ * is reported by mxfp4_decode_layer_status (the flag stays set; reset the
+ * workspace before launching on it again).
  */
 size_t mxfp4_decode_layer_workspace_size(int E, int Mi);
 int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream);

@@ -14,10 +14,10 @@
 //   workgroups [0, nA)      gate/up: slot s, 32 intermediate rows j0..j0+31 of
 //                           both gate and up (64 rows x K=H), K split over the
 //                           4 waves; computes h = silu(g)*u in fp32 and
-//                           publishes it as generation-tagged words.
+//                           publishes it (three E4M3 terms per value).
 //   workgroups [nA, nA+nB)  down + combine: 16 output columns for all E slots.
-//                           They load their down weights first, then poll the
-//                           tagged h words (bounded wait), then run 2 slots per
+//                           They load their down weights first, then wait for
+//                           all of h (bounded), stage it in LDS, run 2 slots per
 //                           wave and combine sum_e w_e*y_e in-workgroup, adding
 //                           the bf16 residual as the reference does.
 //
@@ -25,25 +25,26 @@
 // gate/up workgroup is resident or finished before any down workgroup waits:
 // the wait cannot deadlock.  It is still bounded (kSpinLimit polls); on expiry
 // the kernel sets an error flag, skips its work and exits normally.
-//   * h travels as tagged 64-bit words: 32 bits of payload (E4M3 bytes or the
-//     3 scale codes of a 32-block) and a 32-bit generation tag, written with
+//   * h travels as 32-bit words (4 E4M3 bytes of one term, or the 3 scale
+//     codes of a 32-block), 25 per (slot, 32-row block) record.  A word is
+//     its own flag: between uses it holds the "empty" pattern 0x7FBADBAD,
+//     whose top byte is the E4M3 NaN code that the split of a finite h never
+//     produces (and a codes word has a zero top byte).  Producers store with
 //     agent-scope atomic stores (write-through to the device coherence
-//     point).  A down workgroup polls the very words it needs until every tag
-//     equals the current generation -- the data is the flag, so there is no
-//     store drain, no counter and no extra round trip between "ready" and
-//     "read".  (A release/acquire fence pair would instead write back and
-//     invalidate a whole L2 per workgroup.)
-//   * The generation is the number of launches on the workspace: every
-//     workgroup keeps its own count ("memo") in the workspace, reads it at
-//     start and stores count+1 at the end, so all counts advance together
-//     with no reset between launches or graph replays.  This requires every
-//     launch on a workspace to use the same (E, H, Mi); the workspace header
-//     records them (mxfp4_decode_layer_reset) and a mismatching launch sets
-//     the error flag instead of waiting.
-//   * Within one launch every h word is written once before it is consumed,
-//     and each launch starts with the dispatch-level cache invalidation, so
-//     no reader can hold a stale copy; a word from the previous launch
-//     carries the previous generation and is simply polled again.
+//     point); consumers poll with agent-scope atomic loads, first one word
+//     per thread (a probe that keeps polling traffic low while the weights
+//     stream), then the rest.  (A release/acquire fence pair would instead
+//     write back and invalidate a whole L2 per workgroup.)
+//   * Every consumer reads every word, so no consumer can empty them; instead
+//     there are two buffers, used by alternate launches.  Each workgroup
+//     keeps its own launch count ("memo") in the workspace, reads it at start
+//     and stores count+1 at the end, so all workgroups agree on the parity.
+//     A producer writes its record into buffer (count & 1) and empties its
+//     record in the other buffer, which no workgroup of this launch reads
+//     and the next launch will use.  No reset is needed between launches or
+//     graph replays.  All launches on a workspace must use the same (E, H,
+//     Mi): the workspace header records them (mxfp4_decode_layer_reset) and
+//     a mismatching launch sets the error flag instead of waiting.
 //
 // Registers are kept near 128 VGPRs (h is staged through LDS, the down
 // K-step count is a template bound) so that every workgroup of a layer is
@@ -66,14 +67,16 @@ namespace {
 constexpr int kSpinLimit = 1 << 22;   // polls of one word (~0.2 s)
 constexpr int kTerms = 3;             // E4M3 terms per activation value
 constexpr int kMaxE = 8;
-constexpr int kRecWords = 25;         // tagged words per (slot, 32-block) record of h:
-                                      // 24 x 4 E4M3 bytes (3 terms x 32) + 1 word of scale codes
+constexpr int kRecWords = 32;         // words per (slot, 32-block) record of h: one per value,
+                                      // bytes 0..2 = its E4M3 terms, byte 3 of words 0..2 = the terms' codes
+constexpr uint32_t kEmpty = 0xBADBAD7Fu;  // "no value yet": byte 0 is the E4M3 NaN code, which the term-0
+                                          // byte of a finite value never is
 // workspace layout (bytes)
 constexpr int kCfgOff = 0;            // int32 config word written by reset
 constexpr int kErrOff = 256;          // int32 error flag
-constexpr int kMemoAOff = 1024;       // int32 generation of gate/up workgroup (s, jb): [8][32]
-constexpr int kMemoBOff = 2048;       // int32 generation of down workgroup cb: [128]
-constexpr int kHOff = 4096;           // h records: (E, Mi/32, kRecWords) uint64
+constexpr int kMemoAOff = 1024;       // int32 launch count of gate/up workgroup (s, jb): [8][32]
+constexpr int kMemoBOff = 2048;       // int32 launch count of down workgroup cb: [128]
+constexpr int kHOff = 4096;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -91,6 +94,7 @@ struct LayerArgs {
     float w[kMaxE];           // by-value weights when w_dev is null
     int E, H, Mi;
     int cfg;                  // expected workspace config word
+    int bufwords;             // uint32 words between the two h buffers
     float* out;               // (H) fp32 moe output
     uint16_t* resid;          // (H) bf16 x + bf16(out), or null
     uint8_t* ws;              // workspace base
@@ -124,6 +128,14 @@ __device__ __forceinline__ float e8m0_value(uint32_t code) {
     return code > 0u ? __uint_as_float(code << 23) : __uint_as_float(0x00400000u);
 }
 
+// max over the 4 lanes of a quad (DPP quad permutes: no LDS round trip)
+__device__ __forceinline__ float quad_max(float v) {
+    const float a = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // xor 1
+    v = fmaxf(v, a);
+    const float b = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // xor 2
+    return fmaxf(v, b);
+}
+
 // Splits 8 consecutive values of a 32-block (4 lanes per block, lane quad
 // aligned) into kTerms E4M3 terms: word8[t] receives the 8 E4M3 bytes of term
 // t and codes (byte t) the term's E8M0 scale code.  Each term is the E4M3
@@ -136,8 +148,7 @@ __device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint3
         float am = 0.0f;
 #pragma unroll
         for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
-        am = fmaxf(am, __shfl_xor(am, 1));
-        am = fmaxf(am, __shfl_xor(am, 2));
+        am = quad_max(am);
         const uint32_t code = e4m3_block_code(am);
         const float sc = e8m0_value(code);
         uint32_t word[2];
@@ -158,6 +169,39 @@ __device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint3
         word8[t] = (uint64_t)word[0] | ((uint64_t)word[1] << 32);
         codes |= code << (8 * t);
     }
+}
+
+// max over lanes 0..15 and over 16..31 (each row of 16 lanes), then of both
+// rows, for a value held by lanes 0..31: DPP within rows, readlane across.
+__device__ __forceinline__ float max32(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad xor 1
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad xor 2
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // row half-mirror
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row mirror
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)));
+}
+
+// Splits a 32-block held one value per lane (lanes 0..31) into kTerms E4M3
+// terms, as split8 does: returns the lane's term bytes (byte t = term t) and
+// the block's codes (byte t = E8M0 code of term t, the same in every lane).
+__device__ __forceinline__ uint32_t split32(float v, uint32_t& codes) {
+    uint32_t bytes = 0;
+    codes = 0;
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+        const uint32_t code = e4m3_block_code(max32(__builtin_fabsf(v)));
+        const float sc = e8m0_value(code);
+        mx::v2s p = {0, 0};
+        p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v, 0.0f, sc, false);
+        const uint32_t b = (uint32_t)(uint16_t)p[0] & 0xFFu;
+        typedef float v2f __attribute__((ext_vector_type(2)));
+        const v2f d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(b, sc, false);
+        v -= d[0];
+        bytes |= b << (8 * t);
+        codes |= code << (8 * t);
+    }
+    return bytes;
 }
 
 // Expert id / weight of slot s from the by-value arrays with a uniform index
@@ -195,12 +239,15 @@ __device__ __forceinline__ void set_error(const LayerArgs& a) {
 
 union Smem {
     struct {                                       // gate/up workgroups
+        uint4 zero[2];                             // operand source of the zero rows / steps
         uint8_t x8[kTerms][2048];                  // E4M3 terms of x (H <= 2048)
         uint8_t xsc[kTerms][64];
         float red[4][4][16];
         float h[2][32];
     } a;
     struct {                                       // down workgroups
+        uint4 zero[2];                             // operand source of the zero rows / blocks
+        uint32_t code127[4];                       // [0]: scale source of the zero rows / blocks (h8 stays 16-B aligned)
         uint8_t h8[kMaxE * kTerms * 1024];         // E4M3 terms of h, [slot][term][Mi]
         uint32_t hsc[kMaxE * 32];                  // [slot][32-block]: codes of terms 0..2
         float red[4][16];
@@ -220,7 +267,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int nblk_mi = a.Mi >> 5;
     const int nA = a.E * nblk_mi;
     const int bid = blockIdx.x;
-    uint64_t* hrec = reinterpret_cast<uint64_t*>(a.ws + kHOff);
+    uint32_t* hbuf = reinterpret_cast<uint32_t*>(a.ws + kHOff);
 
     if (bid < nA) {
         // ================================================= gate / up
@@ -238,7 +285,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         if (k0 < H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
         int* memo = reinterpret_cast<int*>(a.ws + kMemoAOff) + s * 32 + jb;
         const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
-        const int gen = *memo + 1;
+        const int launch = *memo;
 
         const int e = DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[s]) : pick_id(a, s);
         const uint8_t* gw = a.gate_wp + (int64_t)e * a.wp_stride_gu;
@@ -287,20 +334,25 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 if ((threadIdx.x & 3) == 0) sm.a.xsc[t][k0 >> 5] = (uint8_t)(codes >> (8 * t));
             }
         }
+        if (threadIdx.x < 2) sm.a.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
         __syncthreads();
 
         // MFMA: step i covers blocks {bpw*wave + sa*gb + i : gb = 0..3}.
-        // Operands first (clamped unconditional LDS reads), then the MFMAs.
+        // Operands first, then the MFMAs.  A zero operand is read from the
+        // zero region (an address select), not selected after the read: a
+        // value select compiles to branches that serialise the LDS reads.
         mx::v8i av[4];
         uint32_t asc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int base = bpw * wave + min(i, sa - 1);
-            const mx::v8i v = cat8(*reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (g >> 1)) * 32 + 16 * (g & 1)]),
-                                   *reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (2 + (g >> 1))) * 32 + 16 * (g & 1)]));
-            const uint32_t c = sm.a.xsc[rr][base + sa * g];
             const bool ok = r < kTerms && i < sa;
-            av[i] = ok ? v : (mx::v8i){0, 0, 0, 0, 0, 0, 0, 0};
+            const uint4* plo = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (g >> 1)) * 32 + 16 * (g & 1)])
+                                  : &sm.a.zero[0];
+            const uint4* phi = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (2 + (g >> 1))) * 32 + 16 * (g & 1)])
+                                  : &sm.a.zero[1];
+            av[i] = cat8(*plo, *phi);
+            const uint32_t c = sm.a.xsc[rr][base + sa * g];
             asc[i] = ok ? c : 127u;
         }
         mx::v4f acc[4];
@@ -319,41 +371,29 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             for (int G = 0; G < 4; ++G) sm.a.red[wave][G][lane] = acc[G][0] + acc[G][1] + acc[G][2];
         }
         __syncthreads();
-        // h = silu(g) * u for the 32 rows (lanes 0..31 of wave 0), split into
-        // E4M3 terms by lane quads 0..3, published as tagged words by lanes 0..24
+        // h = silu(g) * u for the 32 rows, one per lane of wave 0, split into
+        // E4M3 terms and published as one word per value
         if (wave == 0) {
-            float v[8];
+            const int j = lane & 31;
+            float gsum = 0.f, usum = 0.f;
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const int j = (lane & 3) * 8 + i;
-                float gsum = 0.f, usum = 0.f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    gsum += sm.a.red[w][j >> 4][j & 15];
-                    usum += sm.a.red[w][2 + (j >> 4)][j & 15];
-                }
-                v[i] = mx::silu_mul(gsum, usum);
+            for (int w = 0; w < 4; ++w) {
+                gsum += sm.a.red[w][j >> 4][j & 15];
+                usum += sm.a.red[w][2 + (j >> 4)][j & 15];
             }
-            uint64_t w8[kTerms];
             uint32_t codes;
-            split8(v, w8, codes);  // lanes 0..3 hold the block (lanes 4.. repeat it)
-            // word w < 24: term w/8, bytes 4*(w%8).. of the 32-byte term block,
-            // held by lane (w%8)/2 in half (w%2) of its 8 bytes; word 24: codes
-            const int wi = lane;
-            const int src = (wi % 8) >> 1;
-            const int t = wi >> 3;
-            const uint64_t s0 = __shfl(w8[0], src), s1 = __shfl(w8[1], src), s2 = __shfl(w8[2], src);
-            const uint64_t sel = (t == 0) ? s0 : ((t == 1) ? s1 : s2);
-            const uint32_t codes0 = __shfl(codes, 0);
-            uint32_t payload = (wi & 1) ? (uint32_t)(sel >> 32) : (uint32_t)sel;
-            payload = (wi == 24) ? codes0 : payload;
+            const uint32_t bytes = split32(mx::silu_mul(gsum, usum), codes);
+            const uint32_t word = bytes | (j < kTerms ? ((codes >> (8 * j)) & 0xFFu) << 24 : 0u);
             const bool cfg_ok = cfg == a.cfg;
-            if (wi < kRecWords && cfg_ok)
-                __hip_atomic_store(hrec + ((int64_t)s * nblk_mi + jb) * kRecWords + wi,
-                                   (uint64_t)payload | ((uint64_t)(uint32_t)gen << 32), __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            const int64_t w_off = ((int64_t)s * nblk_mi + jb) * kRecWords + j;
+            uint32_t* cur = hbuf + (launch & 1) * a.bufwords;
+            uint32_t* nxt = hbuf + ((launch & 1) ^ 1) * a.bufwords;
+            if (lane < 32 && cfg_ok) {
+                __hip_atomic_store(cur + w_off, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(nxt + w_off, kEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
             if (lane == 0) {
-                *memo = gen;
+                *memo = launch + 1;
                 if (!cfg_ok) set_error(a);
             }
         }
@@ -368,7 +408,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int steps = (kb + 3) >> 2; // MFMA K-steps (6), <= MS
     int* memo = reinterpret_cast<int*>(a.ws + kMemoBOff) + cb;
     const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
-    const int gen = *memo + 1;
+    const int launch = *memo;
     // wave handles slots 2*wave, 2*wave+1; lane group g owns blocks
     // g*steps .. g*steps+steps-1 of its row
     int slot[2], eid[2];
@@ -412,59 +452,76 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         }
     }
 
-    // poll the tagged h words of all slots until they carry this launch's
-    // generation, then stage them in LDS (thread t owns words t, t+256, ...)
+    // poll this launch's h words of all slots until none is empty (one probe
+    // word first, then every round reloads all of this thread's words: a
+    // conditional reload compiles to one wait per word), then unpack the term
+    // bytes and codes into LDS.  Thread t owns words 2048k + 8t .. +7 (values
+    // 8*(t%4).. of one 32-block).
     const int nwords = a.E * nblk_mi * kRecWords;
     const bool cfg_ok = cfg == a.cfg;
-    constexpr int kPer = (kMaxE * 4 * MS * kRecWords + 255) / 256;  // max words per thread
-    uint64_t wv[kPer];
+    constexpr int kGroups = (kMaxE * 4 * MS * kRecWords) / 2048;  // groups of 8 words per thread
+    const uint32_t* cur = hbuf + (launch & 1) * a.bufwords;
+    uint32_t wv[kGroups][8];
     bool ok = cfg_ok;
     if (cfg_ok) {
-#pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int wi = threadIdx.x + 256 * k;
-            wv[k] = __hip_atomic_load(hrec + min(wi, nwords - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
         int spins = 0;
-        while (true) {
+        const int w0 = min(8 * (int)threadIdx.x, nwords - 1);
+        uint32_t probe = __hip_atomic_load(cur + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        while (probe == kEmpty) {
+            if (++spins >= kSpinLimit) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(4);
+            probe = __hip_atomic_load(cur + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        while (ok) {
+#pragma unroll
+            for (int k = 0; k < kGroups; ++k)
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                    wv[k][i] = __hip_atomic_load(cur + min(2048 * k + 8 * (int)threadIdx.x + i, nwords - 1),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             bool pending = false;
 #pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int wi = threadIdx.x + 256 * k;
-                pending |= (wi < nwords) && ((uint32_t)(wv[k] >> 32) != (uint32_t)gen);
-            }
+            for (int k = 0; k < kGroups; ++k)
+#pragma unroll
+                for (int i = 0; i < 8; ++i) pending |= wv[k][i] == kEmpty;
             if (!pending) break;
             if (++spins >= kSpinLimit) {
                 ok = false;
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
-#pragma unroll
-            for (int k = 0; k < kPer; ++k) {
-                const int wi = threadIdx.x + 256 * k;
-                if (wi < nwords && (uint32_t)(wv[k] >> 32) != (uint32_t)gen)
-                    wv[k] = __hip_atomic_load(hrec + wi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
         }
-        // word wi of record (slot, block) -> LDS: term bytes or the codes word
+    }
+    if (ok) {
 #pragma unroll
-        for (int k = 0; k < kPer; ++k) {
-            const int wi = threadIdx.x + 256 * k;
+        for (int k = 0; k < kGroups; ++k) {
+            const int wi = 2048 * k + 8 * (int)threadIdx.x;   // first word; quads never straddle nwords
             if (wi < nwords) {
                 const int rec = wi / kRecWords;
-                const int w = wi - rec * kRecWords;
                 const int sl = rec / nblk_mi;
                 const int blk = rec - sl * nblk_mi;
-                const uint32_t payload = (uint32_t)wv[k];
-                if (w < 24)
-                    *reinterpret_cast<uint32_t*>(sm.b.h8 + (sl * kTerms + (w >> 3)) * Mi + blk * 32 + (w & 7) * 4) = payload;
-                else
-                    sm.b.hsc[sl * 32 + blk] = payload;
+#pragma unroll
+                for (int t = 0; t < kTerms; ++t) {
+                    // byte t of words i = 0..7 -> 8 consecutive E4M3 bytes of term t
+                    const uint32_t sel = 0x0C0C0000u | ((4u + t) << 8) | (uint32_t)t;
+                    const uint32_t lo = __builtin_amdgcn_perm(wv[k][1], wv[k][0], sel) |
+                                        (__builtin_amdgcn_perm(wv[k][3], wv[k][2], sel) << 16);
+                    const uint32_t hi = __builtin_amdgcn_perm(wv[k][5], wv[k][4], sel) |
+                                        (__builtin_amdgcn_perm(wv[k][7], wv[k][6], sel) << 16);
+                    *reinterpret_cast<uint64_t*>(sm.b.h8 + (sl * kTerms + t) * Mi + blk * 32 + 8 * (threadIdx.x & 3)) =
+                        (uint64_t)lo | ((uint64_t)hi << 32);
+                }
+                if ((threadIdx.x & 3) == 0)
+                    sm.b.hsc[sl * 32 + blk] = (wv[k][0] >> 24) | ((wv[k][1] >> 24) << 8) | ((wv[k][2] >> 24) << 16);
             }
         }
     }
     if (!ok) set_error(a);
-    if (threadIdx.x == 0) *memo = gen;
+    if (threadIdx.x < 2) sm.b.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
+    if (threadIdx.x == 2) sm.b.code127[0] = 0x7F7F7F7Fu;
     const bool abort = __syncthreads_or(!ok);
 
     float part = 0.0f;  // this lane's (lane < 16) partial combine over its slots
@@ -475,7 +532,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             if (slot[q] >= a.E) continue;
             const uint8_t* h8 = sm.b.h8 + (slot[q] * kTerms + rr) * Mi;
             const uint32_t* hsq = sm.b.hsc + slot[q] * 32;
-            // operands of all steps first (clamped unconditional LDS reads)
+            // operands of all steps first; zero operands come from the zero
+            // region (an address select, no branch between the LDS reads)
             mx::v8i av[MS];
             uint32_t asc[MS];
 #pragma unroll
@@ -484,12 +542,14 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 const int blo = (g >> 1) * steps + i;
                 const int bhi = (2 + (g >> 1)) * steps + i;
                 const int bown = g * steps + i;
-                const uint4 lo = *reinterpret_cast<const uint4*>(h8 + min(blo, kb - 1) * 32 + 16 * (g & 1));
-                const uint4 hi = *reinterpret_cast<const uint4*>(h8 + min(bhi, kb - 1) * 32 + 16 * (g & 1));
-                const uint32_t c = (hsq[min(bown, kb - 1)] >> (8 * rr)) & 0xFFu;
                 const bool rok = r < kTerms && i < steps;
-                av[i] = cat8(rok && blo < kb ? lo : make_uint4(0, 0, 0, 0), rok && bhi < kb ? hi : make_uint4(0, 0, 0, 0));
-                asc[i] = rok && bown < kb ? c : 127u;
+                const uint4* plo = (rok && blo < kb) ? reinterpret_cast<const uint4*>(h8 + blo * 32 + 16 * (g & 1))
+                                                     : &sm.b.zero[0];
+                const uint4* phi = (rok && bhi < kb) ? reinterpret_cast<const uint4*>(h8 + bhi * 32 + 16 * (g & 1))
+                                                     : &sm.b.zero[1];
+                av[i] = cat8(*plo, *phi);
+                const uint32_t* pc = (rok && bown < kb) ? &hsq[bown] : &sm.b.code127[0];
+                asc[i] = (*pc >> (8 * rr)) & 0xFFu;
             }
             mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -517,27 +577,37 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             a.resid[c] = mx::f32_to_bf16_rne(mx::bf16_to_f32(a.x[c]) + yb);
         }
     }
+    // the launch count last: a store before a barrier would make the barrier
+    // wait for its device-scope acknowledgement
+    if (threadIdx.x == 0) *memo = launch + 1;
 }
 
-__global__ void reset_workspace_kernel(int* ws, int cfg) {
-    for (int i = threadIdx.x; i < kHOff / 4; i += blockDim.x) ws[i] = 0;
-    __syncthreads();
-    if (threadIdx.x == 0) ws[kCfgOff / 4] = cfg;
+__global__ void reset_workspace_kernel(uint32_t* ws, int cfg, int hwords) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < kHOff / 4) ws[i] = (i == kCfgOff / 4) ? (uint32_t)cfg : 0u;
+    if (i < hwords) ws[kHOff / 4 + i] = kEmpty;
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// uint32 words of one h buffer, rounded to 256 bytes
+int buf_words(int E, int Mi) { return (int)(align256((size_t)E * (Mi / 32) * kRecWords * 4) / 4); }
 
 }  // namespace
 
 extern "C" size_t mxfp4_decode_layer_workspace_size(int E, int Mi) {
     if (E <= 0 || Mi <= 0) return 0;
-    return kHOff + align256((size_t)E * (Mi / 32) * kRecWords * 8);
+    return kHOff + (size_t)2 * buf_words(E, Mi) * 4;
 }
 
 extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream) {
     MXH_REQUIRE(workspace, "decode_layer_reset: null workspace");
-    hipLaunchKernelGGL(reset_workspace_kernel, dim3(1), dim3(256), 0, mxh::as_stream(stream),
-                       static_cast<int*>(workspace), layer_cfg(E, H, Mi));
+    MXH_REQUIRE(E >= 1 && E <= kMaxE && Mi >= 32 && Mi <= 1024 && Mi % 32 == 0 && H >= 512 && H <= 2048 && H % 512 == 0,
+                "decode_layer_reset: E=%d H=%d Mi=%d out of range", E, H, Mi);
+    const int hw = 2 * buf_words(E, Mi);
+    const int n = hw > kHOff / 4 ? hw : kHOff / 4;
+    hipLaunchKernelGGL(reset_workspace_kernel, dim3((n + 255) / 256), dim3(256), 0, mxh::as_stream(stream),
+                       static_cast<uint32_t*>(workspace), layer_cfg(E, H, Mi), hw);
     return mxh::launch_status("decode_layer_reset");
 }
 
@@ -592,6 +662,7 @@ extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, co
     a.H = H;
     a.Mi = Mi;
     a.cfg = layer_cfg(E, H, Mi);
+    a.bufwords = buf_words(E, Mi);
     a.out = out;
     a.resid = static_cast<uint16_t*>(resid_out);
     a.ws = static_cast<uint8_t*>(workspace);
