@@ -228,6 +228,8 @@ __device__ __forceinline__ T ld_sel(const T* p, bool ok, T zero) {
     return ok ? v : zero;
 }
 
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ mx::v8i cat8(uint4 lo, uint4 hi) {
     mx::v8i a = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
     return a;
@@ -475,13 +477,21 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             __builtin_amdgcn_s_sleep(4);
             probe = __hip_atomic_load(cur + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        // 16-byte loads with the agent-scope cache policy (sc1, as the atomic
+        // loads use); out-of-range words read as 0 (buffer bounds)
+        const __amdgpu_buffer_rsrc_t rs =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(cur), (short)0, nwords * 4, 0x00020000);
         while (ok) {
 #pragma unroll
             for (int k = 0; k < kGroups; ++k)
 #pragma unroll
-                for (int i = 0; i < 8; ++i)
-                    wv[k][i] = __hip_atomic_load(cur + min(2048 * k + 8 * (int)threadIdx.x + i, nwords - 1),
-                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                for (int h = 0; h < 2; ++h) {
+                    const v4u q = __builtin_amdgcn_raw_buffer_load_b128(rs, (2048 * k + 8 * (int)threadIdx.x + 4 * h) * 4, 0, 16);
+                    wv[k][4 * h + 0] = q.x;
+                    wv[k][4 * h + 1] = q.y;
+                    wv[k][4 * h + 2] = q.z;
+                    wv[k][4 * h + 3] = q.w;
+                }
             bool pending = false;
 #pragma unroll
             for (int k = 0; k < kGroups; ++k)
@@ -493,6 +503,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 break;
             }
             __builtin_amdgcn_s_sleep(2);
+            asm volatile("" ::: "memory");   // the words may change: reload them next round
         }
     }
     if (ok) {
