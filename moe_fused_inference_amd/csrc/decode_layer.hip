@@ -250,8 +250,8 @@ union Smem {
     struct {                                       // down workgroups
         uint4 zero[2];                             // operand source of the zero rows / blocks
         uint32_t code127[4];                       // [0]: scale source of the zero rows / blocks (h8 stays 16-B aligned)
-        uint8_t h8[kMaxE * kTerms * 1024];         // E4M3 terms of h, [slot][term][Mi]
-        uint32_t hsc[kMaxE * 32];                  // [slot][32-block]: codes of terms 0..2
+        uint8_t h8[kMaxE * kTerms * 1024];         // E4M3 terms of h, [record][term][32], record = slot*Mi/32 + block
+        uint32_t hsc[kMaxE * 32];                  // [record]: codes of terms 0..2
         float red[4][16];
         int abort;
     } b;
@@ -511,9 +511,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         for (int k = 0; k < kGroups; ++k) {
             const int wi = 2048 * k + 8 * (int)threadIdx.x;   // first word; quads never straddle nwords
             if (wi < nwords) {
-                const int rec = wi / kRecWords;
-                const int sl = rec / nblk_mi;
-                const int blk = rec - sl * nblk_mi;
+                const int rec = 64 * k + ((int)threadIdx.x >> 2);   // wi / kRecWords
 #pragma unroll
                 for (int t = 0; t < kTerms; ++t) {
                     // byte t of words i = 0..7 -> 8 consecutive E4M3 bytes of term t
@@ -522,11 +520,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                                         (__builtin_amdgcn_perm(wv[k][3], wv[k][2], sel) << 16);
                     const uint32_t hi = __builtin_amdgcn_perm(wv[k][5], wv[k][4], sel) |
                                         (__builtin_amdgcn_perm(wv[k][7], wv[k][6], sel) << 16);
-                    *reinterpret_cast<uint64_t*>(sm.b.h8 + (sl * kTerms + t) * Mi + blk * 32 + 8 * (threadIdx.x & 3)) =
+                    *reinterpret_cast<uint64_t*>(sm.b.h8 + (rec * kTerms + t) * 32 + 8 * (threadIdx.x & 3)) =
                         (uint64_t)lo | ((uint64_t)hi << 32);
                 }
                 if ((threadIdx.x & 3) == 0)
-                    sm.b.hsc[sl * 32 + blk] = (wv[k][0] >> 24) | ((wv[k][1] >> 24) << 8) | ((wv[k][2] >> 24) << 16);
+                    sm.b.hsc[rec] = (wv[k][0] >> 24) | ((wv[k][1] >> 24) << 8) | ((wv[k][2] >> 24) << 16);
             }
         }
     }
@@ -538,41 +536,56 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     float part = 0.0f;  // this lane's (lane < 16) partial combine over its slots
     if (!abort) {
         const int sb0 = (g * steps) & ~3;
+        bool live[2];
+        const uint8_t* h8[2];
+        const uint32_t* hsq[2];
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
-            if (slot[q] >= a.E) continue;
-            const uint8_t* h8 = sm.b.h8 + (slot[q] * kTerms + rr) * Mi;
-            const uint32_t* hsq = sm.b.hsc + slot[q] * 32;
-            // operands of all steps first; zero operands come from the zero
-            // region (an address select, no branch between the LDS reads)
-            mx::v8i av[MS];
-            uint32_t asc[MS];
+            live[q] = slot[q] < a.E;                                              // wave-uniform
+            const int sl = live[q] ? slot[q] : 0;
+            h8[q] = sm.b.h8 + (sl * kb * kTerms + rr) * 32;                       // block b at + b*kTerms*32
+            hsq[q] = sm.b.hsc + sl * kb;
+        }
+        // operands of both slots for all steps first (their LDS reads issue
+        // back to back), then the two slots' MFMA chains interleaved step by
+        // step (independent accumulators).  Zero operands come from the zero
+        // region: an address select, no branch between the LDS reads.
+        mx::v8i av[2][MS];
+        uint32_t asc[2][MS], bsc[2][MS];
 #pragma unroll
-            for (int i = 0; i < MS; ++i) {
-                // step i: B lane group gb holds block gb*steps + i
-                const int blo = (g >> 1) * steps + i;
-                const int bhi = (2 + (g >> 1)) * steps + i;
-                const int bown = g * steps + i;
-                const bool rok = r < kTerms && i < steps;
-                const uint4* plo = (rok && blo < kb) ? reinterpret_cast<const uint4*>(h8 + blo * 32 + 16 * (g & 1))
-                                                     : &sm.b.zero[0];
-                const uint4* phi = (rok && bhi < kb) ? reinterpret_cast<const uint4*>(h8 + bhi * 32 + 16 * (g & 1))
-                                                     : &sm.b.zero[1];
-                av[i] = cat8(*plo, *phi);
-                const uint32_t* pc = (rok && bown < kb) ? &hsq[bown] : &sm.b.code127[0];
-                asc[i] = (*pc >> (8 * rr)) & 0xFFu;
-            }
-            mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+        for (int i = 0; i < MS; ++i) {
+            // step i: B lane group gb holds block gb*steps + i
+            const int blo = (g >> 1) * steps + i;
+            const int bhi = (2 + (g >> 1)) * steps + i;
+            const int bown = g * steps + i;
+            const bool rok = r < kTerms && i < steps;
+            // weight scale byte of block g*steps+i from the aligned dwords
+            // (blocks past the row carry zero data, so any scale is fine)
+            const int bi = g * steps + i - sb0;           // 0..10
 #pragma unroll
-            for (int i = 0; i < MS; ++i) {
-                // weight scale byte of block g*steps+i from the aligned dwords
-                // (blocks past the row carry zero data, so any scale is fine)
-                const int bi = g * steps + i - sb0;           // 0..10
+            for (int q = 0; q < 2; ++q) {
+                const bool ok = rok && live[q];
+                const uint4* plo = (ok && blo < kb) ? reinterpret_cast<const uint4*>(h8[q] + blo * (kTerms * 32) + 16 * (g & 1))
+                                                    : &sm.b.zero[0];
+                const uint4* phi = (ok && bhi < kb) ? reinterpret_cast<const uint4*>(h8[q] + bhi * (kTerms * 32) + 16 * (g & 1))
+                                                    : &sm.b.zero[1];
+                const uint32_t* pc = (ok && bown < kb) ? &hsq[q][bown] : &sm.b.code127[0];
+                av[q][i] = cat8(*plo, *phi);
+                asc[q][i] = (*pc >> (8 * rr)) & 0xFFu;
                 const uint32_t wd = bi < 4 ? bsw[q][0] : (bi < 8 ? bsw[q][1] : bsw[q][2]);
-                acc = mx::mfma16_fp8a_fp4b(av[i], bq[q][i], acc, asc[i], (wd >> (8 * (bi & 3))) & 0xFFu);
+                bsc[q][i] = (wd >> (8 * (bi & 3))) & 0xFFu;
             }
-            mx::pin(acc);
-            part = fmaf(wgt[q], acc[0] + acc[1] + acc[2], part);
+        }
+        mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+        for (int i = 0; i < MS; ++i)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                acc[q] = mx::mfma16_fp8a_fp4b(av[q][i], bq[q][i], acc[q], asc[q][i], bsc[q][i]);
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            mx::pin(acc[q]);
+            if (live[q]) part = fmaf(wgt[q], acc[q][0] + acc[q][1] + acc[q][2], part);
         }
     }
     if (lane < 16) sm.b.red[wave][lane] = part;
