@@ -18,6 +18,9 @@ int lin_pq_gemv(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const 
 int lin_pq_gemm(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc,
                 float* y, int M, int N, int Kp, hipStream_t st);
 bool lin_pq_gemm_supported(int M, int N, int Kp);
+int lin_pq_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc,
+                 float* y, int M, int N, int Kp, hipStream_t st);
+bool lin_pq_gemm2_supported(int M, int N, int Kp);
 }  // namespace mxh
 
 namespace {
@@ -32,6 +35,8 @@ extern "C" int mxfp4_lin_pq(const uint8_t* xq, const uint8_t* xsc, const uint8_t
     MXH_REQUIRE(Kp % 32 == 0, "lin_pq: Kp=%d must be a multiple of 32", Kp);
     MXH_REQUIRE(K <= Kp, "lin_pq: K=%d exceeds Kp=%d", K, Kp);
     hipStream_t st = mxh::as_stream(stream);
+    if (M > kGemvMaxM && mxh::lin_pq_gemm2_supported(M, N, Kp))
+        return mxh::lin_pq_gemm2(xq, xsc, wp, wsc, y, M, N, Kp, st);
     if (M > kGemvMaxM && mxh::lin_pq_gemm_supported(M, N, Kp))
         return mxh::lin_pq_gemm(xq, xsc, wp, wsc, y, M, N, Kp, st);
     return mxh::lin_pq_gemv(xq, xsc, wp, wsc, y, M, N, K, Kp, st);

@@ -28,7 +28,8 @@ def _w(dext, N, K, seed):
 # shapes of tests/correctness/test_mxfp4_decode.py:78-79 plus GEMM-path shapes
 LIN_SHAPES = [(1, 32, 64), (1, 768, 2048), (1, 2048, 768), (3, 128, 100), (1, 4096, 2048),
               (2, 2048, 2048), (16, 64, 96), (17, 64, 256), (128, 128, 256), (200, 300, 1000),
-              (129, 257, 40), (512, 1536, 2048)]
+              (129, 257, 40), (512, 1536, 2048), (300, 520, 768), (2048, 2048, 768),
+              (2048, 4096, 512), (2000, 4000, 768)]   # the last two on the 256 x 256 tile GEMM
 
 
 @pytest.mark.parametrize("M,N,K", LIN_SHAPES)
