@@ -508,7 +508,7 @@ def main():
         "layer_bytes": LAYER_BYTES, "layer_flops": LAYER_FLOPS,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_layer_kernel<false>",
+                     "kernel": "decode_layer_kernel<false, 6>",
                      "timing": "HIP events on the launching stream around the timed graph replays / launches; "
                                "rocprofv3 kernel-trace average of the same kernel agrees (profiles/)"},
         "cpu_baseline": cpu,

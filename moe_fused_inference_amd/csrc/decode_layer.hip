@@ -25,16 +25,19 @@
 // gate/up workgroup is resident or finished before any down workgroup waits:
 // the wait cannot deadlock.  It is still bounded (kSpinLimit polls); on expiry
 // the kernel sets an error flag, skips its work and exits normally.
-//   * h travels as 32-bit words (4 E4M3 bytes of one term, or the 3 scale
-//     codes of a 32-block), 25 per (slot, 32-row block) record.  A word is
-//     its own flag: between uses it holds the "empty" pattern 0x7FBADBAD,
-//     whose top byte is the E4M3 NaN code that the split of a finite h never
-//     produces (and a codes word has a zero top byte).  Producers store with
-//     agent-scope atomic stores (write-through to the device coherence
-//     point); consumers poll with agent-scope atomic loads, first one word
-//     per thread (a probe that keeps polling traffic low while the weights
-//     stream), then the rest.  (A release/acquire fence pair would instead
-//     write back and invalidate a whole L2 per workgroup.)
+//   * h travels as 32-bit words, one per value: bytes 0..2 hold the value's
+//     three E4M3 terms, and byte 3 of words 0..2 of a (slot, 32-block) record
+//     holds the E8M0 code of term 0..2.  A word is its own flag: between uses
+//     it holds kEmpty, whose byte 0 is the E4M3 NaN code: term 0 of a finite
+//     h never takes it, and a non-finite h makes term 1 a NaN code as well
+//     (kEmpty's byte 1 is not), so no published word equals kEmpty.
+//     Producers store with agent-scope
+//     atomic stores (write-through to the device coherence point).  A
+//     consumer first polls one word per thread with agent-scope atomic loads
+//     (little traffic while the weights stream), then reloads all of its
+//     words with 16-byte buffer loads carrying the same agent-scope cache
+//     policy until none is empty.  (A release/acquire fence pair would
+//     instead write back and invalidate a whole L2 per workgroup.)
 //   * Every consumer reads every word, so no consumer can empty them; instead
 //     there are two buffers, used by alternate launches.  Each workgroup
 //     keeps its own launch count ("memo") in the workspace, reads it at start
