@@ -186,6 +186,42 @@ int mxfp4_moe_group(const int64_t* topi, int T, int topk, int n_experts, int* co
                     int* pairs, void* stream);
 
 /* ---------------------------------------------------------------------
+ * Router top-k on the GPU.  Replaces the host-side routing of every MoE
+ * layer (runtime/model_runner_v2.py:189-192 decode, :272-275 batch, and
+ * moe_route :100-105):  probs = softmax(logits.float(), -1);
+ * topv, topi = topk(probs, k); topv /= topv.sum(-1) if norm.
+ *   logits  fp32 (M, n_experts), rows ldl floats apart
+ *   ids     int32 (M, k) out, descending probability (exact ties: lower
+ *           index first; torch.topk leaves their order unspecified)
+ *   ids64   optional int64 (M, k) out (torch's topi layout), or NULL
+ *   w       fp32 (M, k) out: topv, renormalised over the k winners (summed
+ *           in rank order) when norm != 0
+ * n_experts <= 1024, k <= min(32, n_experts).  The ids feed the fused layer's
+ * device routing (mxfp4_moe_decode_layer ids_dev/w_dev) or
+ * mxfp4_route_tables, with no host round trip.
+ */
+int mxfp4_route_topk(const float* logits, int64_t ldl, int M, int n_experts, int k, int norm,
+                     int32_t* ids, int64_t* ids64, float* w, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Device pointer tables of the drop-in grouped ops from device ids: the
+ * token-major lists the reference builds on the host and copies to the
+ * device (runtime/model_runner_v2.py:279-286, src/ext/mxfp4_decode_binding.cpp:
+ * 44-60).  For row m, slot e (ids int32 (M, k)):
+ *   gu_wp_tab[m*2k + e]     = gate_wp + id*Mi*Kp_h/2,  [m*2k + k + e] = up
+ *   gu_ws_tab[...]          the same for the scales (Mi*Kp_h/32 per expert)
+ *   dn_wp_tab[m*k + e]      = down_wp + id*H*Kp_mi/2,  dn_ws_tab likewise
+ * over weights stacked per layer as for mxfp4_moe_decode_layer (Kp_h, Kp_mi
+ * = H, Mi rounded up to 32).  The tables are what mxfp4_moe_gateup_devtab /
+ * mxfp4_moe_down_devtab take.  Ids outside [0, n_experts) are clamped into
+ * range (memory safety only; routing produced by mxfp4_route_topk is valid).
+ */
+int mxfp4_route_tables(const int32_t* ids, int M, int k, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                       const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                       const uint8_t* down_ws, int n_experts, int H, int Mi, int64_t* gu_wp_tab,
+                       int64_t* gu_ws_tab, int64_t* dn_wp_tab, int64_t* dn_ws_tab, void* stream);
+
+/* ---------------------------------------------------------------------
  * Grouped MoE over a batch of tokens (prefill, speculative verify).
  * Replaces ModelRunnerV2.moe_compute (runtime/model_runner_v2.py:108-122):
  * per expert e the rows of torch.where(topi == e) go through `forward` with

@@ -144,6 +144,60 @@ def moe_group(topi, n_experts):
     return counts, offs, pairs
 
 
+def route_topk(logits, k, norm=True, want_int64=False, out=None):
+    """GPU router top-k (mxfp4_route_topk): softmax over the last dim of the
+    fp32 logits (M, n), top-k, renormalised over the winners when norm --
+    runtime/model_runner_v2.py:189-192 without the host round trip.
+    Returns (ids int32 (M, k), w fp32 (M, k)) and, with want_int64, also
+    topi int64 (M, k) (torch.topk's dtype).  `out` = (ids, w) reuses
+    preallocated contiguous tensors (e.g. bound into a captured graph)."""
+    lib = _lib.load()
+    if logits.dim() != 2 or logits.dtype != torch.float32 or not logits.is_cuda:
+        raise RuntimeError("logits must be a 2-D cuda float32 tensor")
+    if logits.stride(1) != 1:
+        logits = logits.contiguous()
+    M, n = logits.shape
+    dev = logits.device
+    if out is not None:
+        ids, w = out
+        if (ids.dtype != torch.int32 or w.dtype != torch.float32 or ids.numel() != M * k or w.numel() != M * k
+                or not ids.is_contiguous() or not w.is_contiguous() or not ids.is_cuda or not w.is_cuda):
+            raise RuntimeError(f"out must be contiguous cuda int32 / float32 tensors of {M * k} elements")
+    else:
+        ids = torch.empty((M, k), dtype=torch.int32, device=dev)
+        w = torch.empty((M, k), dtype=torch.float32, device=dev)
+    ids64 = torch.empty((M, k), dtype=torch.int64, device=dev) if want_int64 else None
+    _lib.check(lib.mxfp4_route_topk(logits.data_ptr(), logits.stride(0), M, n, k, int(bool(norm)), ids.data_ptr(),
+                                    ids64.data_ptr() if want_int64 else None, w.data_ptr(),
+                                    torch.cuda.current_stream(dev).cuda_stream), "route_topk")
+    return (ids, w, ids64) if want_int64 else (ids, w)
+
+
+def route_tables(ids, experts):
+    """Device pointer tables for moe_gateup_tab / moe_down_tab from device
+    ids (mxfp4_route_tables): ids int32 (M, k) -> (gu_wp, gu_ws) int64
+    (M*2k,) in the token-major order m*2k + proj*k + e, and (dn_wp, dn_ws)
+    int64 (M*k,) -- the lists of runtime/model_runner_v2.py:279-286."""
+    lib = _lib.load()
+    experts.check()
+    if ids.dim() != 2 or ids.dtype != torch.int32 or not ids.is_cuda:
+        raise RuntimeError("ids must be a 2-D cuda int32 tensor")
+    ids = ids.contiguous()
+    M, k = ids.shape
+    dev = ids.device
+    gu_wp = torch.empty(M * 2 * k, dtype=torch.int64, device=dev)
+    gu_ws = torch.empty_like(gu_wp)
+    dn_wp = torch.empty(M * k, dtype=torch.int64, device=dev)
+    dn_ws = torch.empty_like(dn_wp)
+    _lib.check(lib.mxfp4_route_tables(ids.data_ptr(), M, k, experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
+                                      experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
+                                      experts.down_wp.data_ptr(), experts.down_ws.data_ptr(), experts.n_experts,
+                                      experts.hidden, experts.inter, gu_wp.data_ptr(), gu_ws.data_ptr(),
+                                      dn_wp.data_ptr(), dn_ws.data_ptr(), torch.cuda.current_stream(dev).cuda_stream),
+               "route_tables")
+    return gu_wp, gu_ws, dn_wp, dn_ws
+
+
 def prefill_workspace(T, topk, n_experts, H, Mi, device="cuda"):
     """Scratch memory for one moe_compute call of this shape (reusable by
     stream-ordered calls; nothing persists between calls)."""

@@ -153,6 +153,28 @@ def token_major_tables(topi, n_tokens, k):
     return np.array(gu, np.int64), np.array(dn, np.int64)
 
 
+def route_topk_np(logits, k=8, renorm=True):
+    """numpy restatement of the routing of runtime/model_runner_v2.py:189-192
+    (softmax in fp32 -> top-k -> renormalise), in the device kernel's order:
+    max, exp(l - max), sum, divide; top-k descending with exact ties broken
+    towards the lower index (torch.topk leaves their order unspecified);
+    renormalisation sums the k winners in rank order.  Returns
+    (topi int64 (M, k), topv fp32 (M, k))."""
+    lg = np.atleast_2d(np.asarray(logits, np.float32))
+    mx = lg.max(axis=-1, keepdims=True)
+    e = np.exp((lg - mx).astype(np.float32)).astype(np.float32)
+    s = e.sum(axis=-1, dtype=np.float32, keepdims=True)
+    p = (e / s).astype(np.float32)
+    order = np.argsort(-p, axis=-1, kind="stable")[:, :k]
+    topv = np.take_along_axis(p, order, axis=-1)
+    if renorm:
+        ts = np.zeros((p.shape[0], 1), np.float32)
+        for r in range(k):
+            ts = (ts + topv[:, r:r + 1]).astype(np.float32)
+        topv = (topv / ts).astype(np.float32)
+    return order.astype(np.int64), topv.astype(np.float32)
+
+
 def group_by_expert(topi):
     """Token->expert grouping for the M<=16 grouped path.
 

@@ -232,3 +232,44 @@ def test_moe_prefill_ref_single_expert_weight_one_is_forward_chain():
     u = ops.forward_ref(x, uwp, uws).astype(np.float32)
     y = ops.forward_ref(ops.silu_mul_f32(g, u), dwp, dws)
     np.testing.assert_array_equal(out, fmt.bf16_round(fmt.bf16_round(y)).astype(np.float64))
+
+
+# --------------------------------------------------------------------- GPU routing oracle
+@pytest.mark.parametrize("n,k", [(128, 8), (60, 1), (256, 32), (1024, 8), (8, 8), (65, 3)])
+def test_route_topk_np_matches_torch(n, k):
+    """The numpy restatement against the reference's own calls (torch softmax,
+    topk, renormalise on CPU): identical ids, weights to a few ulp."""
+    rng = np.random.default_rng(n * 7 + k)
+    lg = (rng.standard_normal((64, n)) * 3).astype(np.float32)
+    ti, tv = ops.route_topk_np(lg, k)
+    ri, rv = ops.route_ref(lg, k)
+    assert np.array_equal(ti, ri)
+    assert np.abs(tv - rv).max() <= 1e-6 * np.abs(rv).max()
+    _, raw = ops.route_topk_np(lg, k, renorm=False)
+    p = np.exp(lg - lg.max(-1, keepdims=True))
+    p /= p.sum(-1, keepdims=True)
+    assert np.allclose(raw, np.sort(p, -1)[:, ::-1][:, :k], rtol=1e-5, atol=0)
+
+
+def test_route_topk_np_special_cases():
+    # all-equal logits: ties go to the lower index, weights 1/k
+    ti, tv = ops.route_topk_np(np.zeros((2, 16), np.float32), 4)
+    assert np.array_equal(ti, [[0, 1, 2, 3]] * 2) and np.allclose(tv, 0.25)
+    # -inf logits (masked experts) are never chosen while finite ones remain
+    lg = np.full((1, 10), -np.inf, np.float32)
+    lg[0, [7, 2, 9]] = [1.0, 3.0, 2.0]
+    ti, tv = ops.route_topk_np(lg, 3)
+    assert np.array_equal(ti, [[2, 9, 7]])
+    e = np.exp(np.array([3.0, 2.0, 1.0]) - 3.0)
+    assert np.allclose(tv[0], e / e.sum(), rtol=1e-6)
+    # k == n: a full descending sort; renormalised weights are the softmax itself
+    lg = np.array([[0.5, -1.0, 2.0, 0.0]], np.float32)
+    ti, tv = ops.route_topk_np(lg, 4)
+    assert np.array_equal(ti, [[2, 0, 3, 1]])
+    p = np.exp(lg[0] - 2.0)
+    assert np.allclose(tv[0], (p / p.sum())[[2, 0, 3, 1]], rtol=1e-6)
+    # one dominant logit: weight ~1 on it
+    lg = np.zeros((1, 32), np.float32)
+    lg[0, 11] = 40.0
+    ti, tv = ops.route_topk_np(lg, 8)
+    assert ti[0, 0] == 11 and tv[0, 0] > 0.999999 and np.array_equal(ti[0, 1:], np.arange(7))
