@@ -84,12 +84,16 @@ def build_layers(torch, lib, dev, n_layers):
     return layers
 
 
-def draw_routes(torch, n_steps, n_layers, seed):
-    """Fresh N(0,1) router logits per (step, layer) -> softmax -> top-8 -> renorm
-    (runtime/model_runner_v2.py:189-192)."""
+def draw_logits(torch, n_steps, n_layers, seed):
+    """Fresh N(0,1) router logits per (step, layer), on the host."""
     g = torch.Generator()
     g.manual_seed(seed)
-    logits = torch.randn((n_steps, n_layers, N_EXP), generator=g)
+    return torch.randn((n_steps, n_layers, N_EXP), generator=g)
+
+
+def draw_routes(torch, n_steps, n_layers, seed):
+    """draw_logits -> softmax -> top-8 -> renorm (runtime/model_runner_v2.py:189-192)."""
+    logits = draw_logits(torch, n_steps, n_layers, seed)
     p = torch.softmax(logits.float(), -1)
     tv, ti = torch.topk(p, TOPK, dim=-1)
     tv = tv / tv.sum(-1, keepdim=True)
@@ -119,6 +123,75 @@ def make_decode_graph(torch, layers, routes, x0, ws, outs, bufs):
                 c()
     torch.cuda.synchronize()
     return graph, calls
+
+
+def devroute_graph(torch, layers, logits_host, x0, ws, outs, bufs, routes):
+    """The decode steps with routing on the GPU: per layer route_topk on that
+    layer's resident logits, then the fused layer reading ids / weights from
+    device memory -- one graph, no host round trip per layer.  Checks the
+    device ids of every (step, layer) against the host routing first."""
+    from moe_fused_inference_amd.moe_layer import DecodeLayerCall, route_topk
+    S = logits_host.shape[0]
+    logits = logits_host.float().cuda()
+    ids = torch.empty((S, LAYERS, TOPK), dtype=torch.int32, device="cuda")
+    w = torch.empty((S, LAYERS, TOPK), dtype=torch.float32, device="cuda")
+    calls = []
+    for s in range(S):
+        src = x0
+        for L, lay in enumerate(layers):
+            calls.append((logits[s, L:L + 1], ids[s, L], w[s, L],
+                          DecodeLayerCall(src, ids[s, L], w[s, L], lay, outs[L], bufs[L % 2], ws)))
+            src = bufs[L % 2]
+
+    def run():
+        for lg, i, ww, c in calls:
+            route_topk(lg, TOPK, out=(i.view(1, TOPK), ww.view(1, TOPK)))
+            c()
+
+    run()
+    torch.cuda.synchronize()
+    if not torch.equal(ids.cpu(), routes[0]):
+        raise RuntimeError("device routing differs from the host routing")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            run()
+    torch.cuda.synchronize()
+    return graph, (logits, ids, w, calls)
+
+
+def routed_graph(torch, layers, logits_host, x0, ws, outs, bufs, routes):
+    """The decode steps with the routing inside the fused launch
+    (RoutedLayerCall on each layer's resident logits).  Checks the ids the
+    launches report against the host routing first."""
+    from moe_fused_inference_amd.moe_layer import RoutedLayerCall
+    S = logits_host.shape[0]
+    logits = logits_host.float().cuda()
+    ids = torch.empty((S, LAYERS, TOPK), dtype=torch.int32, device="cuda")
+    w = torch.empty((S, LAYERS, TOPK), dtype=torch.float32, device="cuda")
+    calls = []
+    for s in range(S):
+        src = x0
+        for L, lay in enumerate(layers):
+            calls.append(RoutedLayerCall(src, logits[s, L], TOPK, lay, outs[L], bufs[L % 2], ws,
+                                         ids_out=ids[s, L], w_out=w[s, L]))
+            src = bufs[L % 2]
+    for c in calls:
+        c()
+    torch.cuda.synchronize()
+    if not torch.equal(ids.cpu(), routes[0]):
+        raise RuntimeError("in-kernel routing differs from the host routing")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    return graph, (logits, ids, w, calls)
 
 
 def time_graph(torch, graph, steps, warmup):
@@ -476,6 +549,32 @@ def main():
                                 "note": "prequant + moe_gateup + moe_down + moe_combine + bf16 residual "
                                         "(torch add), graph-captured, activations MXFP4 as the reference"}
         log(f"drop-in path: {us_d:.3f} us/layer")
+        rg, keep = devroute_graph(torch, layers, draw_logits(torch, S_ROUTES, LAYERS, seed=7), x0, ws, outs,
+                                  bufs, routes)
+        ms_r = time_graph(torch, rg, max(3, args.steps // 2), 2)
+        us_r = ms_r * 1e3 / n_launch
+        extra["device_routing"] = {"us_per_layer": round(us_r, 3),
+                                   "gbs": round(LAYER_BYTES / (us_r * 1e-6) / 1e9, 1),
+                                   "launches_per_layer": 2,
+                                   "note": "route_topk (softmax/top-8/renorm of the layer's resident fp32 "
+                                           "logits) + fused layer with device ids/weights, graph-captured; "
+                                           "ids checked equal to the host routing"}
+        log(f"device routing: {us_r:.3f} us/layer (route_topk + fused layer)")
+        del rg, keep
+        fg, keep = routed_graph(torch, layers, draw_logits(torch, S_ROUTES, LAYERS, seed=7), x0, ws, outs, bufs,
+                                routes)
+        ms_f = time_graph(torch, fg, max(3, args.steps // 2), 2)
+        us_f = ms_f * 1e3 / n_launch
+        extra["fused_routing"] = {"us_per_layer": round(us_f, 3),
+                                  "gbs": round(LAYER_BYTES / (us_f * 1e-6) / 1e9, 1),
+                                  "launches_per_layer": 1,
+                                  "note": "mxfp4_moe_decode_layer_routed: softmax/top-8/renorm of the layer's "
+                                          "resident fp32 logits inside the fused launch, graph-captured; ids "
+                                          "checked equal to the host routing"}
+        log(f"fused routing: {us_f:.3f} us/layer (one launch per layer, routing included)")
+        del fg, keep
+        if layer_status(ws) != 0:
+            raise RuntimeError("fused decode layer reported an expired wait")
         pre = {}
         for (M, N, K) in ((512, 1536, 2048), (2048, 2048, 768), (4096, 4096, 2048)):
             pre[f"{M}x{N}x{K}"] = bench_gemm(torch, lext, dext, M, N, K)
@@ -508,7 +607,7 @@ def main():
         "layer_bytes": LAYER_BYTES, "layer_flops": LAYER_FLOPS,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_layer_kernel<false, 6>",
+                     "kernel": "decode_layer_kernel<0, 6>",
                      "timing": "HIP events on the launching stream around the timed graph replays / launches; "
                                "rocprofv3 kernel-trace average of the same kernel agrees (profiles/)"},
         "cpu_baseline": cpu,

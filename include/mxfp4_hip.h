@@ -173,6 +173,22 @@ int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* 
                            int n_experts, int E, int H, int Mi, float* out, void* resid_out,
                            void* workspace, size_t workspace_bytes, void* stream);
 
+/* As mxfp4_moe_decode_layer with the routing computed in the same launch
+ * from the layer's router logits (runtime/model_runner_v2.py:189-192:
+ * softmax over n_experts fp32 logits, top-E, renormalised when norm), the
+ * same rule and ids as mxfp4_route_topk.  Every workgroup derives the E
+ * (id, weight) pairs itself, so the step needs no separate routing launch and
+ * no host round trip.  logits: fp32 (n_experts) in device memory,
+ * n_experts <= 256.  ids_out / w_out: optional int32 / fp32 (E) device
+ * arrays receiving the routing (both or neither).
+ */
+int mxfp4_moe_decode_layer_routed(const void* x, const float* logits, int norm, int32_t* ids_out,
+                                  float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                  const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                  const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                  float* out, void* resid_out, void* workspace, size_t workspace_bytes,
+                                  void* stream);
+
 /* ---------------------------------------------------------------------
  * Token -> expert grouping (the bookkeeping of torch.where(topi == e) in
  * runtime/model_runner_v2.py:111 and of the token-major tables :279-286).

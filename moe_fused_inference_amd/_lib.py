@@ -34,6 +34,8 @@ SIGNATURES = {
     "mxfp4_decode_layer_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),
     "mxfp4_moe_decode_layer": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                       _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_moe_decode_layer_routed": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                             _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "mxfp4_moe_group": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_route_topk": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_route_tables": (_c_i, [_c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i,

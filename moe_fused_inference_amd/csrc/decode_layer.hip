@@ -49,9 +49,11 @@
 //     Mi): the workspace header records them (mxfp4_decode_layer_reset) and
 //     a mismatching launch sets the error flag instead of waiting.
 //
-// Registers are kept near 128 VGPRs (h is staged through LDS, the down
-// K-step count is a template bound) so that every workgroup of a layer is
-// resident from the start and all weight loads are in flight at once.  The
+// Registers stay at or below 256 VGPRs per lane (184 at Mi <= 768; h is
+// staged through LDS, the down K-step count is a template bound), so two
+// 256-thread workgroups fit per CU: 512 slots for the E*Mi/32 + H/16 = 320
+// workgroups of a layer, every one resident from the start and all weight
+// loads in flight at once.  The
 // MFMA loops read their operands with clamped, unconditional LDS loads so the
 // reads of a phase issue back to back ahead of the MFMA chain.
 //
@@ -95,6 +97,11 @@ struct LayerArgs {
     const float* w_dev;       // (E) combine weights in device memory, or null
     int32_t ids[kMaxE];       // by-value ids when ids_dev is null
     float w[kMaxE];           // by-value weights when w_dev is null
+    const float* logits;      // (n_experts) fp32 router logits: routing computed in-kernel
+    int n_experts;            // experts per layer (logits routing)
+    int norm;                 // renormalise the top-E weights (logits routing)
+    int32_t* ids_out;         // optional (E) ids / weights written by workgroup 0 (logits routing)
+    float* w_out;
     int E, H, Mi;
     int cfg;                  // expected workspace config word
     int bufwords;             // uint32 words between the two h buffers
@@ -260,7 +267,13 @@ union Smem {
     } b;
 };
 
-template <bool DEV_IDS, int MS>
+// Where the routing comes from: kernel arguments, device arrays, or router
+// logits in device memory (softmax / top-E / renormalise computed by every
+// wave at entry, mx::wave_topk).
+enum { ROUTE_HOST = 0, ROUTE_DEV_IDS = 1, ROUTE_LOGITS = 2 };
+constexpr int kRouteNpl = 4;          // logits routing: up to 256 experts
+
+template <int ROUTE, int MS>
 __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     __shared__ __align__(16) Smem sm;
 
@@ -273,6 +286,16 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int nA = a.E * nblk_mi;
     const int bid = blockIdx.x;
     uint32_t* hbuf = reinterpret_cast<uint32_t*>(a.ws + kHOff);
+    // logits routing: lane r < E of every wave holds rank r (id, weight)
+    int rid = 0;
+    float rw = 0.0f;
+    if constexpr (ROUTE == ROUTE_LOGITS) {
+        mx::wave_topk<kRouteNpl>(a.logits, a.n_experts, a.E, a.norm, rid, rw);
+        if (bid == 0 && wave == 0 && lane < a.E && a.ids_out) {
+            a.ids_out[lane] = rid;
+            a.w_out[lane] = rw;
+        }
+    }
 
     if (bid < nA) {
         // ================================================= gate / up
@@ -292,7 +315,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
         const int launch = *memo;
 
-        const int e = DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[s]) : pick_id(a, s);
+        const int e = ROUTE == ROUTE_LOGITS ? __builtin_amdgcn_readfirstlane(__shfl(rid, s))
+                      : ROUTE == ROUTE_DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[s]) : pick_id(a, s);
         const uint8_t* gw = a.gate_wp + (int64_t)e * a.wp_stride_gu;
         const uint8_t* gs = a.gate_ws + (int64_t)e * a.ws_stride_gu;
         const uint8_t* uw = a.up_wp + (int64_t)e * a.wp_stride_gu;
@@ -422,8 +446,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     for (int q = 0; q < 2; ++q) {
         slot[q] = 2 * wave + q;
         const int sl = slot[q] < a.E ? slot[q] : 0;
-        eid[q] = DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[sl]) : pick_id(a, sl);
-        wgt[q] = DEV_IDS ? a.w_dev[sl] : pick_w(a, sl);
+        eid[q] = ROUTE == ROUTE_LOGITS ? __builtin_amdgcn_readfirstlane(__shfl(rid, sl))
+                 : ROUTE == ROUTE_DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[sl]) : pick_id(a, sl);
+        wgt[q] = ROUTE == ROUTE_LOGITS ? __shfl(rw, sl) : ROUTE == ROUTE_DEV_IDS ? a.w_dev[sl] : pick_w(a, sl);
     }
     uint4 bq[2][MS];
     uint32_t bsw[2][3];   // dwords holding the scale bytes of blocks g*steps..
@@ -648,23 +673,21 @@ extern "C" int mxfp4_decode_layer_status(const void* workspace, int* error_flag)
     return MXFP4_OK;
 }
 
-extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* w_host,
-                                      const int32_t* ids_dev, const float* w_dev,
-                                      const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
-                                      const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
-                                      int n_experts, int E, int H, int Mi, float* out, void* resid_out,
-                                      void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+// Checks and fills the launch arguments shared by the routing variants.
+int layer_args(LayerArgs& a, const void* x, const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+               const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws, int n_experts, int E, int H,
+               int Mi, float* out, void* resid_out, void* workspace, size_t workspace_bytes) {
     MXH_REQUIRE(x && gate_wp && gate_ws && up_wp && up_ws && down_wp && down_ws && out && workspace,
                 "moe_decode_layer: null pointer");
     MXH_REQUIRE(E >= 1 && E <= kMaxE, "moe_decode_layer: E=%d must be in [1, 8]", E);
+    MXH_REQUIRE(n_experts >= E, "moe_decode_layer: n_experts=%d < E=%d", n_experts, E);
     MXH_REQUIRE(H % 512 == 0 && H >= 512 && H <= 2048, "moe_decode_layer: H=%d must be a multiple of 512 in [512, 2048]", H);
     MXH_REQUIRE(Mi % 32 == 0 && Mi >= 32 && Mi <= 1024, "moe_decode_layer: Mi=%d must be a multiple of 32 in [32, 1024]", Mi);
-    MXH_REQUIRE((ids_dev != nullptr) == (w_dev != nullptr), "moe_decode_layer: give ids and weights both on device or both on host");
-    MXH_REQUIRE(ids_dev || (ids_host && w_host), "moe_decode_layer: missing routing");
     MXH_REQUIRE(workspace_bytes >= mxfp4_decode_layer_workspace_size(E, Mi), "moe_decode_layer: workspace too small");
     MXH_REQUIRE(((uintptr_t)workspace & 255) == 0, "moe_decode_layer: workspace must be 256-byte aligned");
     MXH_REQUIRE(((uintptr_t)x & 15) == 0, "moe_decode_layer: x must be 16-byte aligned");
-    LayerArgs a{};
+    a = LayerArgs{};
     a.x = static_cast<const uint16_t*>(x);
     a.gate_wp = gate_wp;
     a.gate_ws = gate_ws;
@@ -676,6 +699,41 @@ extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, co
     a.ws_stride_gu = (int64_t)Mi * (H / 32);
     a.wp_stride_dn = (int64_t)H * (Mi / 2);
     a.ws_stride_dn = (int64_t)H * (Mi / 32);
+    a.n_experts = n_experts;
+    a.E = E;
+    a.H = H;
+    a.Mi = Mi;
+    a.cfg = layer_cfg(E, H, Mi);
+    a.bufwords = buf_words(E, Mi);
+    a.out = out;
+    a.resid = static_cast<uint16_t*>(resid_out);
+    a.ws = static_cast<uint8_t*>(workspace);
+    return MXFP4_OK;
+}
+
+template <int ROUTE>
+int launch_layer(const LayerArgs& a, hipStream_t st) {
+    const int nA = a.E * (a.Mi / 32);
+    const int nB = a.H / 16;
+    const int steps = (a.Mi / 32 + 3) / 4;
+    if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), dim3(nA + nB), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), dim3(nA + nB), dim3(256), 0, st, a);
+    return mxh::launch_status("moe_decode_layer");
+}
+}  // namespace
+
+extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, const float* w_host,
+                                      const int32_t* ids_dev, const float* w_dev,
+                                      const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                                      const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                                      int n_experts, int E, int H, int Mi, float* out, void* resid_out,
+                                      void* workspace, size_t workspace_bytes, void* stream) {
+    LayerArgs a;
+    const int rc = layer_args(a, x, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E, H, Mi, out,
+                              resid_out, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE((ids_dev != nullptr) == (w_dev != nullptr), "moe_decode_layer: give ids and weights both on device or both on host");
+    MXH_REQUIRE(ids_dev || (ids_host && w_host), "moe_decode_layer: missing routing");
     a.ids_dev = ids_dev;
     a.w_dev = w_dev;
     if (!ids_dev) {
@@ -685,24 +743,26 @@ extern "C" int mxfp4_moe_decode_layer(const void* x, const int32_t* ids_host, co
             a.w[s] = w_host[s];
         }
     }
-    a.E = E;
-    a.H = H;
-    a.Mi = Mi;
-    a.cfg = layer_cfg(E, H, Mi);
-    a.bufwords = buf_words(E, Mi);
-    a.out = out;
-    a.resid = static_cast<uint16_t*>(resid_out);
-    a.ws = static_cast<uint8_t*>(workspace);
-    const int nA = E * (Mi / 32);
-    const int nB = H / 16;
-    const int steps = (Mi / 32 + 3) / 4;
     hipStream_t st = mxh::as_stream(stream);
-    if (steps <= 6) {
-        if (ids_dev) hipLaunchKernelGGL((decode_layer_kernel<true, 6>), dim3(nA + nB), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((decode_layer_kernel<false, 6>), dim3(nA + nB), dim3(256), 0, st, a);
-    } else {
-        if (ids_dev) hipLaunchKernelGGL((decode_layer_kernel<true, 8>), dim3(nA + nB), dim3(256), 0, st, a);
-        else hipLaunchKernelGGL((decode_layer_kernel<false, 8>), dim3(nA + nB), dim3(256), 0, st, a);
-    }
-    return mxh::launch_status("moe_decode_layer");
+    return ids_dev ? launch_layer<ROUTE_DEV_IDS>(a, st) : launch_layer<ROUTE_HOST>(a, st);
+}
+
+extern "C" int mxfp4_moe_decode_layer_routed(const void* x, const float* logits, int norm, int32_t* ids_out,
+                                             float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                             const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                             const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                             float* out, void* resid_out, void* workspace, size_t workspace_bytes,
+                                             void* stream) {
+    LayerArgs a;
+    const int rc = layer_args(a, x, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E, H, Mi, out,
+                              resid_out, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE(logits, "moe_decode_layer_routed: null logits");
+    MXH_REQUIRE(n_experts <= 64 * kRouteNpl, "moe_decode_layer_routed: n_experts=%d > %d", n_experts, 64 * kRouteNpl);
+    MXH_REQUIRE((ids_out != nullptr) == (w_out != nullptr), "moe_decode_layer_routed: give ids_out and w_out both or neither");
+    a.logits = logits;
+    a.norm = norm ? 1 : 0;
+    a.ids_out = ids_out;
+    a.w_out = w_out;
+    return launch_layer<ROUTE_LOGITS>(a, mxh::as_stream(stream));
 }

@@ -143,4 +143,82 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
+// Reduction over the wave, result in every lane: DPP within rows of 16 lanes
+// (quad xor 1, xor 2, half-row mirror, row mirror: each step combines
+// disjoint lane sets, so every lane ends with its row's total), then the four
+// row results.  For the maximum, NaN inputs are ignored (maxNum), so NaN can
+// mark "no value".
+template <bool MAX>
+__device__ __forceinline__ float wave_reduce_dpp(float v) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+    return op(op(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))),
+              op(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48))));
+}
+
+// Router top-k of one row by one wave (runtime/model_runner_v2.py:189-192:
+// softmax, top-k, renormalise).  The softmax is monotonic, so the k winners
+// are taken in descending logit order (k rounds of a wave maximum; exact
+// ties: lower index), which is torch.topk's order on the probabilities except
+// where two different logits round to the same probability (an order torch
+// leaves unspecified).  Weights: e_r = exp(l_r - l_max) of the winners;
+// renormalised w_r = e_r / sum_r e_r (rank order), which is
+// topv_r / sum(topv) of the probabilities; otherwise w_r = e_r / sum over
+// the row.  Lane r < k receives rank r.  The row has n <= 64*NPL entries,
+// element i*64 + lane held by the lane; k <= 64.  NaN logits are never
+// chosen.
+template <int NPL>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int n, int k, int norm, int& id, float& w) {
+    const int lane = threadIdx.x & 63;
+    const float kNone = __builtin_nanf("");
+    float v[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int idx = i * 64 + lane;
+        v[i] = idx < n ? lg[idx] : kNone;
+    }
+    float my_l = 0.0f;
+    int my_i = 0;
+    for (int r = 0; r < k; ++r) {
+        float b = v[0];
+#pragma unroll
+        for (int i = 1; i < NPL; ++i) b = fmaxf(b, v[i]);
+        const float m = wave_reduce_dpp<true>(b);
+        int win = 0;
+#pragma unroll
+        for (int i = NPL - 1; i >= 0; --i) {   // the lowest index holding m wins
+            const uint64_t bal = __ballot(v[i] == m);
+            if (bal) win = i * 64 + (int)__builtin_ctzll(bal);
+        }
+        if (lane == r) {
+            my_l = m;
+            my_i = win;
+        }
+        if ((win & 63) == lane) {
+#pragma unroll
+            for (int i = 0; i < NPL; ++i)
+                if (i == (win >> 6)) v[i] = kNone;
+        }
+    }
+    const float lmax = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(my_l), 0));
+    const float e = lane < k ? expf(my_l - lmax) : 0.0f;
+    float den = 0.0f;
+    if (norm) {
+        for (int r = 0; r < k; ++r) den += __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), r));
+    } else {
+        float s = 0.0f;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i)
+            if (i * 64 + lane < n) s += expf(lg[i * 64 + lane] - lmax);
+        den = wave_reduce_dpp<false>(s);
+    }
+    id = my_i;
+    w = e / den;
+}
+
 }  // namespace mx

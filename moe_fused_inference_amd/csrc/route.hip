@@ -15,8 +15,6 @@
 //   route_tables_kernel   the int64 pointer tables of moe_gateup_tab /
 //                         moe_down_tab (entry m*2k + proj*k + e, and m*k + e)
 //                         from the ids and the stacked expert weights.
-#include <climits>
-
 #include "mx_device.h"
 #include "mx_host.h"
 
@@ -25,18 +23,7 @@ namespace {
 constexpr int kMaxN = 1024;   // experts per row
 constexpr int kMaxK = 32;     // routed slots per row
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
-    return v;
-}
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
-    return v;
-}
-
-// NPL logits per lane: element i*64 + lane of the row.
+// NPL logits per lane: element i*64 + lane of the row (mx::wave_topk).
 template <int NPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restrict__ logits, int64_t ldl, int M,
                                                           int n, int k, int norm, int32_t* __restrict__ ids,
@@ -44,67 +31,14 @@ __global__ __launch_bounds__(256) void router_topk_kernel(const float* __restric
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= M) return;   // the whole wave; no barriers below
-    const float* lg = logits + (int64_t)row * ldl;
-    float v[NPL];
-    float mx = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int idx = i * 64 + lane;
-        v[i] = idx < n ? lg[idx] : -INFINITY;
-        mx = fmaxf(mx, v[i]);
-    }
-    mx = wave_max(mx);
-    float s = 0.0f;
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int idx = i * 64 + lane;
-        v[i] = idx < n ? expf(v[i] - mx) : 0.0f;
-        s += v[i];
-    }
-    s = wave_sum(s);
-    // probabilities; -1 marks "not a candidate" (past n, or already taken)
-#pragma unroll
-    for (int i = 0; i < NPL; ++i) v[i] = (i * 64 + lane) < n ? v[i] / s : -1.0f;
-
-    float my_p = 0.0f;
-    int my_i = 0;
-    for (int r = 0; r < k; ++r) {
-        float bp = -1.0f;   // probabilities are >= 0; taken / padding entries hold -1
-        int bi = INT_MAX;
-#pragma unroll
-        for (int i = 0; i < NPL; ++i)   // ascending index: strict > keeps the lower one on ties
-            if (v[i] > bp) {
-                bp = v[i];
-                bi = i * 64 + lane;
-            }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            const float op = __shfl_xor(bp, off);
-            const int oi = __shfl_xor(bi, off);
-            if (op > bp || (op == bp && oi < bi)) {
-                bp = op;
-                bi = oi;
-            }
-        }
-        bi = bi < n ? bi : 0;   // no candidate left (non-finite row): keep the index in range
-        if (lane == r) {
-            my_p = bp;
-            my_i = bi;
-        }
-        if ((bi & 63) == lane) {
-#pragma unroll
-            for (int i = 0; i < NPL; ++i)
-                if (i == (bi >> 6)) v[i] = -1.0f;
-        }
-    }
-    // renormalise over the k winners, summed in rank order
-    float ts = 0.0f;
-    for (int r = 0; r < k; ++r) ts += __shfl(my_p, r);
+    int id;
+    float wt;
+    mx::wave_topk<NPL>(logits + (int64_t)row * ldl, n, k, norm, id, wt);
     if (lane < k) {
         const int64_t o = (int64_t)row * k + lane;
-        ids[o] = my_i;
-        if (ids64) ids64[o] = my_i;
-        w[o] = norm ? my_p / ts : my_p;
+        ids[o] = id;
+        if (ids64) ids64[o] = id;
+        w[o] = wt;
     }
 }
 

@@ -96,6 +96,54 @@ class DecodeLayerCall:
         _lib.check(self.lib.mxfp4_moe_decode_layer(*self.args, s), "moe_decode_layer")
 
 
+class RoutedLayerCall:
+    """Pre-bound arguments of one fused-layer launch that routes itself from
+    the layer's fp32 router logits (mxfp4_moe_decode_layer_routed)."""
+
+    def __init__(self, x, logits, E, experts, out, resid, ws, norm=True, ids_out=None, w_out=None):
+        self.lib = _lib.load()
+        if logits.dtype != torch.float32 or not logits.is_cuda or not logits.is_contiguous():
+            raise RuntimeError("logits must be a contiguous cuda float32 tensor")
+        if logits.numel() != experts.n_experts:
+            raise RuntimeError(f"logits has {logits.numel()} entries, expected n_experts={experts.n_experts}")
+        if (ids_out is None) != (w_out is None):
+            raise RuntimeError("give ids_out and w_out both or neither")
+        self.keep = (x, logits, experts, out, resid, ws, ids_out, w_out)
+        self.args = (x.data_ptr(), logits.data_ptr(), int(bool(norm)),
+                     ids_out.data_ptr() if ids_out is not None else None,
+                     w_out.data_ptr() if w_out is not None else None,
+                     experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
+                     experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
+                     experts.down_wp.data_ptr(), experts.down_ws.data_ptr(),
+                     experts.n_experts, int(E), experts.hidden, experts.inter,
+                     out.data_ptr(), resid.data_ptr() if resid is not None else None,
+                     ws.data_ptr(), ws.numel())
+
+    def __call__(self, stream=None):
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        _lib.check(self.lib.mxfp4_moe_decode_layer_routed(*self.args, s), "moe_decode_layer_routed")
+
+
+def decode_layer_routed(x, logits, E, experts, norm=True, out=None, resid=None, ws=None, want_routing=False):
+    """One token through the layer, routing included: softmax / top-E /
+    renormalise of the fp32 router logits (n_experts,) computed in the same
+    launch.  Returns (out, resid) or, with want_routing, (out, resid, ids
+    int32 (E,), w fp32 (E,))."""
+    experts.check()
+    if x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise RuntimeError("x must be a cuda bfloat16 tensor")
+    x = x.reshape(-1).contiguous()
+    logits = logits.reshape(-1).float().contiguous()
+    if out is None:
+        out = torch.empty(experts.hidden, dtype=torch.float32, device=x.device)
+    if ws is None:
+        ws = workspace(E, experts.inter, experts.hidden, x.device)
+    ids = torch.empty(E, dtype=torch.int32, device=x.device) if want_routing else None
+    w = torch.empty(E, dtype=torch.float32, device=x.device) if want_routing else None
+    RoutedLayerCall(x, logits, E, experts, out, resid, ws, norm, ids, w)()
+    return (out, resid, ids, w) if want_routing else (out, resid)
+
+
 def decode_layer(x, ids, w, experts, out=None, resid=None, ws=None):
     """x (1, H) or (H,) bf16 -> (out fp32 (H,), resid bf16 (H,) or None).
 

@@ -155,11 +155,10 @@ def token_major_tables(topi, n_tokens, k):
 
 def route_topk_np(logits, k=8, renorm=True):
     """numpy restatement of the routing of runtime/model_runner_v2.py:189-192
-    (softmax in fp32 -> top-k -> renormalise), in the device kernel's order:
-    max, exp(l - max), sum, divide; top-k descending with exact ties broken
-    towards the lower index (torch.topk leaves their order unspecified);
-    renormalisation sums the k winners in rank order.  Returns
-    (topi int64 (M, k), topv fp32 (M, k))."""
+    (softmax in fp32 -> top-k -> renormalise): max, exp(l - max), sum,
+    divide; top-k descending with exact ties broken towards the lower index
+    (torch.topk leaves their order unspecified); the renormalisation sums the
+    k winners in rank order.  Returns (topi int64 (M, k), topv fp32 (M, k))."""
     lg = np.atleast_2d(np.asarray(logits, np.float32))
     mx = lg.max(axis=-1, keepdims=True)
     e = np.exp((lg - mx).astype(np.float32)).astype(np.float32)

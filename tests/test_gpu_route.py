@@ -180,3 +180,85 @@ def test_fused_layer_device_routing_in_graph(dext):
             src = r
         log(f"  replay {rep}: device routing in the graph equals host routing")
     assert moe_layer.layer_status(wsp) == 0 and moe_layer.layer_status(hws) == 0
+
+
+@pytest.mark.parametrize("n_exp,E,H,Mi,norm", [(128, 8, 2048, 768, True), (16, 8, 1024, 256, True),
+                                               (200, 4, 512, 96, False), (9, 2, 512, 64, True)])
+def test_fused_layer_routes_itself(dext, n_exp, E, H, Mi, norm):
+    """mxfp4_moe_decode_layer_routed: the in-launch routing gives the oracle's
+    ids, and the output equals the host-routed launch with those ids and the
+    same weights, bit for bit."""
+    stack = _stack(dext, n_exp, H, Mi, seed=5100 + n_exp)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(n_exp + E)
+    ws1, ws2 = moe_layer.workspace(E, Mi, H), moe_layer.workspace(E, Mi, H)
+    for it in range(3):
+        x = torch.randn((1, H), generator=g, device=DEV).bfloat16()
+        lg = torch.randn(n_exp, generator=g, device=DEV) * 2
+        r1 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        o1, _, ids, w = moe_layer.decode_layer_routed(x, lg, E, stack, norm=norm, resid=r1, ws=ws1,
+                                                      want_routing=True)
+        torch.cuda.synchronize()
+        ti, tv = ops.route_topk_np(np_(lg)[None], E, renorm=norm)
+        assert np_(ids).tolist() == ti[0].tolist()
+        assert np.abs(np_(w) - tv[0]).max() <= W_TOL
+        r2 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        o2, _ = moe_layer.decode_layer(x, ti[0].tolist(), np_(w).tolist(), stack, resid=r2, ws=ws2)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, o2) and torch.equal(r1, r2), it
+    assert moe_layer.layer_status(ws1) == 0 and moe_layer.layer_status(ws2) == 0
+    log(f"  routed layer n={n_exp} E={E} H={H} Mi={Mi}: ids exact, output equals host routing")
+
+
+def test_fused_routed_layers_in_graph(dext):
+    """Three self-routing layers in one captured graph, replayed with fresh
+    logits copied in before each replay; every replay equals eager."""
+    n_exp, E, H, Mi, L = 32, 8, 2048, 768, 3
+    stack = _stack(dext, n_exp, H, Mi, seed=6100)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(21)
+    x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
+    logits = torch.empty((L, n_exp), dtype=torch.float32, device=DEV)
+    outs = [torch.empty(H, dtype=torch.float32, device=DEV) for _ in range(L)]
+    bufs = [torch.empty(H, dtype=torch.bfloat16, device=DEV) for _ in range(L)]
+    ids = [torch.empty(E, dtype=torch.int32, device=DEV) for _ in range(L)]
+    ws_ = [torch.empty(E, dtype=torch.float32, device=DEV) for _ in range(L)]
+    wsp = moe_layer.workspace(E, Mi, H)
+    calls, src = [], x0
+    for i in range(L):
+        calls.append(moe_layer.RoutedLayerCall(src, logits[i], E, stack, outs[i], bufs[i], wsp,
+                                               ids_out=ids[i], w_out=ws_[i]))
+        src = bufs[i]
+
+    def step():
+        for c in calls:
+            c()
+
+    logits.copy_(torch.randn((L, n_exp), generator=g, device=DEV))
+    step()
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        step()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            step()
+    torch.cuda.synchronize()
+    for rep in range(3):
+        logits.copy_(torch.randn((L, n_exp), generator=g, device=DEV))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = [o.clone() for o in outs] + [bufs[-1].clone()]
+        got_ids = [i.clone() for i in ids]
+        _ = torch.randn(1024, device=DEV).sum().item()   # unrelated eager work
+        step()
+        torch.cuda.synchronize()
+        for i in range(L):
+            assert torch.equal(got[i], outs[i]) and torch.equal(got_ids[i], ids[i]), (rep, i)
+            assert np_(ids[i]).tolist() == ops.route_topk_np(np_(logits[i])[None], E)[0][0].tolist()
+        assert torch.equal(got[-1], bufs[-1])
+        log(f"  replay {rep}: self-routing layers equal eager")
+    assert moe_layer.layer_status(wsp) == 0
