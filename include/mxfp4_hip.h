@@ -135,6 +135,33 @@ int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
                       float* out, int M, int N, void* stream);
 
 /* ---------------------------------------------------------------------
+ * Decode attention over one layer's FP8 KV cache.
+ * Replaces mxfp4v2::launch_attn_decode_v2 (src/ext/mxfp4_decode.cu:366-430),
+ * bound as `attn_decode` (src/ext/mxfp4_decode_binding.cpp:213-230).
+ *   q        bf16 (M, Hq, D), D = 128, Hq = G*Hkv with G in {1,2,4,8,16}
+ *   kvk/kvv  cache bytes (max_pos, Hkv, D) in the reference's E4M3 codec
+ *            (kvk 16-byte aligned)
+ *   dpos     device int32: base position; token m sits at dpos+m and
+ *            attends to positions 0..dpos+m (rows outside [0, max_pos) are
+ *            skipped, as in the reference); read on the device, so a
+ *            captured graph follows updates of it
+ *   sc       f32 (M, Hq, max_pos) scratch; receives the raw scores q.k
+ *   o        f32 (M, Hq, D): softmax(q.k / sqrt(D)) . v
+ */
+int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
+                      float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos, void* stream);
+
+/* ---------------------------------------------------------------------
+ * KV write: k, v bf16 (M, Hkv, D) -> the reference's E4M3 bytes (rounding
+ * half away from zero, >= 248 saturating to 0x7F) at rows dpos+m < max_pos
+ * of kvk / kvv (max_pos, Hkv, D); nothing when dpos < 0.
+ * Replaces mxfp4v2::launch_kvwrite_v2 (src/ext/mxfp4_decode.cu:437-489),
+ * bound as `kv_write` (src/ext/mxfp4_decode_binding.cpp:161-173).
+ */
+int mxfp4_kv_write(const void* k, const void* v, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos,
+                   int M, int Hkv, int D, int max_pos, void* stream);
+
+/* ---------------------------------------------------------------------
  * Fused decode MoE layer, one launch per layer, batch 1.
  * Replaces the per-layer sequence prequant -> moe_gateup -> moe_down ->
  * moe_combine -> `x + moe.bfloat16()` of runtime/model_runner_v2.py:185-208

@@ -162,10 +162,46 @@ class DecodeExt:
         return yd
 
     def attn_decode(self, q, kvk, kvv, dpos, sc, M):
-        raise NotImplementedError("attn_decode (FP8 KV decode attention) is not part of this build yet")
+        """Decode attention over one layer's E4M3 KV cache -> f32 (M,Hq,D).
+
+        q (M,Hq,D) bf16; kvk/kvv (max_pos,Hkv,D) u8; dpos (1,) int32 on the
+        device (base position; token m attends to 0..dpos+m); sc
+        (M,Hq,max_pos) f32 scratch that receives the raw scores
+        (src/ext/mxfp4_decode_binding.cpp:213-230)."""
+        _require(torch.is_tensor(q) and q.dim() == 3 and q.dtype == torch.bfloat16 and q.is_cuda,
+                 "q must be a cuda bf16 (M,Hq,D) tensor")
+        q = q.contiguous()
+        M = int(M)
+        _require(kvk.dtype == torch.uint8 and kvv.dtype == torch.uint8 and kvk.dim() == 3 and kvv.shape == kvk.shape,
+                 "kvk/kvv must be uint8 (max_pos,Hkv,D) tensors of one shape")
+        _require(kvk.is_contiguous() and kvv.is_contiguous(), "kvk/kvv must be contiguous")
+        _require(dpos.dtype == torch.int32 and dpos.is_cuda, "dpos must be a cuda int32 tensor")
+        Hq, D = int(q.shape[1]), int(q.shape[2])
+        max_pos, Hkv = int(kvk.shape[0]), int(kvk.shape[1])
+        _require(int(q.shape[0]) >= M, "q has fewer than M rows")
+        _require(sc.dtype == torch.float32 and sc.is_contiguous() and sc.numel() >= M * Hq * max_pos,
+                 "sc must be a contiguous f32 buffer of M*Hq*max_pos elements")
+        o = torch.empty((M, Hq, D), dtype=torch.float32, device=q.device)
+        _lib.check(self._lib.mxfp4_attn_decode(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(),
+                                               sc.data_ptr(), o.data_ptr(), M, Hq, Hkv, D, max_pos, _stream(q)),
+                   "attn_decode")
+        return o
 
     def kv_write(self, k, v, kvk, kvv, dpos, M):
-        raise NotImplementedError("kv_write (FP8 KV write) is not part of this build yet")
+        """k/v (M,Hkv,D) bf16 -> E4M3 bytes at rows dpos+m of kvk/kvv
+        (max_pos,Hkv,D) u8, in place (src/ext/mxfp4_decode_binding.cpp:161-173)."""
+        _require(torch.is_tensor(k) and torch.is_tensor(v) and k.dtype == torch.bfloat16 and v.dtype == torch.bfloat16
+                 and k.is_cuda and v.is_cuda, "k/v must be cuda bf16")
+        k, v = k.contiguous(), v.contiguous()
+        M = int(M)
+        _require(kvk.dtype == torch.uint8 and kvv.dtype == torch.uint8 and kvk.dim() == 3 and kvv.shape == kvk.shape,
+                 "kvk/kvv must be uint8 (max_pos,Hkv,D) tensors of one shape")
+        _require(kvk.is_contiguous() and kvv.is_contiguous(), "kvk/kvv must be contiguous")
+        _require(dpos.dtype == torch.int32 and dpos.is_cuda, "dpos must be a cuda int32 tensor")
+        max_pos, Hkv, D = (int(d) for d in kvk.shape)
+        _require(k.numel() >= M * Hkv * D and v.numel() >= M * Hkv * D, "k/v have fewer than M*Hkv*D elements")
+        _lib.check(self._lib.mxfp4_kv_write(k.data_ptr(), v.data_ptr(), kvk.data_ptr(), kvv.data_ptr(),
+                                            dpos.data_ptr(), M, Hkv, D, max_pos, _stream(k)), "kv_write")
 
 
 _ext = None

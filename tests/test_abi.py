@@ -90,5 +90,7 @@ def test_python_surface_checks_mirror_reference(lib):
         d.moe_combine(torch.zeros(5, 8), torch.zeros(4), 2)
     with pytest.raises(TypeError):
         d.moe_down(torch.zeros(2, 128), [w8] * 2, [w8] * 2, 2, 8, 64)  # stale 6-arg call
-    with pytest.raises(NotImplementedError):
-        d.attn_decode(None, None, None, None, None, 1)
+    with pytest.raises(RuntimeError, match="q must be a cuda bf16"):
+        d.attn_decode(torch.zeros(1, 32, 128, dtype=torch.bfloat16), None, None, None, None, 1)
+    with pytest.raises(RuntimeError, match="k/v must be cuda bf16"):
+        d.kv_write(torch.zeros(1, 4, 128), torch.zeros(1, 4, 128), None, None, None, 1)
