@@ -49,7 +49,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy", "prefill"], default=None,
+    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy", "prefill", "attn"], default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
 
@@ -271,6 +271,46 @@ def bench_gemm(torch, lext, dext, M, N, K, reps=20):
     return res
 
 
+def bench_attn(torch, dext, ctx=4096, M=1, reps=50):
+    """Config 5 attention shape: decode attention (Hq=32, Hkv=4, D=128) over one
+    layer's FP8 KV cache at context `ctx`, plus the KV write of the new token,
+    graph-captured as the reference's graph runner uses them
+    (runtime/model_runner_v3.py:98-126).  Roofline: the K and V bytes of the
+    context (HBM-bound)."""
+    Hq, Hkv, D, max_pos = 32, 4, 128, 4096
+    g = torch.Generator(device="cuda")
+    g.manual_seed(ctx)
+    kvk = torch.randint(0, 120, (max_pos, Hkv, D), generator=g, device="cuda", dtype=torch.uint8)
+    kvv = torch.randint(0, 120, (max_pos, Hkv, D), generator=g, device="cuda", dtype=torch.uint8)
+    q = torch.randn((M, Hq, D), generator=g, device="cuda").bfloat16()
+    k = torch.randn((M, Hkv, D), generator=g, device="cuda").bfloat16()
+    v = torch.randn((M, Hkv, D), generator=g, device="cuda").bfloat16()
+    dpos = torch.tensor([ctx - M], dtype=torch.int32, device="cuda")
+    sc = torch.empty((M, Hq, max_pos), dtype=torch.float32, device="cuda")
+    out = torch.empty((M, Hq, D), dtype=torch.float32, device="cuda")
+
+    def fn():
+        dext.kv_write(k, v, kvk, kvv, dpos, M)
+        out.copy_(dext.attn_decode(q, kvk, kvv, dpos, sc, M))
+
+    fn()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        fn()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=side):
+            fn()
+    torch.cuda.synchronize()
+    ms = time_graph(torch, graph, reps, 5)
+    kv_bytes = 2 * ctx * Hkv * D
+    return {"context": ctx, "M": M, "us": round(ms * 1e3, 2), "kv_bytes": kv_bytes,
+            "gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
+            "note": "kv_write + attn_decode (score + combine kernels), Hq=32 Hkv=4 D=128, graph replay"}
+
+
 def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
     """Config 4: M=9 tokens, Zipf(1.1)-biased routing over 128 experts, grouped
     drop-in path (moe_gateup + moe_down + moe_combine)."""
@@ -474,6 +514,8 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
             log(f"gemm {M}x{N}x{K}: {bench_gemm(torch, lext, dext, M, N, K)}")
     elif args.only == "prefill":
         log(f"prefill moe: {bench_prefill_moe(torch, lext, layers[2])}")
+    elif args.only == "attn":
+        log(f"attn decode: {[bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]}")
     elif args.only == "spec":
         log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
 
@@ -510,7 +552,7 @@ def main():
     ws = workspace(TOPK, MI, H, dev)
     outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    if args.only in ("dropin", "gemm", "spec", "prefill"):
+    if args.only in ("dropin", "gemm", "spec", "prefill", "attn"):
         return only_extra(args, torch, dext, lext, layers, routes, x0)
     graph, calls = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
     log("decode graph captured")
@@ -586,6 +628,9 @@ def main():
         pf = bench_prefill_moe(torch, lext, layers[2])
         extra["prefill_moe_3b"] = pf
         log(f"prefill moe (config 3b): {pf}")
+        at = [bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]
+        extra["attn_decode_cfg5"] = at
+        log(f"attn decode (config 5 shape): {at}")
 
     cpu = None
     if not args.no_cpu:

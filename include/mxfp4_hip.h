@@ -138,18 +138,23 @@ int mxfp4_moe_combine(const float* yd, int ystride, const float* w, int E,
  * Decode attention over one layer's FP8 KV cache.
  * Replaces mxfp4v2::launch_attn_decode_v2 (src/ext/mxfp4_decode.cu:366-430),
  * bound as `attn_decode` (src/ext/mxfp4_decode_binding.cpp:213-230).
- *   q        bf16 (M, Hq, D), D = 128, Hq = G*Hkv with G in {1,2,4,8,16}
- *   kvk/kvv  cache bytes (max_pos, Hkv, D) in the reference's E4M3 codec
- *            (kvk 16-byte aligned)
- *   dpos     device int32: base position; token m sits at dpos+m and
- *            attends to positions 0..dpos+m (rows outside [0, max_pos) are
- *            skipped, as in the reference); read on the device, so a
- *            captured graph follows updates of it
- *   sc       f32 (M, Hq, max_pos) scratch; receives the raw scores q.k
- *   o        f32 (M, Hq, D): softmax(q.k / sqrt(D)) . v
+ *   q          bf16 (M, Hq, D), D = 128, Hq = G*Hkv with G in {1,2,4,8,16}
+ *   kvk/kvv    cache bytes (max_pos, Hkv, D) in the reference's E4M3 codec
+ *              (kvk 16-byte aligned)
+ *   dpos       device int32: base position; token m sits at dpos+m and
+ *              attends to positions 0..dpos+m (rows outside [0, max_pos)
+ *              are skipped, as in the reference); read on the device, so a
+ *              captured graph follows updates of it
+ *   sc         f32 (M, Hq, max_pos) scratch; receives the raw scores q.k
+ *   o          f32 (M, Hq, D): softmax(q.k / sqrt(D)) . v
+ *   workspace  16-byte aligned device memory of
+ *              mxfp4_attn_decode_workspace_size(M, Hq, max_pos) bytes (the
+ *              per-64-position softmax partials; nothing persists)
  */
+size_t mxfp4_attn_decode_workspace_size(int M, int Hq, int max_pos);
 int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
-                      float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos, void* stream);
+                      float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos,
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * KV write: k, v bf16 (M, Hkv, D) -> the reference's E4M3 bytes (rounding

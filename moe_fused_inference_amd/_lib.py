@@ -36,7 +36,9 @@ SIGNATURES = {
                                       _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "mxfp4_moe_decode_layer_routed": (_c_i, [_c_p, _c_p, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                              _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
-    "mxfp4_attn_decode": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p]),
+    "mxfp4_attn_decode_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
+    "mxfp4_attn_decode": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                 _c_p, _c_sz, _c_p]),
     "mxfp4_kv_write": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_moe_group": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_route_topk": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),

@@ -182,9 +182,11 @@ class DecodeExt:
         _require(sc.dtype == torch.float32 and sc.is_contiguous() and sc.numel() >= M * Hq * max_pos,
                  "sc must be a contiguous f32 buffer of M*Hq*max_pos elements")
         o = torch.empty((M, Hq, D), dtype=torch.float32, device=q.device)
+        wsb = self._lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=q.device)
         _lib.check(self._lib.mxfp4_attn_decode(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(),
-                                               sc.data_ptr(), o.data_ptr(), M, Hq, Hkv, D, max_pos, _stream(q)),
-                   "attn_decode")
+                                               sc.data_ptr(), o.data_ptr(), M, Hq, Hkv, D, max_pos, ws.data_ptr(),
+                                               wsb, _stream(q)), "attn_decode")
         return o
 
     def kv_write(self, k, v, kvk, kvv, dpos, M):

@@ -90,9 +90,11 @@ def test_attn_decode_rows_past_the_cache_are_skipped(dext):
     sc = torch.zeros((M, Hq, max_pos), dtype=torch.float32, device=DEV)
     dpos = torch.tensor([max_pos - 1], dtype=torch.int32, device=DEV)
     lib = _lib.load()
+    wsb = lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
     _lib.check(lib.mxfp4_attn_decode(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(), sc.data_ptr(),
-                                     o.data_ptr(), M, Hq, Hkv, D, max_pos, torch.cuda.current_stream().cuda_stream),
-               "attn_decode")
+                                     o.data_ptr(), M, Hq, Hkv, D, max_pos, ws.data_ptr(), wsb,
+                                     torch.cuda.current_stream().cuda_stream), "attn_decode")
     torch.cuda.synchronize()
     assert not torch.isnan(o[0]).any() and torch.isnan(o[1:]).all()
     ref, _ = attn.attn_decode_ref(q.float().cpu().numpy(), np_(kvk), np_(kvv), max_pos - 1)
