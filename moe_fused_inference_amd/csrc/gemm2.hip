@@ -4,20 +4,27 @@
 // E8M0 32-block scales (the lin_pq contract, src/ext/mxfp4_decode.cu:135-170).
 // Used when Kp is a multiple of 256, M > 16 and the grid has at least 128 tiles.
 //
-// * Workgroup tile 256 x BN (BN = 256 here), 8 waves in 2 (M) x 4 (N); a
-//   wave owns 128 x BN/4 as 4 x BN/128 v_mfma_scale_f32_32x32x64_f8f6f4
-//   accumulators.
-// * K step BK (BK/2 bytes of each operand row; BK = 256 here).  Global -> LDS with
-//   global_load_lds_dwordx4 (no registers, no repacking): lane i of an
+// * Workgroup tile 256 x BN (BN = 256 here), NW = 8 waves in 2 (M) x 4 (N); a
+//   wave owns 128 x 64 as 4 x 2 v_mfma_scale_f32_32x32x64_f8f6f4
+//   accumulators.  (NW = 4, 128 x 128 per wave with the accumulators in AGPRs,
+//   would read a third less from LDS but does not fit the register file
+//   without spills.)
+// * K step BK (BK/2 bytes of each operand row; BK = 256 here).  Global -> LDS
+//   with buffer_load_dwordx4 ... lds (no registers, no repacking): lane i of an
 //   instruction writes LDS bytes [16i, 16i+16) of a 1 KB block of whole rows.
 //   The lane loads the global 16-byte chunk that belongs at its LDS slot under
 //   an XOR swizzle, chosen so that the 16 lanes of one ds_read_b128 phase
 //   (16 consecutive rows, one chunk each, 256 bytes over the 64 banks) hit 16
 //   different 16-byte bank groups.
 // * NSTAGE stages in a ring, one workgroup per CU: the copies of the next
-//   NSTAGE-1 steps are in flight during the MFMAs of a step.  Every wave
-//   issues the same number of copies per step, so a step's arrival is a fixed
-//   vmcnt.
+//   NSTAGE-1 steps are in flight during the MFMAs of a step.  A step's copies
+//   are spread over its four MFMA substeps (issued in one burst they held
+//   back each wave's MFMAs while the memory pipeline accepted them).  Every
+//   wave issues the same number of copies per step, so a step's arrival is a
+//   fixed vmcnt.
+// * Measured limit (MI355X): the K loop is bound by LDS bandwidth, about
+//   110 B/clk per CU: a step moves 68 KB into LDS and reads 192 KB of
+//   operands out of it, against ~1 us of MFMA work.
 // * Scales: BK/32 bytes per row per step, loaded the same way (4 bytes per
 //   lane) and permuted once per step (v_perm_b32) so that op_sel = ks selects
 //   the byte of K-substep ks.
@@ -30,9 +37,8 @@
 namespace {
 
 constexpr int BM = 256;
-constexpr int NTHREADS = 512;
 
-template <int BN, int BK>
+template <int BN, int BK, int NW>
 struct Tile {
     static constexpr int ROWB = BK / 2;                   // data bytes per row per step
     static constexpr int CPR = ROWB / 16;                 // 16-byte chunks per row
@@ -43,14 +49,18 @@ struct Tile {
     static constexpr int W_BYTES = BN * ROWB;
     static constexpr int S_BYTES = (BM + BN) * SCB;
     static constexpr int STAGE = A_BYTES + W_BYTES + S_BYTES;
-    static constexpr int TN = BN / 128;                   // 32-col accumulator tiles per wave
-    static constexpr int A_CP = A_BYTES / 1024 / 8;       // A copies per wave per step
-    static constexpr int W_CP = W_BYTES / 1024 / 8;
+    static constexpr int NTHREADS = 64 * NW;
+    static constexpr int WN_W = NW / 2;                   // waves along N (2 along M)
+    static constexpr int WCOLS = BN / WN_W;               // columns per wave
+    static constexpr int TN = WCOLS / 32;                 // 32-col accumulator tiles per wave
+    static constexpr int A_CP = A_BYTES / 1024 / NW;      // A copies per wave per step
+    static constexpr int W_CP = W_BYTES / 1024 / NW;
     static constexpr int S_Q = S_BYTES / 256;             // scale copies (4 bytes x 64 lanes)
-    static constexpr int S_CP = (S_Q + 7) / 8;
+    static constexpr int S_CP = (S_Q + NW - 1) / NW;
     static constexpr int COPIES = A_CP + W_CP + S_CP;
     static_assert(CPR == 4 || CPR == 8, "BK 128 or 256");
-    static_assert(A_BYTES % 8192 == 0 && W_BYTES % 8192 == 0 && S_BYTES % 256 == 0, "copy split");
+    static_assert(A_BYTES % (1024 * NW) == 0 && W_BYTES % (1024 * NW) == 0 && S_BYTES % 256 == 0, "copy split");
+    static_assert(NW == 4 || NW == 8, "4 or 8 waves");
 };
 
 struct G2Args {
@@ -70,23 +80,42 @@ struct G2Args {
 // own wait insertion treats any pending LDS copy as aliasing every later LDS
 // read and would wait for all of them (vmcnt(0)) before the first operand read
 // of a step, collapsing the stage ring.  The copies are waited for explicitly
-// (s_waitcnt vmcnt(n) before each step's barrier).  The LDS address goes in M0,
+// (s_waitcnt vmcnt(n) before each step's barrier).  They are buffer loads with
+// an LDS destination: the tile's base and extent sit in a scalar buffer
+// descriptor (rows past the operand's end read as zero), each copy's row block
+// and K offset in the scalar soffset, so a lane keeps one 32-bit offset per
+// operand instead of a 64-bit address per copy.  The LDS address goes in M0,
 // which is saved and restored around the copy.
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
 __device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
 }
-__device__ __forceinline__ void dma16(const void* src, uint8_t* dst) {
+// Descriptor of `bytes` bytes at `base` (clamped to >= 0), in SGPRs.
+__device__ __forceinline__ v4u buf_rsrc(const uint8_t* base, int64_t bytes) {
+    const uint64_t a = (uint64_t)(uintptr_t)base;
+    const uint32_t n = bytes > 0 ? (uint32_t)bytes : 0u;
+    v4u r;
+    r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu);
+    r.z = __builtin_amdgcn_readfirstlane(n);
+    r.w = 0x00020000u;
+    return r;
+}
+__device__ __forceinline__ void dma16(uint32_t voff, v4u rs, uint32_t soff, uint32_t dst) {
     uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(dst)))
+                 : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(dst)), "s"(rs),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
                  : "memory");
 }
-__device__ __forceinline__ void dma4(const void* src, uint8_t* dst) {
+__device__ __forceinline__ void dma4(uint32_t voff, v4u rs, uint32_t soff, uint32_t dst) {
     uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %1, off\n\ts_mov_b32 m0, %0"
+    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %1, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
                  : "=&s"(saved)
-                 : "v"(src), "s"(__builtin_amdgcn_readfirstlane(lds_addr(dst)))
+                 : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(dst)), "s"(rs),
+                   "s"(__builtin_amdgcn_readfirstlane(soff))
                  : "memory");
 }
 
@@ -102,45 +131,87 @@ __device__ __forceinline__ int swz_key(int r) {
     else return ((r >> 1) ^ (r >> 2)) & 3;
 }
 
-// Issues the global -> LDS copies of K-step k0 (elements) into stage `buf`:
-// Tile::COPIES instructions per wave.
-template <int BN, int BK>
-__device__ __forceinline__ void issue_stage(const G2Args& g, uint8_t* buf, int m0, int n0, int k0) {
-    using T = Tile<BN, BK>;
+// Per-tile copy state: descriptors of the tile's A / W rows and scale rows,
+// and the lane's byte offsets within them.
+struct CopyState {
+    v4u ra, rw, rsa, rsw;
+    uint32_t va[2], vw[2];   // lane offset of A / W copies with an even / odd index
+    uint32_t vs;             // lane offset of scale copies
+};
+
+template <int BN, int BK, int NW>
+__device__ __forceinline__ CopyState copy_state(const G2Args& g, int m0, int n0) {
+    using T = Tile<BN, BK, NW>;
     const int w = threadIdx.x >> 6;
     const int l = threadIdx.x & 63;
-    const int cbytes = g.Kp >> 1;
-    const int nch = g.Kp >> 5;
-    const int lrow = l / T::CPR;
-    const int slot = l % T::CPR;
+    const int64_t cbytes = g.Kp >> 1, nch = g.Kp >> 5;
+    CopyState c;
+    c.ra = buf_rsrc(g.aq + m0 * cbytes, (int64_t)(g.M - m0) * cbytes);
+    c.rw = buf_rsrc(g.wp + n0 * cbytes, (int64_t)(g.N - n0) * cbytes);
+    c.rsa = buf_rsrc(g.as + m0 * nch, (int64_t)(g.M - m0) * nch);
+    c.rsw = buf_rsrc(g.ws + n0 * nch, (int64_t)(g.N - n0) * nch);
+    const int lrow = l / T::CPR, slot = l % T::CPR;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        // copy j of the wave covers rows (w*CP + j)*RPB + lrow; with an even
+        // CP the swizzle key (row mod 16) depends on j only through its parity
+        const int ra = (w * T::A_CP + p) * T::RPB + lrow;
+        const int rw = (w * T::W_CP + p) * T::RPB + lrow;
+        c.va[p] = (uint32_t)(ra * cbytes + ((slot ^ swz_key<T::CPR>(ra)) << 4)) - (uint32_t)(p * T::RPB * cbytes);
+        c.vw[p] = (uint32_t)(rw * cbytes + ((slot ^ swz_key<T::CPR>(rw)) << 4)) - (uint32_t)(p * T::RPB * cbytes);
+    }
+    constexpr int LPR = T::SCB / 4;   // lanes per scale row
+    c.vs = (uint32_t)((l / LPR) * nch + 4 * (l % LPR));
+    return c;
+}
+
+// The global -> LDS copies of K-step k0 (elements) into stage `buf`, in KS
+// parts: part q issues the copies c with c % KS == q of the wave's
+// Tile::COPIES (A blocks, then W blocks, then scales), so that the copies of
+// the next step are spread over the MFMA substeps of this one (a wave issues
+// in order, so copies issued in one burst hold back its MFMAs while the
+// memory pipeline accepts them).
+template <int BN, int BK, int NW>
+__device__ __forceinline__ void issue_part(const G2Args& g, const CopyState& c, uint32_t buf, int k0, int part) {
+    using T = Tile<BN, BK, NW>;
+    static_assert(T::A_CP % 2 == 0 && T::W_CP % 2 == 0, "even copy counts (swizzle key parity)");
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar selects below
+    const uint32_t cbytes = g.Kp >> 1, nch = g.Kp >> 5;
 #pragma unroll
     for (int j = 0; j < T::A_CP; ++j) {
-        const int blk = w * T::A_CP + j;
-        const int row = blk * T::RPB + lrow;
-        const int c = slot ^ swz_key<T::CPR>(row);
-        dma16(g.aq + (int64_t)min(m0 + row, g.M - 1) * cbytes + (k0 >> 1) + c * 16, buf + blk * 1024);
+        if (j % T::KS != part) continue;
+        const int blk = w * T::A_CP + j;   // c.va holds the wave's first block; soffset adds block j
+        dma16(c.va[j & 1], c.ra, (uint32_t)(j * T::RPB) * cbytes + (k0 >> 1), buf + blk * 1024);
     }
 #pragma unroll
     for (int j = 0; j < T::W_CP; ++j) {
+        if ((T::A_CP + j) % T::KS != part) continue;
         const int blk = w * T::W_CP + j;
-        const int row = blk * T::RPB + lrow;
-        const int c = slot ^ swz_key<T::CPR>(row);
-        dma16(g.wp + (int64_t)min(n0 + row, g.N - 1) * cbytes + (k0 >> 1) + c * 16,
-              buf + T::A_BYTES + blk * 1024);
+        dma16(c.vw[j & 1], c.rw, (uint32_t)(j * T::RPB) * cbytes + (k0 >> 1), buf + T::A_BYTES + blk * 1024);
     }
     // scales: rows 0..BM-1 of A then 0..BN-1 of W, SCB bytes each, 4 bytes a
     // lane; waves past the last copy rewrite an earlier one (same bytes)
-    constexpr int LPR = T::SCB / 4;                       // lanes per row
+    constexpr int LPR = T::SCB / 4;
 #pragma unroll
     for (int j = 0; j < T::S_CP; ++j) {
+        if ((T::A_CP + T::W_CP + j) % T::KS != part) continue;
         const int q = (w * T::S_CP + j) % T::S_Q;
-        const int wi = q * 64 + l;
-        const int row = wi / LPR;
-        const int part = wi % LPR;
-        const uint8_t* src = row < BM ? g.as + (int64_t)min(m0 + row, g.M - 1) * nch
-                                      : g.ws + (int64_t)min(n0 + row - BM, g.N - 1) * nch;
-        dma4(src + (k0 >> 5) + 4 * part, buf + T::A_BYTES + T::W_BYTES + q * 256);
+        const int row0 = q * 64 / LPR;          // first row of the copy
+        const bool is_a = row0 < BM;
+        v4u rs;
+        rs.x = __builtin_amdgcn_readfirstlane(is_a ? c.rsa.x : c.rsw.x);
+        rs.y = __builtin_amdgcn_readfirstlane(is_a ? c.rsa.y : c.rsw.y);
+        rs.z = __builtin_amdgcn_readfirstlane(is_a ? c.rsa.z : c.rsw.z);
+        rs.w = 0x00020000u;
+        dma4(c.vs, rs, (uint32_t)((is_a ? row0 : row0 - BM)) * nch + (k0 >> 5),
+             buf + T::A_BYTES + T::W_BYTES + q * 256);
     }
+}
+
+template <int BN, int BK, int NW>
+__device__ __forceinline__ void issue_stage(const G2Args& g, const CopyState& c, uint32_t buf, int k0) {
+#pragma unroll
+    for (int q = 0; q < Tile<BN, BK, NW>::KS; ++q) issue_part<BN, BK, NW>(g, c, buf, k0, q);
 }
 
 template <int OP>
@@ -166,20 +237,21 @@ __device__ __forceinline__ uint32_t scale_word(const uint8_t* srow, int h) {
 // wm*128 + i*32 + lr and wn*BN/4 + j*32 + lr, differ from lr by multiples of
 // 16, so their swizzle key is swz_key(lr): one LDS address per operand and
 // K-substep, the row offsets are immediates.
-template <int BN, int BK>
-__device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4][BN / 128]) {
-    using T = Tile<BN, BK>;
+template <int BN, int BK, int NW>
+__device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4][Tile<BN, BK, NW>::TN], const G2Args& g,
+                                          const CopyState& cs, uint32_t nxt, int k_next) {
+    using T = Tile<BN, BK, NW>;
     constexpr int TN = T::TN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = wave / T::WN_W, wn = wave % T::WN_W;
     const int lr = lane & 31;
     const int h = lane >> 5;
     const int key = swz_key<T::CPR>(lr);
     const uint8_t* la = cur + (wm * 128 + lr) * T::ROWB;
-    const uint8_t* lw = cur + T::A_BYTES + (wn * (BN / 4) + lr) * T::ROWB;
+    const uint8_t* lw = cur + T::A_BYTES + (wn * T::WCOLS + lr) * T::ROWB;
     const uint8_t* lsa = cur + T::A_BYTES + T::W_BYTES + (wm * 128 + lr) * T::SCB;
-    const uint8_t* lsw = cur + T::A_BYTES + T::W_BYTES + BM * T::SCB + (wn * (BN / 4) + lr) * T::SCB;
+    const uint8_t* lsw = cur + T::A_BYTES + T::W_BYTES + BM * T::SCB + (wn * T::WCOLS + lr) * T::SCB;
     uint32_t sa[4], sb[TN];
 #pragma unroll
     for (int i = 0; i < 4; ++i) sa[i] = scale_word<T::SCB>(lsa + i * 32 * T::SCB, h);
@@ -187,6 +259,10 @@ __device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4]
     for (int j = 0; j < TN; ++j) sb[j] = scale_word<T::SCB>(lsw + j * 32 * T::SCB, h);
 #pragma unroll
     for (int ks = 0; ks < T::KS; ++ks) {
+        // keep each substep's copies, operand reads and MFMAs together (the
+        // scheduler would otherwise hoist every copy ahead of the MFMAs)
+        __builtin_amdgcn_sched_barrier(0);
+        issue_part<BN, BK, NW>(g, cs, nxt, k_next, ks);
         const int koff = ((2 * ks + h) ^ key) << 4;
         uint4 af[4], bf[TN];
 #pragma unroll
@@ -205,9 +281,9 @@ __device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4]
     }
 }
 
-template <int BN, int BK, int NSTAGE>
-__global__ __launch_bounds__(NTHREADS, 1) void gemm2_kernel(G2Args g) {
-    using T = Tile<BN, BK>;
+template <int BN, int BK, int NSTAGE, int NW>
+__global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
+    using T = Tile<BN, BK, NW>;
     constexpr int TN = T::TN;
     static_assert(NSTAGE >= 2 && NSTAGE * T::STAGE <= 160 * 1024, "LDS ring");
     __shared__ __align__(16) uint8_t ring[NSTAGE * T::STAGE];
@@ -227,7 +303,7 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm2_kernel(G2Args g) {
     const int n0 = tn * BN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int wm = wave / T::WN_W, wn = wave % T::WN_W;
     const int lr = lane & 31;
     const int h = lane >> 5;
     const int nsteps = g.Kp / BK;
@@ -240,9 +316,10 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm2_kernel(G2Args g) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
+    const CopyState cs = copy_state<BN, BK, NW>(g, m0, n0);
+    const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));   // LDS byte address of the ring
 #pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s)
-        if (s < nsteps) issue_stage<BN, BK>(g, ring + s * T::STAGE, m0, n0, s * BK);
+    for (int s = 0; s < NSTAGE - 1; ++s) issue_stage<BN, BK, NW>(g, cs, ring_lds + s * T::STAGE, min(s, nsteps - 1) * BK);
 
     for (int it0 = 0; it0 < nsteps; it0 += NSTAGE) {
 #pragma unroll
@@ -251,32 +328,37 @@ __global__ __launch_bounds__(NTHREADS, 1) void gemm2_kernel(G2Args g) {
             if (it < nsteps) {
                 // this wave's copies of step it have landed (those of the
                 // NSTAGE-2 later steps may still be in flight) and its LDS
-                // reads of step it-1 are done; after the barrier every wave's
-                if (it + NSTAGE - 2 < nsteps)
-                    asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * T::COPIES) : "memory");
-                else
-                    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+                // reads of step it-1 are done; after the barrier every wave's.
+                // Every step issues one stage of copies (past the last step
+                // they re-read the last K slab into a free stage), so the
+                // count is the same at every step.
+                asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((NSTAGE - 2) * T::COPIES) : "memory");
                 __builtin_amdgcn_s_barrier();
                 asm volatile("" ::: "memory");
-                // refill the stage step it-1 used
-                if (it + NSTAGE - 1 < nsteps)
-                    issue_stage<BN, BK>(g, ring + ((s + NSTAGE - 1) % NSTAGE) * T::STAGE, m0, n0,
-                                        (it + NSTAGE - 1) * BK);
-                mfma_step<BN, BK>(ring + s * T::STAGE, acc);
+                // MFMAs on this step's stage; the stage step it-1 used is
+                // refilled with step it+NSTAGE-1, spread over the substeps
+                mfma_step<BN, BK, NW>(ring + s * T::STAGE, acc, g, cs, ring_lds + ((s + NSTAGE - 1) % NSTAGE) * T::STAGE,
+                                  min(it + NSTAGE - 1, nsteps - 1) * BK);
             }
         }
     }
 
+    // the copies issued past the last step must land before the workgroup's
+    // LDS can be handed to another workgroup
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) mx::pin(acc[i][j]);
+        for (int j = 0; j < TN; ++j) {
+            if constexpr (NW == 4) mx::pin_acc(acc[i][j]);
+            else mx::pin(acc[i][j]);
+        }
     // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
-            const int col = n0 + wn * (BN / 4) + j * 32 + lr;
+            const int col = n0 + wn * T::WCOLS + j * 32 + lr;
             if (col >= g.N) continue;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -311,10 +393,12 @@ namespace mxh {
 // 128 x 128 register-staged GEMM; 1024 x 4096 x 2048, 64 tiles, is faster there).
 bool lin_pq_gemm2_supported(int M, int N, int Kp) {
     const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + 255) / 256);
-    return M > 16 && N > 0 && Kp >= 256 && (Kp % 256) == 0 && tiles >= 128;
+    // buffer descriptors address each operand with 32-bit byte offsets
+    const bool fits = (int64_t)M * (Kp / 2) < (1ll << 32) && (int64_t)N * (Kp / 2) < (1ll << 32);
+    return M > 16 && N > 0 && Kp >= 256 && (Kp % 256) == 0 && tiles >= 128 && fits;
 }
 
-template <int BN, int BK, int NSTAGE>
+template <int BN, int BK, int NSTAGE, int NW>
 int launch_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc, float* y, int M, int N,
                  int Kp, hipStream_t st) {
     MXH_REQUIRE(Kp % BK == 0, "lin_pq_gemm2: Kp=%d is not a multiple of %d", Kp, BK);
@@ -322,7 +406,7 @@ int launch_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const
     g.tiles_m = (M + BM - 1) / BM;
     g.tiles_n = (N + BN - 1) / BN;
     xcd_blocks(g);
-    hipLaunchKernelGGL((gemm2_kernel<BN, BK, NSTAGE>), dim3(8 * g.per_xcd), dim3(NTHREADS), 0, st, g);
+    hipLaunchKernelGGL((gemm2_kernel<BN, BK, NSTAGE, NW>), dim3(8 * g.per_xcd), dim3(64 * NW), 0, st, g);
     return launch_status("lin_pq_gemm2");
 }
 
@@ -332,6 +416,6 @@ int lin_pq_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const
                 "lin_pq: packed operands must be 16-byte aligned");
     MXH_REQUIRE(((uintptr_t)xsc & 3) == 0 && ((uintptr_t)wsc & 3) == 0,
                 "lin_pq: scale rows must be 4-byte aligned");
-    return launch_gemm2<256, 256, 2>(xq, xsc, wp, wsc, y, M, N, Kp, st);
+    return launch_gemm2<256, 256, 2, 8>(xq, xsc, wp, wsc, y, M, N, Kp, st);
 }
 }  // namespace mxh

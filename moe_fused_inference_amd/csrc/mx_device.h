@@ -121,6 +121,9 @@ __device__ __forceinline__ v16f mfma32_fp4(uint4 a, uint4 b, v16f c, uint32_t sa
 // value, so the chain must complete before any lane-dependent branch.
 __device__ __forceinline__ void pin(v4f& v) { asm volatile("" : "+v"(v)); }
 __device__ __forceinline__ void pin(v16f& v) { asm volatile("" : "+v"(v)); }
+// The same for accumulators kept in AGPRs (one wave per SIMD, 256 AGPRs of
+// accumulators): pinning them to VGPRs would force copies through the loop.
+__device__ __forceinline__ void pin_acc(v16f& v) { asm volatile("" : "+a"(v)); }
 
 // ---------------------------------------------------------------- misc
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
