@@ -31,6 +31,7 @@
 // * XCD-aware order: workgroup b runs on XCD b % 8; each XCD gets a compact
 //   block of tiles (a few tile rows by a few tile columns), so the A and W
 //   K-slabs of one step are fetched into that XCD's L2 once and shared.
+#include "lds_dma.h"
 #include "mx_device.h"
 #include "mx_host.h"
 
@@ -76,48 +77,11 @@ struct G2Args {
     int per_xcd;        // workgroups per XCD (grid = 8 * per_xcd)
 };
 
-// Global -> LDS copies, written as inline asm on purpose: the compiler's
-// own wait insertion treats any pending LDS copy as aliasing every later LDS
-// read and would wait for all of them (vmcnt(0)) before the first operand read
-// of a step, collapsing the stage ring.  The copies are waited for explicitly
-// (s_waitcnt vmcnt(n) before each step's barrier).  They are buffer loads with
-// an LDS destination: the tile's base and extent sit in a scalar buffer
-// descriptor (rows past the operand's end read as zero), each copy's row block
-// and K offset in the scalar soffset, so a lane keeps one 32-bit offset per
-// operand instead of a 64-bit address per copy.  The LDS address goes in M0,
-// which is saved and restored around the copy.
-typedef uint32_t v4u __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ uint32_t lds_addr(const uint8_t* p) {
-    return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) uint8_t*)p;
-}
-// Descriptor of `bytes` bytes at `base` (clamped to >= 0), in SGPRs.
-__device__ __forceinline__ v4u buf_rsrc(const uint8_t* base, int64_t bytes) {
-    const uint64_t a = (uint64_t)(uintptr_t)base;
-    const uint32_t n = bytes > 0 ? (uint32_t)bytes : 0u;
-    v4u r;
-    r.x = __builtin_amdgcn_readfirstlane((uint32_t)a);
-    r.y = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xFFFFu);
-    r.z = __builtin_amdgcn_readfirstlane(n);
-    r.w = 0x00020000u;
-    return r;
-}
-__device__ __forceinline__ void dma16(uint32_t voff, v4u rs, uint32_t soff, uint32_t dst) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(dst)), "s"(rs),
-                   "s"(__builtin_amdgcn_readfirstlane(soff))
-                 : "memory");
-}
-__device__ __forceinline__ void dma4(uint32_t voff, v4u rs, uint32_t soff, uint32_t dst) {
-    uint32_t saved;
-    asm volatile("s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dword %1, %3, %4 offen lds\n\ts_mov_b32 m0, %0"
-                 : "=&s"(saved)
-                 : "v"(voff), "s"(__builtin_amdgcn_readfirstlane(dst)), "s"(rs),
-                   "s"(__builtin_amdgcn_readfirstlane(soff))
-                 : "memory");
-}
+using mx::buf_rsrc;
+using mx::dma16;
+using mx::dma4;
+using mx::lds_addr;
+using mx::v4u;
 
 // Swizzle of row r: the LDS slot of logical chunk c is c ^ swz_key(r).  A
 // ds_read_b128 phase covers 16 consecutive rows (16-aligned) at one logical
@@ -127,7 +91,7 @@ __device__ __forceinline__ void dma4(uint32_t voff, v4u rs, uint32_t soff, uint3
 // The copies write whole 1 KB blocks, so they never conflict.
 template <int CPR>
 __device__ __forceinline__ int swz_key(int r) {
-    if constexpr (CPR == 8) return (r & 7) ^ ((r >> 3) & 1);
+    if constexpr (CPR == 8) return mx::swz_key128(r);
     else return ((r >> 1) ^ (r >> 2)) & 3;
 }
 
