@@ -222,6 +222,45 @@ int mxfp4_moe_decode_layer_routed(const void* x, const float* logits, int norm, 
                                   void* stream);
 
 /* ---------------------------------------------------------------------
+ * A run of consecutive decode MoE layers in one launch (batch 1).  No single
+ * reference entry point: it replaces the per-layer loop of
+ * runtime/model_runner_v2.py:185-208 (prequant -> moe_gateup -> moe_down ->
+ * moe_combine -> x + moe.bfloat16(), kernels src/ext/mxfp4_decode.cu:24-50,
+ * 177-299) over layers 0..n_layers-1 when every layer's routing is known
+ * before the launch, as in a stack of MoE layers with pre-drawn router
+ * logits.  For each layer l, with e = ids[l][s]:
+ *   y_l = sum_s w[l][s] * down_e(silu(gate_e x_l) * up_e x_l)  (fp32, as
+ *   mxfp4_moe_decode_layer computes it), x_{l+1} = bf16(x_l + bf16(y_l)).
+ *   x            bf16 (H) input of layer 0, 16-byte aligned
+ *   ids, w       int32 / fp32 (n_layers, E) device arrays
+ *   layer_table  device array of n_layers records of six pointers
+ *                {gate_wp, up_wp, down_wp, gate_ws, up_ws, down_ws}, each
+ *                the layer's experts stacked as for mxfp4_moe_decode_layer
+ *   x_out        bf16 (H): x_{n_layers}
+ *   x_all, y_all optional bf16 / fp32 (n_layers, H): x_{l+1} and y_l of
+ *                every layer, or NULL
+ *   strict       0: layer l+1's weights are fetched while layer l runs;
+ *                1: a layer's weights are fetched only once its x is
+ *                complete (the timing of routing that depends on x)
+ *   workspace    mxfp4_decode_stack_workspace_size(E, H, Mi) bytes, 256-byte
+ *                aligned, initialised once by mxfp4_decode_stack_reset; it
+ *                needs no reset between launches or graph replays.
+ * The launch's E*Mi/32 + H/32 workgroups (256 at E=8, H=2048, Mi=768) run
+ * one per CU and must all be resident at once: the call fails with
+ * MXFP4_EINVAL when the GPU has fewer CUs, and no other kernel may occupy
+ * the GPU meanwhile.  Every internal wait is bounded and an expired one is
+ * reported by mxfp4_decode_stack_status.  Results are bit-identical to
+ * n_layers chained mxfp4_moe_decode_layer launches.  Other limits as
+ * mxfp4_moe_decode_layer.
+ */
+size_t mxfp4_decode_stack_workspace_size(int E, int H, int Mi);
+int mxfp4_decode_stack_reset(void* workspace, int E, int H, int Mi, void* stream);
+int mxfp4_decode_stack_status(const void* workspace, int* error_flag);
+int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const float* w, const void* layer_table,
+                           int n_layers, int n_experts, int E, int H, int Mi, void* x_out, void* x_all,
+                           float* y_all, int strict, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
  * Token -> expert grouping (the bookkeeping of torch.where(topi == e) in
  * runtime/model_runner_v2.py:111 and of the token-major tables :279-286).
  * topi int64 (T, topk) device ids.  Writes counts[e] (pairs routed to e),

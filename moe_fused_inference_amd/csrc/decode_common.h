@@ -1,0 +1,137 @@
+// decode_common.h -- activation splitting and word-exchange constants shared by the
+// fused decode kernels (one layer per launch, and several layers per launch).
+//
+// There is no bf16 x FP4 MFMA, so a bf16 (or fp32) activation is split into
+// kTerms E4M3 terms hi + mid + lo, each with its own E8M0 32-block scale, that
+// sum back to the value to about 12 significant bits (exactly for bf16).  The
+// terms are rows 0..2 of the A operand of v_mfma_scale_f32_16x16x128_f8f6f4.
+#pragma once
+#include "mx_device.h"
+
+namespace dl {
+
+constexpr int kSpinLimit = 1 << 22;   // polls of one word (~0.2 s)
+constexpr int kTerms = 3;             // E4M3 terms per activation value
+constexpr int kMaxE = 8;
+constexpr int kRecWords = 32;         // words per (slot, 32-block) record of h: one per value,
+                                      // bytes 0..2 = its E4M3 terms, byte 3 of words 0..2 = the terms' codes
+constexpr uint32_t kEmpty = 0xBADBAD7Fu;  // "no value yet": byte 0 is the E4M3 NaN code, which the term-0
+                                          // byte of a finite value never is
+
+// E8M0 code of the smallest 2^e with amax <= 448*2^e (E4M3 range), e in
+// [-127, 127]; zero blocks get 127.
+__device__ __forceinline__ uint32_t e4m3_block_code(float amax) {
+    if (!(amax > 0.0f)) return 127u;
+    uint32_t bits = __float_as_uint(amax);
+    int ex = (int)(bits >> 23);
+    uint32_t frac = bits & 0x7FFFFFu;
+    int x;
+    if (ex == 0) {
+        int p = 31 - __clz((int)frac);
+        x = p - 149;
+        frac = (frac << (23 - p)) & 0x7FFFFFu;
+    } else {
+        x = ex - 127;
+    }
+    int e = (frac <= 0x600000u) ? x - 8 : x - 7;  // (1+f) <= 1.75 -> 448 fits
+    e = e < -127 ? -127 : (e > 127 ? 127 : e);
+    return (uint32_t)(e + 127);
+}
+
+__device__ __forceinline__ float e8m0_value(uint32_t code) {
+    return code > 0u ? __uint_as_float(code << 23) : __uint_as_float(0x00400000u);
+}
+
+// max over the 4 lanes of a quad (DPP quad permutes: no LDS round trip)
+__device__ __forceinline__ float quad_max(float v) {
+    const float a = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // xor 1
+    v = fmaxf(v, a);
+    const float b = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // xor 2
+    return fmaxf(v, b);
+}
+
+// Splits 8 consecutive values of a 32-block (4 lanes per block, lane quad
+// aligned) into kTerms E4M3 terms: word8[t] receives the 8 E4M3 bytes of term
+// t and codes (byte t) the term's E8M0 scale code.  Each term is the E4M3
+// rounding of what the previous terms left over, so the terms sum to the value
+// up to the last term's rounding (exact for bf16 inputs).
+__device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint32_t& codes) {
+    codes = 0;
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+        float am = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
+        am = quad_max(am);
+        const uint32_t code = e4m3_block_code(am);
+        const float sc = e8m0_value(code);
+        uint32_t word[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            mx::v2s p = {0, 0};
+            p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v[4 * h + 0], v[4 * h + 1], sc, false);
+            p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v[4 * h + 2], v[4 * h + 3], sc, true);
+            word[h] = ((uint32_t)(uint16_t)p[0]) | ((uint32_t)(uint16_t)p[1] << 16);
+            typedef float v2f __attribute__((ext_vector_type(2)));
+            const v2f d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word[h], sc, false);
+            const v2f d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word[h], sc, true);
+            v[4 * h + 0] -= d0[0];
+            v[4 * h + 1] -= d0[1];
+            v[4 * h + 2] -= d1[0];
+            v[4 * h + 3] -= d1[1];
+        }
+        word8[t] = (uint64_t)word[0] | ((uint64_t)word[1] << 32);
+        codes |= code << (8 * t);
+    }
+}
+
+// max over lanes 0..15 and over 16..31 (each row of 16 lanes), then of both
+// rows, for a value held by lanes 0..31: DPP within rows, readlane across.
+__device__ __forceinline__ float max32(float v) {
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));   // quad xor 1
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));   // quad xor 2
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));  // row half-mirror
+    v = fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));  // row mirror
+    return fmaxf(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
+                 __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16)));
+}
+
+// Splits a 32-block held one value per lane (lanes 0..31) into kTerms E4M3
+// terms, as split8 does: returns the lane's term bytes (byte t = term t) and
+// the block's codes (byte t = E8M0 code of term t, the same in every lane).
+__device__ __forceinline__ uint32_t split32(float v, uint32_t& codes) {
+    uint32_t bytes = 0;
+    codes = 0;
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+        const uint32_t code = e4m3_block_code(max32(__builtin_fabsf(v)));
+        const float sc = e8m0_value(code);
+        mx::v2s p = {0, 0};
+        p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v, 0.0f, sc, false);
+        const uint32_t b = (uint32_t)(uint16_t)p[0] & 0xFFu;
+        typedef float v2f __attribute__((ext_vector_type(2)));
+        const v2f d = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(b, sc, false);
+        v -= d[0];
+        bytes |= b << (8 * t);
+        codes |= code << (8 * t);
+    }
+    return bytes;
+}
+
+// Unconditional load from an always-valid (clamped) address, value selected
+// afterwards: keeps every load of a phase in one basic block so the compiler
+// can wait for exactly the loads a computation needs.
+template <typename T>
+__device__ __forceinline__ T ld_sel(const T* p, bool ok, T zero) {
+    const T v = *p;
+    return ok ? v : zero;
+}
+
+typedef uint32_t v4u __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ mx::v8i cat8(uint4 lo, uint4 hi) {
+    mx::v8i a = {(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+    return a;
+}
+
+}  // namespace dl

@@ -172,6 +172,104 @@ def layer_status(ws):
     return flag.value
 
 
+# ----------------------------------------------------------------------------- layer stacks
+class LayerStack:
+    """Consecutive MoE layers (a list of StackedExperts of one shape) for
+    mxfp4_moe_decode_stack: holds the device table of each layer's six
+    stacked weight pointers {gate_wp, up_wp, down_wp, gate_ws, up_ws, down_ws}."""
+
+    def __init__(self, layers, device="cuda"):
+        if not layers:
+            raise RuntimeError("LayerStack needs at least one layer")
+        for lay in layers:
+            lay.check()
+        shape = (layers[0].n_experts, layers[0].hidden, layers[0].inter)
+        if any((l.n_experts, l.hidden, l.inter) != shape for l in layers):
+            raise RuntimeError("all layers of a stack must have the same (n_experts, H, Mi)")
+        self.layers = list(layers)
+        self.n_experts, self.hidden, self.inter = shape
+        rows = [[l.gate_wp.data_ptr(), l.up_wp.data_ptr(), l.down_wp.data_ptr(),
+                 l.gate_ws.data_ptr(), l.up_ws.data_ptr(), l.down_ws.data_ptr()] for l in layers]
+        self.table = torch.tensor(rows, dtype=torch.int64).to(device)
+
+    def __len__(self):
+        return len(self.layers)
+
+
+def stack_workspace(E, H, Mi, device="cuda"):
+    """Workspace for decode_stack launches of shape (E, H, Mi), initialised
+    on the current stream.  Launches sharing it must be stream-ordered."""
+    lib = _lib.load()
+    n = lib.mxfp4_decode_stack_workspace_size(E, H, Mi)
+    ws = torch.empty(n, dtype=torch.uint8, device=device)
+    _lib.check(lib.mxfp4_decode_stack_reset(ws.data_ptr(), E, H, Mi, torch.cuda.current_stream().cuda_stream),
+               "decode_stack_reset")
+    return ws
+
+
+class DecodeStackCall:
+    """Pre-bound arguments of one mxfp4_moe_decode_stack launch: x through
+    every layer of `stack` with device routing ids (L, E) int32 / w (L, E)
+    fp32; x_out (H,) bf16 receives x_L; x_all (L, H) bf16 and y_all (L, H)
+    fp32 optionally receive every layer's x_{l+1} and moe output."""
+
+    def __init__(self, x, ids, w, stack, x_out, ws, x_all=None, y_all=None, strict=False):
+        self.lib = _lib.load()
+        L = len(stack)
+        if ids.dtype != torch.int32 or not ids.is_cuda or ids.dim() != 2 or ids.shape[0] != L:
+            raise RuntimeError(f"ids must be a cuda int32 tensor of shape ({L}, E)")
+        E = int(ids.shape[1])
+        if w.dtype != torch.float32 or not w.is_cuda or tuple(w.shape) != (L, E):
+            raise RuntimeError(f"w must be a cuda float32 tensor of shape ({L}, {E})")
+        if not (ids.is_contiguous() and w.is_contiguous()):
+            raise RuntimeError("ids and w must be contiguous")
+        H = stack.hidden
+        for name, t, dt, shp in (("x", x, torch.bfloat16, (H,)), ("x_out", x_out, torch.bfloat16, (H,))):
+            if t.dtype != dt or not t.is_cuda or tuple(t.reshape(-1).shape) != shp or not t.is_contiguous():
+                raise RuntimeError(f"{name} must be a contiguous cuda {dt} tensor of {shp[0]} elements")
+        if x_all is not None and (x_all.dtype != torch.bfloat16 or tuple(x_all.shape) != (L, H)
+                                  or not x_all.is_contiguous()):
+            raise RuntimeError(f"x_all must be a contiguous bf16 tensor of shape ({L}, {H})")
+        if y_all is not None and (y_all.dtype != torch.float32 or tuple(y_all.shape) != (L, H)
+                                  or not y_all.is_contiguous()):
+            raise RuntimeError(f"y_all must be a contiguous fp32 tensor of shape ({L}, {H})")
+        self.keep = (x, ids, w, stack, x_out, ws, x_all, y_all)
+        self.args = (x.data_ptr(), ids.data_ptr(), w.data_ptr(), stack.table.data_ptr(), L,
+                     stack.n_experts, E, H, stack.inter, x_out.data_ptr(),
+                     x_all.data_ptr() if x_all is not None else None,
+                     y_all.data_ptr() if y_all is not None else None,
+                     int(bool(strict)), ws.data_ptr(), ws.numel())
+
+    def __call__(self, stream=None):
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        _lib.check(self.lib.mxfp4_moe_decode_stack(*self.args, s), "moe_decode_stack")
+
+
+def decode_stack(x, ids, w, stack, ws=None, strict=False, want_all=False):
+    """x (H,) bf16 through every layer of `stack` in one launch; ids (L, E)
+    int32 / w (L, E) fp32 cuda routing.  Returns x_L (H,) bf16, or with
+    want_all (x_L, x_all (L, H) bf16, y_all (L, H) fp32)."""
+    if x.dtype != torch.bfloat16 or not x.is_cuda:
+        raise RuntimeError("x must be a cuda bfloat16 tensor")
+    x = x.reshape(-1).contiguous()
+    E = int(ids.shape[1])
+    if ws is None:
+        ws = stack_workspace(E, stack.hidden, stack.inter, x.device)
+    x_out = torch.empty_like(x)
+    x_all = torch.empty((len(stack), stack.hidden), dtype=torch.bfloat16, device=x.device) if want_all else None
+    y_all = torch.empty((len(stack), stack.hidden), dtype=torch.float32, device=x.device) if want_all else None
+    DecodeStackCall(x, ids, w, stack, x_out, ws, x_all, y_all, strict)()
+    return (x_out, x_all, y_all) if want_all else x_out
+
+
+def stack_status(ws):
+    """Error flag of the layer stack's bounded waits (0 = never expired)."""
+    lib = _lib.load()
+    flag = ctypes.c_int(0)
+    _lib.check(lib.mxfp4_decode_stack_status(ws.data_ptr(), ctypes.byref(flag)), "decode_stack_status")
+    return flag.value
+
+
 # ----------------------------------------------------------------------------- batched tokens
 def moe_group(topi, n_experts):
     """GPU token->expert grouping (mxfp4_moe_group): topi (T, k) int64 ->

@@ -43,6 +43,9 @@ def test_every_declared_symbol_is_exported(lib):
 def test_workspace_size(lib):
     assert lib.mxfp4_linear_workspace_size(4, 2048) == 4096 + 256
     assert lib.mxfp4_linear_workspace_size(0, 2048) == 0
+    # header + memos (4096 B), two h buffers of 8*24*32 words, two x buffers of 2048 words
+    assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 4096 + 2 * (6144 + 2048) * 4
+    assert lib.mxfp4_decode_stack_workspace_size(0, 2048, 768) == 0
 
 
 @pytest.mark.parametrize("call,msg", [
@@ -57,6 +60,14 @@ def test_workspace_size(lib):
     (lambda L: L.mxfp4_linear_forward(16, 0, 16, 16, 16, 2, 8, 64, 64, 256, 1, None), "workspace"),
     (lambda L: L.mxfp4_moe_gateup(16, 16, _lib.ptr_array([16, 0]), _lib.ptr_array([16, 16]), 16,
                                   1, 1, 8, 64, 64, None), "null"),
+    (lambda L: L.mxfp4_moe_decode_stack(None, 16, 16, 16, 2, 128, 8, 2048, 768, 16, None, None, 0, 256,
+                                        1 << 20, None), "null pointer"),
+    (lambda L: L.mxfp4_moe_decode_stack(16, 16, 16, 16, 2, 128, 9, 2048, 768, 16, None, None, 0, 256,
+                                        1 << 20, None), "E=9"),
+    (lambda L: L.mxfp4_moe_decode_stack(16, 16, 16, 16, 0, 128, 8, 2048, 768, 16, None, None, 0, 256,
+                                        1 << 20, None), "n_layers=0"),
+    (lambda L: L.mxfp4_moe_decode_stack(16, 16, 16, 16, 2, 128, 8, 2048, 768, 16, None, None, 0, 256,
+                                        4096, None), "workspace too small"),
 ])
 def test_argument_checks_fail_on_host(lib, call, msg):
     rc = call(lib)

@@ -1,0 +1,158 @@
+"""GPU parity of the multi-layer decode launch (mxfp4_moe_decode_stack).
+
+Two checks per case:
+  * bit-exactness against the same layers run as chained one-layer launches
+    (mxfp4_moe_decode_layer with device routing, x_{l+1} = its bf16 residual
+    output): every layer's fp32 moe output y_l and bf16 x_{l+1};
+  * every layer's y_l against the float64 dequant-to-BF16 oracle
+    (oracle.ops.decode_layer_ref, runtime/model_runner.py:128-131) on that
+    layer's own input x_l, to the north-star bound and a tighter one.
+Repeated launches with different layer counts share one workspace, so the
+buffer parity bookkeeping is exercised across launches.
+"""
+import numpy as np
+import pytest
+import torch
+
+from moe_fused_inference_amd import moe_layer
+from tests.gpu_helpers import COS_NS, DEV, REL_NS, assert_close, log, np_
+from tests.test_gpu_decode_layer import make_stack, oracle_out, routing
+
+pytestmark = pytest.mark.gpu
+COS_TIGHT, REL_TIGHT = 0.99999, 2e-3
+
+
+def stack_routes(g, n_exp, E, L):
+    ids, ws = zip(*[routing(g, n_exp, E) for _ in range(L)])
+    return torch.stack(ids).contiguous(), torch.stack(ws).contiguous()
+
+
+def chained(x0, ids, w, layers, E):
+    """The same layers as L one-layer launches; returns (x_all, y_all)."""
+    H = layers[0].hidden
+    lws = moe_layer.workspace(E, layers[0].inter, H)
+    xs, ys = [], []
+    src = x0
+    for l, lay in enumerate(layers):
+        out = torch.empty(H, dtype=torch.float32, device=DEV)
+        resid = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        moe_layer.decode_layer(src, ids[l].contiguous(), w[l].contiguous(), lay, out=out, resid=resid, ws=lws)
+        xs.append(resid)
+        ys.append(out)
+        src = resid
+    torch.cuda.synchronize()
+    assert moe_layer.layer_status(lws) == 0
+    return torch.stack(xs), torch.stack(ys)
+
+
+@pytest.mark.parametrize("n_exp,E,H,Mi", [(12, 8, 2048, 768), (6, 4, 512, 256), (5, 3, 1024, 96),
+                                          (4, 2, 1536, 160), (6, 4, 1024, 832)])
+def test_stack_matches_chained_layers_and_oracle(dext, n_exp, E, H, Mi):
+    distinct = [make_stack(dext, n_exp, H, Mi, seed=7000 + 97 * i + H + Mi) for i in range(3)]
+    g = torch.Generator(device=DEV)
+    g.manual_seed(H * 3 + Mi)
+    ws = moe_layer.stack_workspace(E, H, Mi)
+    for it, (L, strict) in enumerate([(5, False), (1, False), (4, True), (2, False)]):
+        layers = [distinct[(l + it) % 3] for l in range(L)]
+        stack = moe_layer.LayerStack(layers)
+        x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
+        ids, w = stack_routes(g, n_exp, E, L)
+        log(f"stack n={n_exp} E={E} H={H} Mi={Mi} launch {it}: L={L} strict={strict}")
+        x_out, x_all, y_all = moe_layer.decode_stack(x0, ids, w, stack, ws=ws, strict=strict, want_all=True)
+        torch.cuda.synchronize()
+        assert moe_layer.stack_status(ws) == 0
+        cx, cy = chained(x0, ids, w, layers, E)
+        assert torch.equal(y_all, cy), "moe outputs differ from chained one-layer launches"
+        assert torch.equal(x_all, cx), "residual stream differs from chained one-layer launches"
+        assert torch.equal(x_out, cx[-1])
+        for l in range(L):
+            xl = x0 if l == 0 else x_all[l - 1]
+            ref = oracle_out(layers[l], xl, ids[l].tolist(), w[l].tolist())
+            what = f"  layer {l}"
+            assert_close(np_(y_all[l]), ref, COS_NS, REL_NS, what=what)
+            assert_close(np_(y_all[l]), ref, COS_TIGHT, REL_TIGHT, what=what + " (tight)")
+
+
+def test_stack_strict_equals_prefetch(dext):
+    n_exp, E, H, Mi = 10, 8, 2048, 768
+    layers = [make_stack(dext, n_exp, H, Mi, seed=8100 + i) for i in range(2)] * 3
+    stack = moe_layer.LayerStack(layers)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(11)
+    x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
+    ids, w = stack_routes(g, n_exp, E, len(layers))
+    ws = moe_layer.stack_workspace(E, H, Mi)
+    a = moe_layer.decode_stack(x0, ids, w, stack, ws=ws, strict=False, want_all=True)
+    b = moe_layer.decode_stack(x0, ids, w, stack, ws=ws, strict=True, want_all=True)
+    torch.cuda.synchronize()
+    for u, v in zip(a, b):
+        assert torch.equal(u, v)
+    assert moe_layer.stack_status(ws) == 0
+
+
+def test_stack_graph_replays_match_eager(dext):
+    """Two stack launches (x chained through both) captured in a HIP graph and
+    replayed with eager work between replays; every replay equals eager."""
+    n_exp, E, H, Mi = 10, 8, 2048, 768
+    layers = [make_stack(dext, n_exp, H, Mi, seed=8300 + i) for i in range(3)]
+    stack = moe_layer.LayerStack(layers)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(13)
+    x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
+    r1 = stack_routes(g, n_exp, E, 3)
+    r2 = stack_routes(g, n_exp, E, 3)
+    ws = moe_layer.stack_workspace(E, H, Mi)
+    x1 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    x2 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    y2 = torch.empty((3, H), dtype=torch.float32, device=DEV)
+    calls = [moe_layer.DecodeStackCall(x0, r1[0], r1[1], stack, x1, ws),
+             moe_layer.DecodeStackCall(x1, r2[0], r2[1], stack, x2, ws, y_all=y2)]
+
+    def run():
+        for c in calls:
+            c()
+
+    run()
+    torch.cuda.synchronize()
+    eager = (x2.clone(), y2.clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        run()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(graph, stream=s):
+            run()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        x2.zero_()
+        y2.zero_()
+        _ = torch.randn(1024, device=DEV).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(x2, eager[0]) and torch.equal(y2, eager[1]), rep
+        log(f"  replay {rep} matches eager")
+    assert moe_layer.stack_status(ws) == 0
+
+
+def test_stack_rejects_bad_arguments(dext):
+    n_exp, E, H, Mi = 4, 2, 512, 64
+    lay = make_stack(dext, n_exp, H, Mi, seed=8500)
+    stack = moe_layer.LayerStack([lay, lay])
+    x0 = torch.zeros(H, dtype=torch.bfloat16, device=DEV)
+    ids = torch.zeros((2, E), dtype=torch.int32, device=DEV)
+    w = torch.zeros((2, E), dtype=torch.float32, device=DEV)
+    with pytest.raises(RuntimeError):
+        moe_layer.decode_stack(x0, ids[:1].contiguous(), w[:1].contiguous(), stack)   # L mismatch
+    with pytest.raises(RuntimeError):
+        moe_layer.decode_stack(x0, ids.long(), w, stack)
+    with pytest.raises(RuntimeError):
+        moe_layer.LayerStack([lay, make_stack(dext, n_exp, H, 96, seed=8501)])   # shapes differ
+    # 8*1024/32 + 2048/32 = 320 workgroups: more than one per CU on a 256-CU GPU
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    big = make_stack(dext, 8, 2048, 1024, seed=8502)
+    if 8 * 1024 // 32 + 2048 // 32 > n_cu:
+        with pytest.raises(RuntimeError, match="more than the"):
+            moe_layer.decode_stack(torch.zeros(2048, dtype=torch.bfloat16, device=DEV),
+                                   torch.zeros((1, 8), dtype=torch.int32, device=DEV),
+                                   torch.zeros((1, 8), dtype=torch.float32, device=DEV), moe_layer.LayerStack([big]))
