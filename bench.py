@@ -9,7 +9,12 @@ top-8); prefill MXFP4 GEMM TFLOPS"), workload = config 2:
   every step (softmax -> top-8 -> renorm), so expert choice is ~uniform and
   the 256 MB MALL cannot hold a step's 962 MB working set.
   One step = one decode token through all 48 layers (x_{L+1} = bf16(x_L + moe_L)).
-  Steps are HIP-graph replays of S_ROUTES distinct pre-drawn steps.
+  Headline path: mxfp4_moe_decode_stack, all 48 layers of a step in one launch
+  (layer l+1's experts stream while layer l runs -- the routing of every layer
+  is drawn before the step, as this config defines it).  Steps are HIP-graph
+  replays of S_ROUTES distinct pre-drawn steps.  Also reported: the same
+  launch with routing-dependent timing ("stack_strict": a layer's weights are
+  fetched only once its x is complete) and one fused launch per layer.
 
 value = algorithmic HBM bytes of one layer (8 experts x 2,506,752 B) / mean
 layer time, in GB/s.  Also reported: us/layer, tok/s, the roofline object of
@@ -49,7 +54,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "dropin", "gemm", "spec", "copy", "prefill", "attn"], default=None,
+    ap.add_argument("--only", choices=["decode", "decode1", "dropin", "gemm", "spec", "copy", "prefill", "attn"],
+                    default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
 
@@ -123,6 +129,29 @@ def make_decode_graph(torch, layers, routes, x0, ws, outs, bufs):
                 c()
     torch.cuda.synchronize()
     return graph, calls
+
+
+def make_stack_graph(torch, stack, routes, x0, ws, strict):
+    """S_ROUTES decode steps, each one mxfp4_moe_decode_stack launch over all
+    48 layers with that step's routing (device arrays), captured in a graph."""
+    from moe_fused_inference_amd.moe_layer import DecodeStackCall
+    ti, tv = routes
+    ids = ti.to("cuda").contiguous()
+    w = tv.to("cuda").contiguous()
+    outs = [torch.empty_like(x0) for _ in range(ti.shape[0])]
+    calls = [DecodeStackCall(x0, ids[s], w[s], stack, outs[s], ws, strict=strict) for s in range(ti.shape[0])]
+    for c in calls:  # eager warm-up / validation
+        c()
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            for c in calls:
+                c()
+    torch.cuda.synchronize()
+    return graph, (ids, w, outs, calls)
 
 
 def devroute_graph(torch, layers, logits_host, x0, ws, outs, bufs, routes):
@@ -491,9 +520,10 @@ def copy_reference(torch, nbytes=1 << 30, reps=4):
 
 
 def read_traffic():
-    """HBM bytes per launch of the fused decode kernel from the committed
-    counter summary (key: value lines), or None."""
-    path = os.path.join(ROOT, "profiles", "decode_layer_traffic.txt")
+    """HBM bytes per launch of the headline kernel (decode_stack_kernel, one
+    launch = 48 layers) from the committed counter summary (key: value
+    lines), or None."""
+    path = os.path.join(ROOT, "profiles", "decode_stack_traffic.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -554,33 +584,55 @@ def main():
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     if args.only in ("dropin", "gemm", "spec", "prefill", "attn"):
         return only_extra(args, torch, dext, lext, layers, routes, x0)
+    from moe_fused_inference_amd.moe_layer import LayerStack, stack_status, stack_workspace
+    stack = LayerStack(layers)
+    sws = stack_workspace(TOPK, H, MI, dev)
+    n_launch = S_ROUTES * LAYERS
+    if args.only != "decode1":
+        sgraph, skeep = make_stack_graph(torch, stack, routes, x0, sws, strict=False)
+        log("decode stack graph captured")
+        ms_replay = time_graph(torch, sgraph, args.steps, args.warmup)
+        if stack_status(sws) != 0:
+            raise RuntimeError("decode stack reported an expired wait")
+        us_layer = ms_replay * 1e3 / n_launch
+        gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
+        ms_step = us_layer * LAYERS / 1e3
+        log(f"decode stack: {us_layer:.3f} us/layer, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
+        if args.only == "decode":
+            return
     graph, calls = make_decode_graph(torch, layers, routes, x0, ws, outs, bufs)
-    log("decode graph captured")
-    # eager back-to-back launches of the same calls (no graph), for comparison
-    for c in calls[:LAYERS]:
-        c()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for c in calls:
-        c()
-    ev1.record()
-    torch.cuda.synchronize()
-    log(f"eager fused launches: {ev0.elapsed_time(ev1) * 1e3 / len(calls):.3f} us/layer")
-    ms_replay = time_graph(torch, graph, args.steps, args.warmup)
+    log("one-launch-per-layer graph captured")
+    # the stack's last step equals the eager one-layer chain of the same step, bit for bit
+    if args.only != "decode1" and not torch.equal(skeep[2][-1], bufs[(LAYERS - 1) % 2]):
+        raise RuntimeError("decode stack differs from the one-launch-per-layer chain")
+    ms_one = time_graph(torch, graph, args.steps, args.warmup)
     if layer_status(ws) != 0:
         raise RuntimeError("fused decode layer reported an expired wait")
-    n_launch = S_ROUTES * LAYERS
-    us_layer = ms_replay * 1e3 / n_launch
-    gbs = LAYER_BYTES / (us_layer * 1e-6) / 1e9
-    ms_step = us_layer * LAYERS / 1e3
-    log(f"fused decode: {us_layer:.3f} us/layer, {gbs:.1f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of peak)")
-    if args.only == "decode":
+    us_one = ms_one * 1e3 / n_launch
+    log(f"one launch per layer: {us_one:.3f} us/layer, {LAYER_BYTES / (us_one * 1e-6) / 1e9:.1f} GB/s")
+    if args.only == "decode1":
         return
-
     traffic = read_traffic()
 
-    extra = {}
+    extra = {"one_launch_per_layer": {
+        "us_per_layer": round(us_one, 3), "gbs": round(LAYER_BYTES / (us_one * 1e-6) / 1e9, 1),
+        "launches_per_layer": 1,
+        "note": "mxfp4_moe_decode_layer (decode_layer_kernel<0, 6>), one fused launch per layer, 48 launches per "
+                "step, graph-captured; the stack's results equal this chain bit for bit"}}
+    del graph, calls
+    sg2, keep2 = make_stack_graph(torch, stack, routes, x0, sws, strict=True)
+    ms_strict = time_graph(torch, sg2, max(3, args.steps // 2), 2)
+    us_strict = ms_strict * 1e3 / n_launch
+    if stack_status(sws) != 0:
+        raise RuntimeError("decode stack reported an expired wait")
+    if not all(torch.equal(a, b) for a, b in zip(keep2[2], skeep[2])):
+        raise RuntimeError("strict decode stack differs from the prefetching one")
+    extra["stack_strict"] = {
+        "us_per_layer": round(us_strict, 3), "gbs": round(LAYER_BYTES / (us_strict * 1e-6) / 1e9, 1),
+        "note": "mxfp4_moe_decode_stack with strict=1: a layer's expert weights are fetched only once its x is "
+                "complete, the timing of routing that depends on x (no cross-layer prefetch)"}
+    log(f"decode stack strict: {us_strict:.3f} us/layer")
+    del sg2, keep2
     if not args.skip_extra:
         dg = dropin_graph(torch, dext, layers, routes, x0)
         ms_d = time_graph(torch, dg, max(3, args.steps // 2), 2)
@@ -645,16 +697,19 @@ def main():
         "dtype": "mxfp4(e2m1,e8m0) weights x e4m3x3 activations -> f32",
         "data": "synthetic (seeded random-init weights and router logits)",
         "config": {"workload": "config 2: decode MoE layer, batch 1, top-8 of 128 experts, H=2048, Mi=768, "
-                               "48 resident layers (15.4 GB), fresh routing per layer, fused one-launch kernel",
+                               "48 resident layers (15.4 GB), fresh pre-drawn routing per layer, all 48 layers of "
+                               "a step in one mxfp4_moe_decode_stack launch",
                    "layers": LAYERS, "experts": N_EXP, "top_k": TOPK, "hidden": H, "moe_intermediate": MI,
                    "graph_steps_per_replay": S_ROUTES},
         "us_per_layer": round(us_layer, 3), "tok_per_s": round(1e3 / ms_step, 1),
         "layer_bytes": LAYER_BYTES, "layer_flops": LAYER_FLOPS,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "decode_layer_kernel<0, 6>",
-                     "timing": "HIP events on the launching stream around the timed graph replays / launches; "
-                               "rocprofv3 kernel-trace average of the same kernel agrees (profiles/)"},
+                     "algorithmic_bytes_per_launch": LAYERS * LAYER_BYTES,
+                     "kernel": "decode_stack_kernel<false, 6> (one launch = 48 layers; achieved and traffic "
+                               "per layer = per launch / 48)",
+                     "timing": "HIP events on the launching stream around the timed graph replays; rocprofv3 "
+                               "kernel-trace average of the same kernel agrees (profiles/)"},
         "cpu_baseline": cpu,
     }
     line.update(extra)
