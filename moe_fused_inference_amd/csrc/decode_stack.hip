@@ -29,17 +29,19 @@
 // codes in byte 3 of a record's first three words), x words carry the bf16
 // value in their low half (high half 0, so never kEmpty).  Producers store with
 // agent-scope atomic stores; consumers poll with agent-scope loads.  Each
-// value has two buffers, picked by the parity of a per-workgroup layer count
+// value has three buffers, used round robin by a per-workgroup layer count
 // ("memo", read at entry, + L stored at exit; all workgroups agree on it):
-// layer count c writes buffer c&1.  Before its first MFMA of layer c a
-// producer empties its words of buffer (c&1)^1 and waits for the stores to be
-// acknowledged (s_waitcnt vmcnt(0)), so they are visible before its next
-// publish.  That is safe: the last readers of buffer (c&1)^1 were the
-// consumers of layer c-1, which the producer has already waited for (a
-// gate/up workgroup at layer c has all of x_c, which the down workgroups
-// publish after reading h_{c-1}; a down workgroup at layer c has all of h_c,
-// which the gate/up workgroups publish after reading x_c).  No reset is
-// needed between launches.
+// layer count c publishes into buffer c%3 and then empties its words of
+// buffer (c-1)%3, which is published into again at layer c+2.  That is safe:
+// the readers of (c-1)%3 were the consumers of layer c-1, which the producer
+// has already waited for (a gate/up workgroup at layer c has all of x_c,
+// which the down workgroups publish after reading h_{c-1}; a down workgroup
+// at layer c has all of h_c, which the gate/up workgroups publish after
+// reading x_c).  Before each publish a producer waits for its earlier stores
+// (s_waitcnt vmcnt(0)), so the empties of layer c are visible before anything
+// of layer c+1 is, hence before any consumer polls (c+2)%3 -- a layer after
+// they were issued, so the wait is normally free.  No reset is needed between
+// launches.
 //
 // Co-residency.  The grid (E*Mi/32 + H/32 = 256 workgroups at the headline
 // shape) must be resident at once: every workgroup waits on others of every
@@ -64,6 +66,7 @@ constexpr int kErrOff = 256;          // int32 error flag
 constexpr int kMemoOff = 1024;        // int32 layer count per workgroup
 constexpr int kMaxWg = 768;
 constexpr int kBufOff = kMemoOff + 4 * kMaxWg;   // h buffers, then x buffers (uint32 words)
+constexpr int kNBuf = 3;              // buffers per value, used round robin by layer count
 
 struct StackLayer {
     const uint8_t* wp[3];   // gate, up, down packed data of the layer's experts (stacked)
@@ -82,8 +85,8 @@ struct StackArgs {
     int64_t wp_stride_dn, ws_stride_dn;   // bytes between experts (down)
     int n_layers, n_experts, E, H, Mi;
     int cfg;                    // expected workspace config word
-    int hwords;                 // words between the two h buffers
-    int xwords;                 // words between the two x buffers
+    int hwords;                 // words between consecutive h buffers
+    int xwords;                 // words between consecutive x buffers
     uint8_t* ws;
 };
 
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
         return;
     }
     uint32_t* hbuf = reinterpret_cast<uint32_t*>(a.ws + kBufOff);
-    uint32_t* xbuf = hbuf + 2 * a.hwords;
+    uint32_t* xbuf = hbuf + kNBuf * a.hwords;
     bool live = true;   // this thread's waits have all succeeded
 
     if (bid < nA) {
@@ -237,23 +240,15 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
         };
         if (!STRICT) load_w(0);
 
+        const int64_t w_off = ((int64_t)s * nblk_mi + jb) * kRecWords + (lane & 31);
         for (int l = 0; l < L; ++l) {
-            const int par = (c0 + l) & 1;
+            const int b = (c0 + l) % kNBuf;             // this layer's buffer
+            const int bprev = (b + kNBuf - 1) % kNBuf;  // the previous layer's
             uint4 xq = make_uint4(0, 0, 0, 0);
             if (l == 0) {
                 if (k0 < H) xq = *reinterpret_cast<const uint4*>(a.x0 + k0);
             } else {
-                live = wait_x(a, xbuf + (par ^ 1) * a.xwords, xq, live);
-            }
-            // empty this record in the other h buffer (its readers, the down
-            // workgroups of the previous layer, are done: x_l is complete) and
-            // wait for the stores before this layer's publish
-            const int64_t w_off = ((int64_t)s * nblk_mi + jb) * kRecWords + (lane & 31);
-            if (wave == 0) {
-                if (lane < 32)
-                    __hip_atomic_store(hbuf + (par ^ 1) * a.hwords + w_off, kEmpty, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                wait_stores();
+                live = wait_x(a, xbuf + bprev * a.xwords, xq, live);
             }
             if (STRICT) load_w(l);
 
@@ -317,8 +312,15 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
                 uint32_t codes;
                 const uint32_t bytes = split32(mx::silu_mul(gsum, usum), codes);
                 const uint32_t word = bytes | (j < kTerms ? ((codes >> (8 * j)) & 0xFFu) << 24 : 0u);
-                if (lane < 32)
-                    __hip_atomic_store(hbuf + par * a.hwords + w_off, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                wait_stores();   // the previous layer's empty-stores are visible before this publish
+                if (lane < 32) {
+                    __hip_atomic_store(hbuf + b * a.hwords + w_off, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    // empty this record in the previous layer's buffer (written
+                    // again two layers on; its readers, the down workgroups of
+                    // the previous layer, are done: x_l is complete)
+                    __hip_atomic_store(hbuf + bprev * a.hwords + w_off, kEmpty, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
             // The next layer's weights stream under the down phase.  Issued
             // after the publish: a burst of loads stalls the issuing wave
@@ -396,16 +398,17 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
     const int nwords = E * nblk_mi * kRecWords;
     constexpr int kGroups = (kMaxE * 4 * MS * kRecWords) / 2048;
     for (int l = 0; l < L; ++l) {
-        const int par = (c0 + l) & 1;
+        const int b = (c0 + l) % kNBuf;
+        const int bprev = (b + kNBuf - 1) % kNBuf;
         if (STRICT) {
             if (l > 0) {
                 uint4 unused;
-                live = wait_x(a, xbuf + (par ^ 1) * a.xwords, unused, live);
+                live = wait_x(a, xbuf + bprev * a.xwords, unused, live);
             }
             load_w(l);
         }
         // h_l: poll all words, unpack term bytes and codes into LDS
-        const uint32_t* cur = hbuf + par * a.hwords;
+        const uint32_t* cur = hbuf + b * a.hwords;
         {
             const __amdgpu_buffer_rsrc_t rs =
                 __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(cur), (short)0, nwords * 4, 0x00020000);
@@ -416,15 +419,6 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
                 for (int h = 0; h < 2; ++h) off[2 * k + h] = min(2048 * k + 8 * (int)threadIdx.x + 4 * h, nwords - 4) * 4;
             v4u v[2 * kGroups];
             live = poll_groups<2 * kGroups>(a, rs, off, v, live);
-            // empty these columns in the other x buffer (its readers, the
-            // gate/up workgroups of this layer, are done: h_l is complete) and
-            // wait for the stores before this layer's publish
-            if (wave == 0) {
-                if (lane < 32)
-                    __hip_atomic_store(xbuf + (par ^ 1) * a.xwords + c0c + lane, kEmpty, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                wait_stores();
-            }
 #pragma unroll
             for (int k = 0; k < kGroups; ++k) {
                 const int wi = 2048 * k + 8 * (int)threadIdx.x;
@@ -507,10 +501,15 @@ __global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
             const float yb = mx::bf16_to_f32(mx::f32_to_bf16_rne(y));
             const uint16_t xn = mx::f32_to_bf16_rne(xown + yb);
             xown = mx::bf16_to_f32(xn);
+            wait_stores();   // the previous layer's empty-stores are visible before this publish
             if (l + 1 < L)
-                __hip_atomic_store(xbuf + par * a.xwords + c, (uint32_t)xn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(xbuf + b * a.xwords + c, (uint32_t)xn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             else
                 a.x_out[c] = xn;
+            // empty these columns in the previous layer's buffer (written again
+            // two layers on; its readers, the gate/up workgroups of this layer,
+            // are done: h_l is complete)
+            __hip_atomic_store(xbuf + bprev * a.xwords + c, kEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (a.x_all) a.x_all[(int64_t)l * H + c] = xn;
             if (a.y_all) a.y_all[(int64_t)l * H + c] = y;
         }
@@ -534,14 +533,14 @@ int x_words(int H) { return (int)(align256((size_t)H * 4) / 4); }
 
 extern "C" size_t mxfp4_decode_stack_workspace_size(int E, int H, int Mi) {
     if (E <= 0 || H <= 0 || Mi <= 0) return 0;
-    return kBufOff + (size_t)2 * (h_words(E, Mi) + x_words(H)) * 4;
+    return kBufOff + (size_t)kNBuf * (h_words(E, Mi) + x_words(H)) * 4;
 }
 
 extern "C" int mxfp4_decode_stack_reset(void* workspace, int E, int H, int Mi, void* stream) {
     MXH_REQUIRE(workspace, "decode_stack_reset: null workspace");
     MXH_REQUIRE(E >= 1 && E <= kMaxE && Mi >= 32 && Mi <= 1024 && Mi % 32 == 0 && H >= 512 && H <= 2048 && H % 512 == 0,
                 "decode_stack_reset: E=%d H=%d Mi=%d out of range", E, H, Mi);
-    const int words = 2 * (h_words(E, Mi) + x_words(H));
+    const int words = kNBuf * (h_words(E, Mi) + x_words(H));
     const int n = words > kBufOff / 4 ? words : kBufOff / 4;
     hipLaunchKernelGGL(reset_stack_kernel, dim3((n + 255) / 256), dim3(256), 0, mxh::as_stream(stream),
                        static_cast<uint32_t*>(workspace), stack_cfg(E, H, Mi), words);

@@ -43,8 +43,8 @@ def test_every_declared_symbol_is_exported(lib):
 def test_workspace_size(lib):
     assert lib.mxfp4_linear_workspace_size(4, 2048) == 4096 + 256
     assert lib.mxfp4_linear_workspace_size(0, 2048) == 0
-    # header + memos (4096 B), two h buffers of 8*24*32 words, two x buffers of 2048 words
-    assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 4096 + 2 * (6144 + 2048) * 4
+    # header + memos (4096 B), three h buffers of 8*24*32 words, three x buffers of 2048 words
+    assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 4096 + 3 * (6144 + 2048) * 4
     assert lib.mxfp4_decode_stack_workspace_size(0, 2048, 768) == 0
 
 
