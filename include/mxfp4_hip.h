@@ -56,8 +56,10 @@ int mxfp4_prequant(const void* x, int64_t ldx, int M, int K, int Kp,
                    uint8_t* xq, uint8_t* xsc, void* stream);
 
 /* Same quantizer for bf16 / fp16 / fp32 rows (src_dtype = MXFP4_DT_*).
- * With round_to_f16 != 0 each element is first rounded to fp16, as the
- * reference's `forward` does (src/ext/mxfp4_binding.cpp:31). */
+ * round_to_f16 = 1: each element is first rounded to fp16, as the
+ * reference's `forward` does (src/ext/mxfp4_binding.cpp:31); 2: first
+ * rounded to bf16 (an fp32 tensor's `.to(torch.bfloat16)` before prequant,
+ * runtime/model_runner_v2.py:262-263); 0: as is. */
 int mxfp4_quantize_rows(const void* x, int src_dtype, int round_to_f16, int64_t ldx,
                         int M, int K, int Kp, uint8_t* q, uint8_t* s, void* stream);
 
@@ -259,6 +261,43 @@ int mxfp4_decode_stack_status(const void* workspace, int* error_flag);
 int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const float* w, const void* layer_table,
                            int n_layers, int n_experts, int E, int H, int Mi, void* x_out, void* x_all,
                            float* y_all, int strict, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
+ * The non-MoE ops of a decode step (the ops the reference's forward_decode / forward_batch run around the MoE,
+ * runtime/model_runner_v2.py:130-300, so a whole step runs on this library).
+ *
+ * mxfp4_embed_rows: out (M, K) bf16 = the MXFP4 rows ids[m] (int32, device)
+ * of an embedding (V, Kp/2) + (V, Kp/32), dequantized exactly:
+ * bf16(sign * E2M1 * 2^(code-127)).  Replaces dequant_rows_gpu
+ * (runtime/weight_store.py:47-65).  K a multiple of 8, out 16-byte aligned.
+ */
+int mxfp4_embed_rows(const uint8_t* wp, const uint8_t* ws, int V, int K, const int32_t* ids, int M,
+                     void* out, void* stream);
+
+/* mxfp4_rmsnorm_quant: per row m of x (M, H) bf16, optionally first
+ * x_out = bf16(x + bf16(resid)) (resid fp32 (M, H), the residual add of
+ * runtime/model_runner_v2.py:185/208), then y = rms_norm(x, w, eps) as
+ * runtime/model_runner.py:20-25 computes it (fp32 mean of squares, bf16 of
+ * x * rsqrt, times the bf16 weight, bf16) and its MXFP4 quantization yq
+ * (M, H/2) / ys (M, H/32), bit-exact to mxfp4_prequant(y).  H a multiple of
+ * 2048 up to 8192; pointers 16-byte aligned. */
+int mxfp4_rmsnorm_quant(const void* x, const float* resid, const void* w, float eps, int M, int H,
+                        void* x_out, void* y, uint8_t* yq, uint8_t* ys, void* stream);
+
+/* mxfp4_qk_norm_rope_kv: qkv fp32 (M, (Hq + 2 Hkv) * D) holds each token's q,
+ * k and v projections side by side.  For token m at position *dpos + m:
+ * q and k heads get RMSNorm with q_norm_w / k_norm_w (bf16 (D)) and the
+ * half-layout RoPE of runtime/model_runner.py:28-41 (theta), q goes to
+ * q_out (M, Hq, D) bf16, k and bf16(v) to the KV cache rows (max_pos, Hkv,
+ * D) in the reference's E4M3 byte codec (as mxfp4_kv_write).  D = 128. */
+int mxfp4_qk_norm_rope_kv(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                          float theta, const int32_t* dpos, int M, int Hq, int Hkv, int D, void* q_out,
+                          uint8_t* kvk, uint8_t* kvv, int max_pos, void* stream);
+
+/* mxfp4_argmax_advance: ids[m] = the first index of the maximum of logits
+ * row m (M, V) fp32 -- greedy decoding, runtime/decode_v2.py:71 -- and,
+ * when dpos is not NULL, *dpos += M afterwards (stream-ordered). */
+int mxfp4_argmax_advance(const float* logits, int M, int V, int32_t* ids, int32_t* dpos, void* stream);
 
 /* ---------------------------------------------------------------------
  * Token -> expert grouping (the bookkeeping of torch.where(topi == e) in

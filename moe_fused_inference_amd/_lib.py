@@ -41,6 +41,11 @@ SIGNATURES = {
     "mxfp4_decode_stack_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),
     "mxfp4_moe_decode_stack": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p,
                                       _c_i, _c_p, _c_sz, _c_p]),
+    "mxfp4_embed_rows": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p, _c_p]),
+    "mxfp4_rmsnorm_quant": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "mxfp4_qk_norm_rope_kv": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_i, _c_i, _c_i, _c_i,
+                                     _c_p, _c_p, _c_p, _c_i, _c_p]),
+    "mxfp4_argmax_advance": (_c_i, [_c_p, _c_i, _c_i, _c_p, _c_p, _c_p]),
     "mxfp4_attn_decode_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
     "mxfp4_attn_decode": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
                                  _c_p, _c_sz, _c_p]),

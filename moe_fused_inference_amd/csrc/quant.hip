@@ -56,7 +56,8 @@ __device__ __forceinline__ void load8(const void* x, int64_t base, int k0, int K
     }
 }
 
-template <int SRC, bool ROUND_F16>
+// RND: 0 none, 1 round each element to fp16 first, 2 to bf16 first.
+template <int SRC, int RND>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int64_t ldx,
                                                             int M, int K, int Kp, int vec,
                                                             uint8_t* __restrict__ q,
@@ -74,9 +75,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    if (ROUND_F16) {
+    if (RND == 1) {
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[i] = mx::round_to_f16(v[i]);
+    }
+    if (RND == 2) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(v[i]));
     }
     float am = 0.0f;
 #pragma unroll
@@ -91,12 +96,12 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
     }
 }
 
-template <int SRC, bool R16>
+template <int SRC, int RND>
 void launch_quant(const void* x, int64_t ldx, int M, int K, int Kp, int vec, uint8_t* q, uint8_t* s,
                   hipStream_t st) {
     const int64_t units = (int64_t)M * (Kp >> 3);
     const int64_t blocks = (units + 255) / 256;
-    hipLaunchKernelGGL((quantize_rows_kernel<SRC, R16>), dim3((unsigned)blocks), dim3(256), 0, st,
+    hipLaunchKernelGGL((quantize_rows_kernel<SRC, RND>), dim3((unsigned)blocks), dim3(256), 0, st,
                        x, ldx, M, K, Kp, vec, q, s);
 }
 
@@ -115,15 +120,18 @@ int quantize_rows_impl(const void* x, int src_dtype, int round_to_f16, int64_t l
     if (M == 0 || Kp == 0) return MXFP4_OK;
     const int esz = src_dtype == MXFP4_DT_F32 ? 4 : 2;
     const int vec = (((uintptr_t)x & 15) == 0) && ((ldx * esz) % 16 == 0);
-    const bool r16 = round_to_f16 != 0;
+    MXH_REQUIRE(round_to_f16 >= 0 && round_to_f16 <= 2, "quantize: rounding mode %d (0, 1 fp16, 2 bf16)", round_to_f16);
     if (src_dtype == MXFP4_DT_BF16) {
-        if (r16) launch_quant<MXFP4_DT_BF16, true>(x, ldx, M, K, Kp, vec, q, s, st);
-        else launch_quant<MXFP4_DT_BF16, false>(x, ldx, M, K, Kp, vec, q, s, st);
+        // bf16 input is already bf16
+        if (round_to_f16 == 1) launch_quant<MXFP4_DT_BF16, 1>(x, ldx, M, K, Kp, vec, q, s, st);
+        else launch_quant<MXFP4_DT_BF16, 0>(x, ldx, M, K, Kp, vec, q, s, st);
     } else if (src_dtype == MXFP4_DT_F16) {
-        launch_quant<MXFP4_DT_F16, false>(x, ldx, M, K, Kp, vec, q, s, st);
+        if (round_to_f16 == 2) launch_quant<MXFP4_DT_F16, 2>(x, ldx, M, K, Kp, vec, q, s, st);
+        else launch_quant<MXFP4_DT_F16, 0>(x, ldx, M, K, Kp, vec, q, s, st);
     } else {
-        if (r16) launch_quant<MXFP4_DT_F32, true>(x, ldx, M, K, Kp, vec, q, s, st);
-        else launch_quant<MXFP4_DT_F32, false>(x, ldx, M, K, Kp, vec, q, s, st);
+        if (round_to_f16 == 1) launch_quant<MXFP4_DT_F32, 1>(x, ldx, M, K, Kp, vec, q, s, st);
+        else if (round_to_f16 == 2) launch_quant<MXFP4_DT_F32, 2>(x, ldx, M, K, Kp, vec, q, s, st);
+        else launch_quant<MXFP4_DT_F32, 0>(x, ldx, M, K, Kp, vec, q, s, st);
     }
     return launch_status("quantize_rows");
 }

@@ -1,0 +1,312 @@
+"""A whole Qwen3-MoE-shaped decode step on this library's kernels.
+
+The reference's step (runtime/model_runner_v2.py:130-217 forward_decode for
+one token, :220-300 forward_batch for M tokens of one sequence, driven by the
+greedy loop of runtime/decode_v2.py:64-71):
+
+    x = embed_rows(ids)                                    (MXFP4 row dequant)
+    per layer:
+        hp  = rms_norm(x) -> MXFP4;  q, k, v = lin_pq(hp)   (one fused q|k|v weight)
+        q, k = rms_norm per head (q_norm, k_norm), RoPE;  k, v -> FP8 KV cache
+        o   = attn_decode(q, cache) -> bf16 -> MXFP4 -> lin_pq(o_proj)
+        x   = x + bf16(o);  hp2 = rms_norm(x) -> MXFP4;  logits = lin_pq(gate)
+        moe = softmax / top-k / renorm routing + experts + weighted combine
+        x   = x + bf16(moe)
+    logits = lin_pq(rms_norm(x));  next ids = argmax;  position += M
+
+Every op is a kernel of this library; positions and token ids live in device
+memory, so one step can be captured in a HIP graph and replayed step after
+step (DecodeStep.capture).  MoE: M = 1 uses the fused one-launch layer with
+in-kernel routing on the bf16 activations (mxfp4_moe_decode_layer_routed);
+M > 1 uses route_topk + the drop-in grouped ops on MXFP4 activations, as
+forward_batch does.  The KV cache uses the reference's E4M3 byte codec
+(kv_write / attn_decode) with no extra scale.
+"""
+import ctypes
+from dataclasses import dataclass, field
+
+import torch
+
+from . import _lib
+from .moe_layer import RoutedLayerCall, StackedExperts, workspace as layer_workspace
+
+
+@dataclass
+class ModelConfig:
+    n_layers: int = 48
+    hidden: int = 2048
+    n_heads: int = 32
+    n_kv_heads: int = 4
+    head_dim: int = 128
+    n_experts: int = 128
+    top_k: int = 8
+    moe_inter: int = 768
+    vocab: int = 151936
+    rms_eps: float = 1e-6
+    rope_theta: float = 1e6
+
+    @property
+    def qkv_rows(self):
+        return (self.n_heads + 2 * self.n_kv_heads) * self.head_dim
+
+
+@dataclass
+class Packed:
+    """An MXFP4 weight (N, K): packed nibbles (N, Kp/2) and E8M0 codes (N, Kp/32)."""
+    wp: torch.Tensor
+    ws: torch.Tensor
+
+    @property
+    def n(self):
+        return int(self.wp.shape[0])
+
+    @property
+    def k(self):
+        return int(self.wp.shape[1]) * 2
+
+
+@dataclass
+class LayerWeights:
+    in_norm: torch.Tensor          # bf16 (H,)
+    qkv: Packed                    # ((Hq + 2 Hkv) D, H): q_proj | k_proj | v_proj rows
+    q_norm: torch.Tensor           # bf16 (D,)
+    k_norm: torch.Tensor           # bf16 (D,)
+    o: Packed                      # (H, Hq D)
+    post_norm: torch.Tensor        # bf16 (H,)
+    gate: Packed                   # (n_experts, H) router
+    experts: StackedExperts
+
+
+@dataclass
+class ModelWeights:
+    embed: Packed                  # (V, H)
+    layers: list
+    final_norm: torch.Tensor       # bf16 (H,)
+    lm_head: Packed                # (V, H)
+
+
+def _quantize(w_bf16):
+    """bf16 (N, K) -> Packed, with the library's bit-exact quantizer."""
+    lib = _lib.load()
+    n, k = w_bf16.shape
+    kp = (k + 31) // 32 * 32
+    wp = torch.empty((n, kp // 2), dtype=torch.uint8, device=w_bf16.device)
+    ws = torch.empty((n, kp // 32), dtype=torch.uint8, device=w_bf16.device)
+    _lib.check(lib.mxfp4_prequant(w_bf16.data_ptr(), k, n, k, kp, wp.data_ptr(), ws.data_ptr(),
+                                  torch.cuda.current_stream().cuda_stream), "prequant")
+    return Packed(wp, ws)
+
+
+def synthetic_model(cfg, seed=0, device="cuda", std=0.02):
+    """Random-init weights of the given shape (no checkpoint): projections,
+    router, experts, embedding and lm_head bf16 N(0, std) quantized to MXFP4;
+    norm weights bf16 1 + N(0, std)."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def rnd(n, k):
+        return _quantize((torch.randn((n, k), generator=g, device=device) * std).bfloat16())
+
+    def norm(n):
+        return (1.0 + std * torch.randn(n, generator=g, device=device)).bfloat16()
+
+    H, D, Mi, n_exp = cfg.hidden, cfg.head_dim, cfg.moe_inter, cfg.n_experts
+    layers = []
+    for _ in range(cfg.n_layers):
+        ex = {}
+        for nm, (n, k) in (("gate", (Mi, H)), ("up", (Mi, H)), ("down", (H, Mi))):
+            wp = torch.empty((n_exp, n, k // 2), dtype=torch.uint8, device=device)
+            ws = torch.empty((n_exp, n, k // 32), dtype=torch.uint8, device=device)
+            chunk = max(1, min(n_exp, (64 << 20) // (n * k * 4)))
+            for e0 in range(0, n_exp, chunk):
+                ce = min(chunk, n_exp - e0)
+                p = rnd(ce * n, k)
+                wp[e0:e0 + ce] = p.wp.view(ce, n, k // 2)
+                ws[e0:e0 + ce] = p.ws.view(ce, n, k // 32)
+            ex[nm + "_wp"], ex[nm + "_ws"] = wp, ws
+        layers.append(LayerWeights(in_norm=norm(H), qkv=rnd(cfg.qkv_rows, H), q_norm=norm(D), k_norm=norm(D),
+                                   o=rnd(H, cfg.n_heads * D), post_norm=norm(H), gate=rnd(n_exp, H),
+                                   experts=StackedExperts(**ex)))
+    return ModelWeights(embed=rnd(cfg.vocab, H), layers=layers, final_norm=norm(H), lm_head=rnd(cfg.vocab, H))
+
+
+@dataclass
+class _Bufs:
+    tensors: dict = field(default_factory=dict)
+
+    def __getattr__(self, k):
+        try:
+            return self.tensors[k]
+        except KeyError:
+            raise AttributeError(k)
+
+
+class DecodeStep:
+    """M tokens of one sequence per step (M = 1: forward_decode; M > 1:
+    forward_batch).  ids (M,) int32 and the base position dpos (1,) int32
+    stay on the device: each step reads them and leaves the greedy next
+    tokens and dpos + M for the next step."""
+
+    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda"):
+        self.lib = _lib.load()
+        self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
+        c = cfg
+        if c.head_dim != 128:
+            raise RuntimeError("head_dim must be 128 (attention kernels)")
+        if c.hidden % 2048:
+            raise RuntimeError("hidden must be a multiple of 2048 (norm kernel)")
+        M, H, D, Hq, Hkv = self.M, c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
+        f32, bf16, u8, i32 = torch.float32, torch.bfloat16, torch.uint8, torch.int32
+        t = {}
+
+        def buf(name, shape, dt):
+            t[name] = torch.zeros(shape, dtype=dt, device=device)
+
+        buf("ids", (M,), i32)
+        buf("dpos", (1,), i32)
+        buf("x", (M, H), bf16)
+        buf("x2", (M, H), bf16)
+        buf("y", (M, H), bf16)
+        buf("yq", (M, H // 2), u8)
+        buf("ys", (M, H // 32), u8)
+        buf("qkv", (M, c.qkv_rows), f32)
+        buf("q", (M, Hq, D), bf16)
+        buf("sc", (M, Hq, self.max_pos), f32)
+        buf("att", (M, Hq, D), f32)
+        buf("aq", (M, Hq * D // 2), u8)
+        buf("as_", (M, Hq * D // 32), u8)
+        buf("oproj", (M, H), f32)
+        buf("glog", (M, c.n_experts), f32)
+        buf("moe", (M, H), f32)
+        buf("logits", (M, c.vocab), f32)
+        nb = self.lib.mxfp4_attn_decode_workspace_size(M, Hq, self.max_pos)
+        buf("attn_ws", ((nb + 15) // 16 * 16,), u8)
+        # KV cache of every layer: (L, max_pos, Hkv, D) E4M3 bytes
+        buf("kvk", (c.n_layers, self.max_pos, Hkv, D), u8)
+        buf("kvv", (c.n_layers, self.max_pos, Hkv, D), u8)
+        if M == 1:
+            self.layer_ws = layer_workspace(c.top_k, c.moe_inter, H, device)
+            self.moe_calls = [RoutedLayerCall(t["y"][0], t["glog"][0], c.top_k, lw.experts, t["moe"][0], None,
+                                              self.layer_ws) for lw in model.layers]
+        else:
+            E = c.top_k
+            buf("rid", (M, E), i32)
+            buf("rw", (M, E), f32)
+            buf("gu_wp", (M * 2 * E,), torch.int64)
+            buf("gu_ws", (M * 2 * E,), torch.int64)
+            buf("dn_wp", (M * E,), torch.int64)
+            buf("dn_ws", (M * E,), torch.int64)
+            buf("gu", (M * E, 2 * c.moe_inter), f32)
+            buf("yd", (M * E, H), f32)
+        self.b = _Bufs(t)
+
+    # ------------------------------------------------------------------ state
+    def set_state(self, ids, pos):
+        """Token ids (M,) and the base position of the next step."""
+        self.b.ids.copy_(torch.as_tensor(ids, dtype=torch.int32).reshape(-1))
+        self.b.dpos.fill_(int(pos))
+
+    def fill_cache(self, upto, seed=1):
+        """Synthetic context: random E4M3 bytes for positions [0, upto) of
+        every layer's cache (codes of |v| < 2, no NaN code)."""
+        g = torch.Generator(device=self.b.kvk.device)
+        g.manual_seed(seed)
+        for kv in (self.b.kvk, self.b.kvv):
+            r = torch.randint(0, 256, kv[:, :upto].shape, generator=g, device=kv.device, dtype=torch.int32)
+            kv[:, :upto] = ((r & 0x80) | (r & 0x3F)).to(torch.uint8)   # exponent field <= 7: |v| < 2
+
+    # ------------------------------------------------------------------ one step
+    def _ck(self, rc, what):
+        _lib.check(rc, what)
+
+    def _lin(self, xq, xs, w, N, K, out, s):
+        kp = (K + 31) // 32 * 32
+        self._ck(self.lib.mxfp4_lin_pq(xq.data_ptr(), xs.data_ptr(), w.wp.data_ptr(), w.ws.data_ptr(), out.data_ptr(),
+                                       self.M, N, K, kp, s), "lin_pq")
+
+    def run(self, on_layer=None):
+        """Issue one step on the current stream.  on_layer(l, x, moe): an
+        optional eager hook after each layer's MoE (x is the residual stream
+        before the MoE residual is added)."""
+        lib, c, b, M = self.lib, self.cfg, self.b, self.M
+        s = torch.cuda.current_stream().cuda_stream
+        H, D, Hq, Hkv = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
+        m = self.model
+        self._ck(lib.mxfp4_embed_rows(m.embed.wp.data_ptr(), m.embed.ws.data_ptr(), c.vocab, H, b.ids.data_ptr(), M,
+                                      b.x.data_ptr(), s), "embed_rows")
+        xa, xb = b.x, b.x2          # residual stream ping-pong
+        for l, lw in enumerate(m.layers):
+            # input norm (+ the previous layer's MoE residual)
+            if l == 0:
+                self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), None, lw.in_norm.data_ptr(), c.rms_eps, M, H, None,
+                                                 b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s), "rmsnorm_quant")
+            else:
+                self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.moe.data_ptr(), lw.in_norm.data_ptr(), c.rms_eps, M,
+                                                 H, xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(),
+                                                 s), "rmsnorm_quant")
+                xa, xb = xb, xa
+            # attention
+            self._lin(b.yq, b.ys, lw.qkv, c.qkv_rows, H, b.qkv, s)
+            kvk, kvv = b.kvk[l], b.kvv[l]
+            self._ck(lib.mxfp4_qk_norm_rope_kv(b.qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), c.rms_eps,
+                                               c.rope_theta, b.dpos.data_ptr(), M, Hq, Hkv, D, b.q.data_ptr(),
+                                               kvk.data_ptr(), kvv.data_ptr(), self.max_pos, s), "qk_norm_rope_kv")
+            self._ck(lib.mxfp4_attn_decode(b.q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), b.dpos.data_ptr(),
+                                           b.sc.data_ptr(), b.att.data_ptr(), M, Hq, Hkv, D, self.max_pos,
+                                           b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode")
+            # o = attention.to(bf16) -> MXFP4 -> o_proj
+            self._ck(lib.mxfp4_quantize_rows(b.att.data_ptr(), 2, 2, Hq * D, M, Hq * D, Hq * D, b.aq.data_ptr(),
+                                             b.as_.data_ptr(), s), "quantize_rows")
+            self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
+            # x = x + bf16(o); post-attention norm; router logits
+            self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.oproj.data_ptr(), lw.post_norm.data_ptr(), c.rms_eps, M,
+                                             H, xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s),
+                     "rmsnorm_quant")
+            xa, xb = xb, xa
+            self._lin(b.yq, b.ys, lw.gate, c.n_experts, H, b.glog, s)
+            # MoE
+            if M == 1:
+                self.moe_calls[l](s)
+            else:
+                self._moe_batch(lw.experts, s)
+            if on_layer is not None:
+                on_layer(l, xa, b.moe)
+        # final norm (+ the last MoE residual), lm_head, greedy next tokens
+        self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.moe.data_ptr(), m.final_norm.data_ptr(), c.rms_eps, M, H,
+                                         xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s),
+                 "rmsnorm_quant")
+        self._lin(b.yq, b.ys, m.lm_head, c.vocab, H, b.logits, s)
+        self._ck(lib.mxfp4_argmax_advance(b.logits.data_ptr(), M, c.vocab, b.ids.data_ptr(), b.dpos.data_ptr(), s),
+                 "argmax_advance")
+        self.x_final = xb
+
+    def _moe_batch(self, ex, s):
+        lib, c, b, M = self.lib, self.cfg, self.b, self.M
+        E, H, Mi = c.top_k, c.hidden, c.moe_inter
+        self._ck(lib.mxfp4_route_topk(b.glog.data_ptr(), c.n_experts, M, c.n_experts, E, 1, b.rid.data_ptr(), None,
+                                      b.rw.data_ptr(), s), "route_topk")
+        self._ck(lib.mxfp4_route_tables(b.rid.data_ptr(), M, E, ex.gate_wp.data_ptr(), ex.gate_ws.data_ptr(),
+                                        ex.up_wp.data_ptr(), ex.up_ws.data_ptr(), ex.down_wp.data_ptr(),
+                                        ex.down_ws.data_ptr(), c.n_experts, H, Mi, b.gu_wp.data_ptr(),
+                                        b.gu_ws.data_ptr(), b.dn_wp.data_ptr(), b.dn_ws.data_ptr(), s), "route_tables")
+        kh, km = (H + 31) // 32 * 32, (Mi + 31) // 32 * 32
+        self._ck(lib.mxfp4_moe_gateup_devtab(b.yq.data_ptr(), b.ys.data_ptr(), b.gu_wp.data_ptr(), b.gu_ws.data_ptr(),
+                                             b.gu.data_ptr(), E, M, Mi, H, kh, s), "moe_gateup_tab")
+        self._ck(lib.mxfp4_moe_down_devtab(b.gu.data_ptr(), b.dn_wp.data_ptr(), b.dn_ws.data_ptr(), b.yd.data_ptr(), E,
+                                           M, H, Mi, km, s), "moe_down_tab")
+        self._ck(lib.mxfp4_moe_combine(b.yd.data_ptr(), H, b.rw.data_ptr(), E, b.moe.data_ptr(), M, H, s),
+                 "moe_combine")
+
+    # ------------------------------------------------------------------ graphs
+    def capture(self):
+        """One step captured in a HIP graph (replay = one more step)."""
+        self.run()                       # warm-up (also advances the state)
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                self.run()
+        torch.cuda.synchronize()
+        return graph

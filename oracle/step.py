@@ -1,0 +1,129 @@
+"""CPU restatement of the reference's decode step -- test infrastructure
+(only tests/ use it).
+
+Reference:
+  rms_norm          runtime/model_runner.py:20-25
+  apply_rope        runtime/model_runner.py:28-41 (half layout, theta)
+  dequant_rows_gpu  runtime/weight_store.py:47-65 (embedding rows)
+  forward_decode    runtime/model_runner_v2.py:130-217 (one token)
+  forward_batch     runtime/model_runner_v2.py:220-300 (M tokens of one sequence)
+  greedy next token runtime/decode_v2.py:71 (logits[-1].argmax())
+
+numpy float32 where the reference computes in fp32 and bf16 rounding where it
+rounds; the matmuls (lin_pq, attention, MoE) are the float64 oracles of
+oracle/ops.py and oracle/attn.py.  Differences to the GPU step come from
+fp32 accumulation order and the transcendental functions (rsqrt, cos, sin,
+exp), so the comparison is to a tolerance.
+"""
+import numpy as np
+
+from . import attn as attn_ref
+from . import mxfp4 as fmt
+from . import ops
+
+bf16 = fmt.bf16_round
+
+
+def rms_norm_ref(x, w, eps, bf16_input=True):
+    """runtime/model_runner.py:20-25: xf = x.float(); xf * rsqrt(mean(xf^2) + eps);
+    cast back to the input dtype; times the bf16 weight (bf16 * bf16 -> bf16
+    for bf16 input, fp32 for fp32 input -- the caller's .bfloat16() then
+    rounds).  Returns bf16 values as float32."""
+    xf = np.asarray(x, np.float32)
+    var = np.mean(xf.astype(np.float64) ** 2, axis=-1, keepdims=True).astype(np.float32)
+    r = (np.float32(1.0) / np.sqrt(var + np.float32(eps))).astype(np.float32)
+    y = (xf * r).astype(np.float32)
+    if bf16_input:
+        y = bf16(y)
+    return bf16((y * np.asarray(w, np.float32)).astype(np.float32))
+
+
+def rope_ref(x, positions, theta):
+    """runtime/model_runner.py:28-41 on x (T, nh, D) bf16 values: fp32
+    inv_freq and angles, x * cos + rotate_half(x) * sin in fp32, to bf16."""
+    x = np.asarray(x, np.float32)
+    D = x.shape[-1]
+    inv = (np.float32(1.0) / np.power(np.float32(theta), np.arange(0, D, 2, dtype=np.float32) / np.float32(D))).astype(np.float32)
+    freqs = (np.asarray(positions, np.float32)[:, None] * inv[None, :]).astype(np.float32)
+    cos = np.cos(freqs.astype(np.float64)).astype(np.float32)
+    sin = np.sin(freqs.astype(np.float64)).astype(np.float32)
+    cos = np.concatenate([cos, cos], axis=-1)[:, None, :]
+    sin = np.concatenate([sin, sin], axis=-1)[:, None, :]
+    rot = np.concatenate([-x[..., D // 2:], x[..., : D // 2]], axis=-1)
+    return bf16(((x * cos).astype(np.float32) + (rot * sin).astype(np.float32)).astype(np.float32))
+
+
+def embed_ref(wp, ws, ids, K):
+    """runtime/weight_store.py:47-65: rows ids of an MXFP4 matrix, dequantized, to bf16."""
+    ids = np.asarray(ids)
+    return bf16(fmt.dequant_rows(wp[ids], ws[ids], K).astype(np.float32))
+
+
+def argmax_ref(logits):
+    """First index of each row's maximum (torch.argmax)."""
+    return np.argmax(np.asarray(logits), axis=-1).astype(np.int32)
+
+
+def step_ref(w, cfg, ids, base, kvk, kvv, fused_moe, x_teacher=None):
+    """One step of M = len(ids) tokens at positions base..base+M-1.
+
+    w: dict of numpy arrays (keys as DecodeStep's weights: embed, layers[l]
+    {in_norm, qkv, q_norm, k_norm, o, post_norm, gate, experts}, final_norm,
+    lm_head; Packed weights as (wp, ws) pairs, experts as {e: ((gwp, gws),
+    (uwp, uws), (dwp, dws))}).  kvk, kvv: (L, max_pos, Hkv, D) uint8 caches,
+    updated in place.  fused_moe: the MoE on bf16 activations
+    (decode_layer_ref, the one-token fused path) or, False, the drop-in ops on
+    MXFP4 activations (forward_batch).  x_teacher: optional list of the
+    residual stream after each layer as another implementation computed it;
+    layer l > 0 and the head then start from x_teacher[l-1] / x_teacher[-1]
+    instead of this function's own value (teacher forcing, so each layer is
+    compared on identical inputs).  Returns (logits (M, V) float64,
+    [x after each layer] bf16 values)."""
+    ids = np.asarray(ids)
+    M = len(ids)
+    H, D, Hq, Hkv, E = cfg.hidden, cfg.head_dim, cfg.n_heads, cfg.n_kv_heads, cfg.top_k
+    eps = cfg.rms_eps
+    pos = np.arange(base, base + M)
+    x = embed_ref(*w["embed"], ids, H)
+    xs = []
+    for l, lw in enumerate(w["layers"]):
+        if x_teacher is not None and l > 0:
+            x = np.asarray(x_teacher[l - 1], np.float32)
+        hp = rms_norm_ref(x, lw["in_norm"], eps)
+        hq, hs = fmt.quantize_rows(hp)
+        qkv = ops.lin_pq_ref(hq, hs, *lw["qkv"]).astype(np.float32)
+        q = qkv[:, : Hq * D].reshape(M, Hq, D)
+        k = qkv[:, Hq * D:(Hq + Hkv) * D].reshape(M, Hkv, D)
+        v = qkv[:, (Hq + Hkv) * D:].reshape(M, Hkv, D)
+        qn = rms_norm_ref(q, lw["q_norm"], eps, bf16_input=False)
+        kn = rms_norm_ref(k, lw["k_norm"], eps, bf16_input=False)
+        qr, kr = rope_ref(qn, pos, cfg.rope_theta), rope_ref(kn, pos, cfg.rope_theta)
+        attn_ref.kv_write_ref(kr, bf16(v), kvk[l], kvv[l], base)
+        o_att, _ = attn_ref.attn_decode_ref(qr, kvk[l], kvv[l], base)
+        of = bf16(o_att.astype(np.float32)).reshape(M, Hq * D)
+        aq, as_ = fmt.quantize_rows(of)
+        o = ops.lin_pq_ref(aq, as_, *lw["o"]).astype(np.float32)
+        x = bf16((x + bf16(o)).astype(np.float32))
+        hp2 = rms_norm_ref(x, lw["post_norm"], eps)
+        h2q, h2s = fmt.quantize_rows(hp2)
+        glog = ops.lin_pq_ref(h2q, h2s, *lw["gate"]).astype(np.float32)
+        topi, topv = ops.route_topk_np(glog, E, renorm=True)
+        if fused_moe:
+            moe = ops.decode_layer_ref(hp2, topi, topv, lw["experts"]).astype(np.float32)
+        else:
+            ex = lw["experts"]
+            # token-major table: entry m*2E + proj*E + e (runtime/model_runner_v2.py:279-286)
+            tw = [ex[int(e)][proj][0] for m in range(M) for proj in (0, 1) for e in topi[m]]
+            ts = [ex[int(e)][proj][1] for m in range(M) for proj in (0, 1) for e in topi[m]]
+            gu = ops.moe_gateup_ref(h2q, h2s, tw, ts, E, M, cfg.moe_inter)
+            yd = ops.moe_down_ref(gu, [ex[int(e)][2][0] for e in topi.reshape(-1)],
+                                  [ex[int(e)][2][1] for e in topi.reshape(-1)], E, M, H, cfg.moe_inter)
+            moe = ops.moe_combine_ref(yd, topv.astype(np.float32), M).astype(np.float32)
+        x = bf16((x + bf16(moe)).astype(np.float32))
+        xs.append(x)
+    if x_teacher is not None:
+        x = np.asarray(x_teacher[-1], np.float32)
+    xf = rms_norm_ref(x, w["final_norm"], eps)
+    fq, fs = fmt.quantize_rows(xf)
+    logits = ops.lin_pq_ref(fq, fs, *w["lm_head"])
+    return logits, xs
