@@ -54,7 +54,8 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-extra", action="store_true", help="only the headline decode measurement")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["decode", "decode1", "dropin", "gemm", "spec", "copy", "prefill", "attn"],
+    ap.add_argument("--only", choices=["decode", "decode1", "dropin", "gemm", "spec", "copy", "prefill", "attn",
+                                       "step"],
                     default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
     return ap.parse_args()
@@ -340,6 +341,48 @@ def bench_attn(torch, dext, ctx=4096, M=1, reps=50):
             "note": "kv_write + attn_decode (score + combine kernels), Hq=32 Hkv=4 D=128, graph replay"}
 
 
+def bench_step(torch, layers, M, steps=128):
+    """Config 5: a whole random-init Qwen3-30B-A3B-shaped decode step (48
+    layers, GQA 32/4 x 128, FP8 KV cache, 128 experts top-8 MXFP4, vocab
+    151936) on this library's kernels, M tokens of one sequence per step,
+    `steps` greedy steps ending at context 4096, one HIP graph per step.
+    The experts are the config-2 layers already resident."""
+    from moe_fused_inference_amd.decode_step import DecodeStep, ModelConfig, synthetic_model
+    cfg = ModelConfig()
+    model = synthetic_model(cfg, seed=77, experts=layers)
+    st = DecodeStep(model, cfg, M=M, max_pos=4096)
+    start = 4096 - steps * M
+    st.fill_cache(start + 1, seed=3)      # +1: the warm-up step of capture() writes position `start`
+    g = torch.Generator().manual_seed(5)
+    ids0 = torch.randint(0, cfg.vocab, (M,), generator=g)
+    st.set_state(ids0, start - 1)
+    graph = st.capture()                  # warm-up step at start-1..; the timed steps follow
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    st.set_state(ids0, start)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    end_pos = int(st.b.dpos.item())
+    moe_graph = st.capture_fn(st.run_moe_only)
+    reps = 10
+    e0.record()
+    for _ in range(reps):
+        moe_graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms_moe = e0.elapsed_time(e1) / reps
+    del graph, moe_graph, st, model
+    return {"M": M, "steps": steps, "context_end": end_pos, "ms_per_step": round(ms, 3),
+            "tok_per_s": round(M * 1e3 / ms, 1), "moe_ms_per_step": round(ms_moe, 3),
+            "moe_share": round(ms_moe / ms, 3),
+            "note": "random-init Qwen3-30B-A3B shape, greedy, graph replay per step; MoE share = the step's 48 "
+                    "MoE blocks replayed alone / the step"}
+
+
 def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
     """Config 4: M=9 tokens, Zipf(1.1)-biased routing over 128 experts, grouped
     drop-in path (moe_gateup + moe_down + moe_combine)."""
@@ -546,6 +589,8 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
         log(f"prefill moe: {bench_prefill_moe(torch, lext, layers[2])}")
     elif args.only == "attn":
         log(f"attn decode: {[bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]}")
+    elif args.only == "step":
+        log(f"decode step (config 5): {[bench_step(torch, layers, M) for M in (1, 8)]}")
     elif args.only == "spec":
         log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
 
@@ -582,7 +627,7 @@ def main():
     ws = workspace(TOPK, MI, H, dev)
     outs = [torch.empty(H, dtype=torch.float32, device=dev) for _ in range(LAYERS)]
     bufs = [torch.empty(H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    if args.only in ("dropin", "gemm", "spec", "prefill", "attn"):
+    if args.only in ("dropin", "gemm", "spec", "prefill", "attn", "step"):
         return only_extra(args, torch, dext, lext, layers, routes, x0)
     from moe_fused_inference_amd.moe_layer import LayerStack, stack_status, stack_workspace
     stack = LayerStack(layers)
@@ -683,6 +728,9 @@ def main():
         at = [bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]
         extra["attn_decode_cfg5"] = at
         log(f"attn decode (config 5 shape): {at}")
+        ds = [bench_step(torch, layers, M) for M in (1, 8)]
+        extra["decode_step_cfg5"] = ds
+        log(f"decode step (config 5): {ds}")
 
     cpu = None
     if not args.no_cpu:

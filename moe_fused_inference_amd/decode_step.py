@@ -97,10 +97,11 @@ def _quantize(w_bf16):
     return Packed(wp, ws)
 
 
-def synthetic_model(cfg, seed=0, device="cuda", std=0.02):
+def synthetic_model(cfg, seed=0, device="cuda", std=0.02, experts=None):
     """Random-init weights of the given shape (no checkpoint): projections,
     router, experts, embedding and lm_head bf16 N(0, std) quantized to MXFP4;
-    norm weights bf16 1 + N(0, std)."""
+    norm weights bf16 1 + N(0, std).  experts: optional list of per-layer
+    StackedExperts to use instead of new random ones."""
     g = torch.Generator(device=device)
     g.manual_seed(seed)
 
@@ -112,7 +113,12 @@ def synthetic_model(cfg, seed=0, device="cuda", std=0.02):
 
     H, D, Mi, n_exp = cfg.hidden, cfg.head_dim, cfg.moe_inter, cfg.n_experts
     layers = []
-    for _ in range(cfg.n_layers):
+    for li in range(cfg.n_layers):
+        if experts is not None:
+            layers.append(LayerWeights(in_norm=norm(H), qkv=rnd(cfg.qkv_rows, H), q_norm=norm(D), k_norm=norm(D),
+                                       o=rnd(H, cfg.n_heads * D), post_norm=norm(H), gate=rnd(n_exp, H),
+                                       experts=experts[li]))
+            continue
         ex = {}
         for nm, (n, k) in (("gate", (Mi, H)), ("up", (Mi, H)), ("down", (H, Mi))):
             wp = torch.empty((n_exp, n, k // 2), dtype=torch.uint8, device=device)
@@ -296,6 +302,29 @@ class DecodeStep:
                                            M, H, Mi, km, s), "moe_down_tab")
         self._ck(lib.mxfp4_moe_combine(b.yd.data_ptr(), H, b.rw.data_ptr(), E, b.moe.data_ptr(), M, H, s),
                  "moe_combine")
+
+    def run_moe_only(self):
+        """The step's 48 MoE blocks alone, on the buffers the last step left
+        (router logits, normed activations): for measuring the MoE share."""
+        s = torch.cuda.current_stream().cuda_stream
+        for l, lw in enumerate(self.model.layers):
+            if self.M == 1:
+                self.moe_calls[l](s)
+            else:
+                self._moe_batch(lw.experts, s)
+
+    def capture_fn(self, fn):
+        """Any issue function captured in a HIP graph (fn runs once first)."""
+        fn()
+        torch.cuda.synchronize()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                fn()
+        torch.cuda.synchronize()
+        return graph
 
     # ------------------------------------------------------------------ graphs
     def capture(self):
