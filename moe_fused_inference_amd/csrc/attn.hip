@@ -60,20 +60,36 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     if (s0 >= S) return;                       // uniform over the workgroup
     __shared__ __align__(16) float qs[G][kD];
     __shared__ float ps[G][kChunk];
+    // Both phases' cache rows are loaded first (one memory latency for the
+    // workgroup): K words of the score thread (position p, quarter qd of D)
+    // and V words of the partial-sum thread (4 columns cq, positions
+    // pl*8..pl*8+7; rows past S clamped in bounds, their weight is 0).
+    const int p = threadIdx.x >> 2, qd = threadIdx.x & 3;
+    const int s = s0 + p;
+    uint4 b0 = make_uint4(0, 0, 0, 0), b1 = make_uint4(0, 0, 0, 0);
+    if (s < S) {
+        const uint8_t* kr = kvk + ((int64_t)s * Hkv + g) * kD + qd * 32;
+        b0 = *reinterpret_cast<const uint4*>(kr);
+        b1 = *reinterpret_cast<const uint4*>(kr + 16);
+    }
+    const int cq = threadIdx.x & 31, pl = threadIdx.x >> 5;
+    const int last = S - 1 - s0;               // last valid row of the chunk
+    uint32_t vw[8];
+    {
+        const uint8_t* vcol = kvv + ((int64_t)s0 * Hkv + g) * kD + cq * 4;
+        const int64_t vstride = (int64_t)Hkv * kD;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t*>(vcol + (int64_t)min(pl * 8 + i, last) * vstride);
+    }
     for (int i = threadIdx.x; i < G * kD; i += 256)
         qs[i / kD][i % kD] = bf16_to_f32(q[((int64_t)m * Hq + g * G + i / kD) * kD + i % kD]);
     __syncthreads();
     // ---- scores: thread = (position p, quarter qd of D)
     {
-        const int p = threadIdx.x >> 2, qd = threadIdx.x & 3;
-        const int s = s0 + p;
         float acc[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) acc[h] = 0.0f;
         if (s < S) {
-            const uint8_t* kr = kvk + ((int64_t)s * Hkv + g) * kD + qd * 32;
-            const uint4 b0 = *reinterpret_cast<const uint4*>(kr);
-            const uint4 b1 = *reinterpret_cast<const uint4*>(kr + 16);
             const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
             // 4 columns per step: their q values come from LDS as one float4
             // per head (the 16 threads of a quarter read the same address)
@@ -129,17 +145,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     }
     __syncthreads();
     // ---- partial V sums: thread = 4 columns (cq) x 8 of the chunk's
-    // positions (pl), all G heads.  Its 8 V words are loaded before use (one
-    // memory latency); rows past S are clamped in bounds and carry weight
-    // exp(-inf) = 0.  The 8 position lanes are summed through LDS.
+    // positions (pl), all G heads, from the V words loaded at entry.  The 8
+    // position lanes are summed through LDS.
     {
-        const int cq = threadIdx.x & 31, pl = threadIdx.x >> 5;
-        const int last = S - 1 - s0;           // last valid row of the chunk
-        const uint8_t* vcol = kvv + ((int64_t)s0 * Hkv + g) * kD + cq * 4;
-        const int64_t vstride = (int64_t)Hkv * kD;
-        uint32_t vw[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t*>(vcol + (int64_t)min(pl * 8 + i, last) * vstride);
         float4 acc[G];
 #pragma unroll
         for (int h = 0; h < G; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);

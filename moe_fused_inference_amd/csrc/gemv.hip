@@ -145,8 +145,11 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
     return acc;
 }
 
-template <class Tab, int AMODE>
-__global__ __launch_bounds__(256) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
+// NW waves per workgroup, 16 weight rows each.  NW = 1 spreads a small-N
+// launch (the dense lin_pq projections of a decode step) over 4x more
+// workgroups, so more CUs stream at once.
+template <class Tab, int AMODE, int NW>
+__global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];  // A_SILU: 16 rows of quantized h
     __shared__ int s_rows[kMaxT];
     __shared__ int s_cnt, s_first;
@@ -186,7 +189,7 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(Tab tab, GemvArgs a) 
     const int steps = (nch + 3) >> 2;     // MFMA K-steps; lane group g owns blocks [g*steps, g*steps+steps)
     const int r = lane & 15;
     const int g = lane >> 4;
-    const int n0 = blockIdx.x * 64 + wave * 16;
+    const int n0 = blockIdx.x * (16 * NW) + wave * 16;
     const int nrow = min(n0 + r, a.N - 1);
     const uint8_t* wrow = wp + (int64_t)nrow * (a.Kp >> 1);
     const uint8_t* srow = ws + (int64_t)nrow * nch;
@@ -200,7 +203,7 @@ __global__ __launch_bounds__(256) void grouped_gemv_kernel(Tab tab, GemvArgs a) 
             // Build the 16-row A tile: h = silu(g)*u (fp32) quantized per
             // 32-block with the bit-exact rule; rows past the group are zero.
             const int upr = a.Kp >> 3;
-            for (int u = threadIdx.x; u < 16 * upr; u += 256) {
+            for (int u = threadIdx.x; u < 16 * upr; u += 64 * NW) {
                 const int rr = u / upr;
                 const int uu = u - rr * upr;
                 const int k0 = uu * 8;
@@ -283,11 +286,20 @@ size_t silu_lds_bytes(int Kp) { return (size_t)16 * ((Kp >> 1) + (Kp >> 5)); }
 
 template <class Tab>
 int launch_gemv(const Tab& tab, const GemvArgs& a, int amode, hipStream_t st) {
-    dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.T);
-    if (amode == A_FP4) {
-        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4>), grid, dim3(256), 0, st, tab, a);
+    // one wave per workgroup when the 4-wave grid would not reach 4
+    // workgroups per CU (the A_SILU tile build is shared by the waves of a
+    // workgroup, so that path keeps 4)
+    const bool one = amode == A_FP4 && (int64_t)((a.N + 63) / 64) * a.T < 1024;
+    if (one) {
+        dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)a.T);
+        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 1>), grid, dim3(64), 0, st, tab, a);
     } else {
-        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU>), grid, dim3(256), silu_lds_bytes(a.Kp), st, tab, a);
+        dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.T);
+        if (amode == A_FP4)
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 4>), grid, dim3(256), 0, st, tab, a);
+        else
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4>), grid, dim3(256), silu_lds_bytes(a.Kp), st,
+                               tab, a);
     }
     return mxh::launch_status("grouped_gemv");
 }

@@ -155,9 +155,10 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const uint16_t* __restr
 // ------------------------------------------------------------------ q/k norm + RoPE + KV write
 constexpr int kD = 128;
 
-// Workgroup (token m); wave w handles heads w, w+4, ... of the Hq + Hkv + Hkv
-// (q, k, v) heads of the fused projection row; lane l owns elements l and
-// l + 64 of a head, which are the RoPE partners (D = 128, half layout).
+// Workgroup (token m, 4 heads): wave w handles head 4*blockIdx.y + w of the
+// Hq + Hkv + Hkv (q, k, v) heads of the fused projection row; lane l owns
+// elements l and l + 64 of a head, which are the RoPE partners (D = 128, half
+// layout).
 __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict__ qkv, const uint16_t* __restrict__ qw,
                                                          const uint16_t* __restrict__ kw, float eps, float theta,
                                                          const int32_t* __restrict__ dpos, int Hq, int Hkv,
@@ -167,6 +168,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int nh = Hq + 2 * Hkv;
+    const int h = blockIdx.y * 4 + wave;
+    if (h >= nh) return;
     const int pos = *dpos + m;
     const float* row = qkv + (int64_t)m * nh * kD;
     // inv_freq = 1 / theta^(2j/D) and the angle pos * inv_freq in fp32
@@ -174,7 +177,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
     const float inv_freq = 1.0f / powf(theta, (float)(2 * lane) / (float)kD);
     const float ang = (float)pos * inv_freq;
     const float c = cosf(ang), s = sinf(ang);
-    for (int h = wave; h < nh; h += 4) {
+    {
         const float a = row[h * kD + lane], b = row[h * kD + lane + 64];
         if (h >= Hq + Hkv) {   // v: bf16, then the KV byte
             const int hv = h - Hq - Hkv;
@@ -183,7 +186,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
                 dst[lane] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(a)));
                 dst[lane + 64] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(b)));
             }
-            continue;
+            return;
         }
         // head RMSNorm on fp32: (x * rsqrt(mean(x^2) + eps)) * w, then bf16
         float ss = fmaf(a, a, b * b);
@@ -294,7 +297,7 @@ extern "C" int mxfp4_qk_norm_rope_kv(const float* qkv, const void* q_norm_w, con
     MXH_REQUIRE(D == kD, "qk_norm_rope_kv: D=%d (the reference's kernels assume 128)", D);
     MXH_REQUIRE(M > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pos > 0, "qk_norm_rope_kv: M=%d Hq=%d Hkv=%d max_pos=%d", M,
                 Hq, Hkv, max_pos);
-    hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(M), dim3(256), 0, mxh::as_stream(stream), qkv,
+    hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(M, (Hq + 2 * Hkv + 3) / 4), dim3(256), 0, mxh::as_stream(stream), qkv,
                        static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w), eps, theta, dpos,
                        Hq, Hkv, static_cast<uint16_t*>(q_out), kvk, kvv, max_pos);
     return mxh::launch_status("qk_norm_rope_kv");
