@@ -58,6 +58,7 @@ def parse():
                                        "step"],
                     default=None,
                     help="run one measurement only (for rocprofv3 runs); prints no JSON line")
+    ap.add_argument("--step-m", type=int, nargs="+", default=[1, 8], help="batch sizes of the config-5 step")
     return ap.parse_args()
 
 
@@ -590,7 +591,7 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
     elif args.only == "attn":
         log(f"attn decode: {[bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]}")
     elif args.only == "step":
-        log(f"decode step (config 5): {[bench_step(torch, layers, M) for M in (1, 8)]}")
+        log(f"decode step (config 5): {[bench_step(torch, layers, M) for M in args.step_m]}")
     elif args.only == "spec":
         log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
 
@@ -728,7 +729,7 @@ def main():
         at = [bench_attn(torch, dext, ctx) for ctx in (512, 4096)] + [bench_attn(torch, dext, 4096, M=8)]
         extra["attn_decode_cfg5"] = at
         log(f"attn decode (config 5 shape): {at}")
-        ds = [bench_step(torch, layers, M) for M in (1, 8)]
+        ds = [bench_step(torch, layers, M) for M in args.step_m]
         extra["decode_step_cfg5"] = ds
         log(f"decode step (config 5): {ds}")
 
