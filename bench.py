@@ -339,7 +339,7 @@ def bench_attn(torch, dext, ctx=4096, M=1, reps=50):
     kv_bytes = 2 * ctx * Hkv * D
     return {"context": ctx, "M": M, "us": round(ms * 1e3, 2), "kv_bytes": kv_bytes,
             "gbs": round(kv_bytes / (ms * 1e-3) / 1e9, 1),
-            "note": "kv_write + attn_decode (score + combine kernels), Hq=32 Hkv=4 D=128, graph replay"}
+            "note": "kv_write + attn_decode (score + merge kernels), Hq=32 Hkv=4 D=128, graph replay"}
 
 
 def bench_step(torch, layers, M, steps=128):

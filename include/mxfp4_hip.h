@@ -158,6 +158,15 @@ int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, con
                       float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos,
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* mxfp4_attn_decode_mx: mxfp4_attn_decode whose output can also (or only)
+ * be the MXFP4 rows of bf16(o), the activation of the o_proj lin_pq
+ * (runtime/model_runner_v2.py:175-178: o.bfloat16() -> prequant): oq u8
+ * (M, Hq*D/2) and os u8 (M, Hq*D/32), bit-exact to mxfp4_quantize_rows of
+ * o with bf16 rounding (mode 2).  o may be NULL when oq/os are given. */
+int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
+                         float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
+                         int max_pos, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * KV write: k, v bf16 (M, Hkv, D) -> the reference's E4M3 bytes (rounding
  * half away from zero, >= 248 saturating to 0x7F) at rows dpos+m < max_pos
@@ -289,15 +298,25 @@ int mxfp4_rmsnorm_quant(const void* x, const float* resid, const void* w, float 
  * q and k heads get RMSNorm with q_norm_w / k_norm_w (bf16 (D)) and the
  * half-layout RoPE of runtime/model_runner.py:28-41 (theta), q goes to
  * q_out (M, Hq, D) bf16, k and bf16(v) to the KV cache rows (max_pos, Hkv,
- * D) in the reference's E4M3 byte codec (as mxfp4_kv_write).  D = 128. */
+ * D) as E4M3 bytes.  codec 0: the decode extension's kv_write codec (as
+ * mxfp4_kv_write; the graph runner's write, runtime/model_runner_v3.py:
+ * 98-101); codec 1: torch's float8_e4m3fn conversion (round to nearest
+ * even, 0x7F above 464; the batch step's write,
+ * runtime/model_runner_v2.py:256-257).  D = 128. */
 int mxfp4_qk_norm_rope_kv(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
                           float theta, const int32_t* dpos, int M, int Hq, int Hkv, int D, void* q_out,
-                          uint8_t* kvk, uint8_t* kvv, int max_pos, void* stream);
+                          uint8_t* kvk, uint8_t* kvv, int max_pos, int codec, void* stream);
 
 /* mxfp4_argmax_advance: ids[m] = the first index of the maximum of logits
- * row m (M, V) fp32 -- greedy decoding, runtime/decode_v2.py:71 -- and,
- * when dpos is not NULL, *dpos += M afterwards (stream-ordered). */
-int mxfp4_argmax_advance(const float* logits, int M, int V, int32_t* ids, int32_t* dpos, void* stream);
+ * row m (M, V) fp32, NaN never winning -- greedy decoding,
+ * runtime/decode_v2.py:71 -- and, when dpos is not NULL, *dpos += M once
+ * every row is done.  ws: mxfp4_argmax_workspace_size(M, V) bytes, 256-byte
+ * aligned, zero-filled once before its first use; every call leaves it
+ * zero-filled again (so no clearing between calls or graph replays).  Calls
+ * that share a workspace must not run concurrently. */
+size_t mxfp4_argmax_workspace_size(int M, int V);
+int mxfp4_argmax_advance(const float* logits, int M, int V, int32_t* ids, int32_t* dpos, void* ws,
+                         size_t ws_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * Token -> expert grouping (the bookkeeping of torch.where(topi == e) in

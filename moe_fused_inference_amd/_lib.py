@@ -44,11 +44,14 @@ SIGNATURES = {
     "mxfp4_embed_rows": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p, _c_p]),
     "mxfp4_rmsnorm_quant": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_qk_norm_rope_kv": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_i, _c_i, _c_i, _c_i,
-                                     _c_p, _c_p, _c_p, _c_i, _c_p]),
-    "mxfp4_argmax_advance": (_c_i, [_c_p, _c_i, _c_i, _c_p, _c_p, _c_p]),
+                                     _c_p, _c_p, _c_p, _c_i, _c_i, _c_p]),
+    "mxfp4_argmax_workspace_size": (_c_sz, [_c_i, _c_i]),
+    "mxfp4_argmax_advance": (_c_i, [_c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_sz, _c_p]),
     "mxfp4_attn_decode_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
     "mxfp4_attn_decode": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
                                  _c_p, _c_sz, _c_p]),
+    "mxfp4_attn_decode_mx": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
+                                    _c_p, _c_sz, _c_p]),
     "mxfp4_kv_write": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_moe_group": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_route_topk": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),

@@ -17,7 +17,8 @@
 //                        sum of V (V rows read once for the group) -> one
 //                        record per (token, head, chunk) in the workspace.
 //   attn_final_kernel    workgroup (query head, token): merges the records
-//                        (split softmax: rescale by exp(m_c - max)).
+//                        (split softmax: rescale by exp(m_c - max)); fp32
+//                        output and/or its bf16 -> MXFP4 rows.
 //   kv_write_kernel      k, v (M, Hkv, D) bf16 -> E4M3 bytes at row pos.
 //
 // The byte codec is the reference's own (f32_to_e4m3 / e4m3_to_f32 at
@@ -40,12 +41,15 @@ constexpr int kChunk = 64;       // positions per score workgroup
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
 constexpr int kPart = 132;       // floats per partial record: max, sum, 128 column sums, pad
+constexpr int kMaxChunks = 1024; // max_pos <= 65536
 
-// Workgroup (64-position chunk, kv head g, token m): the scores of the chunk
-// for all G query heads of the group (K rows read once, q staged in LDS),
-// stored raw into sc; then per head the chunk's max, exp(x - max) and sum,
-// and the partial weighted sum of the chunk's V rows (read once for the
-// group).  Writes one partial record per (token, head, chunk).
+// Workgroup (64-position chunk, kv head g, token m):
+//  1. the chunk's K and V rows and the group's q are loaded before anything
+//     waits (the position only masks; rows past max_pos are clamped), so the
+//     workgroup pays one memory latency;
+//  2. scores of all G query heads of the group (raw dot products also go to
+//     sc), per head the chunk max, exp(x - max) and sum, and the partial
+//     weighted sum of V -> one record per (token, head, chunk).
 template <int G>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q,
                                                            const uint8_t* __restrict__ kvk,
@@ -53,38 +57,53 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                                                            float* __restrict__ part, const int32_t* __restrict__ dpos,
                                                            int Hq, int Hkv, int max_pos, int nchunk, float invsqrt) {
     const int m = blockIdx.z, g = blockIdx.y, chunk = blockIdx.x;
-    const int pos = *dpos + m;
-    if (pos < 0 || pos >= max_pos) return;
-    const int S = pos + 1;
+    const int tid = threadIdx.x;
     const int s0 = chunk * kChunk;
-    if (s0 >= S) return;                       // uniform over the workgroup
+    const int rowmax = max_pos - 1 - s0;       // last in-bounds row of the chunk (s0 < max_pos)
     __shared__ __align__(16) float qs[G][kD];
     __shared__ float ps[G][kChunk];
-    // Both phases' cache rows are loaded first (one memory latency for the
-    // workgroup): K words of the score thread (position p, quarter qd of D)
-    // and V words of the partial-sum thread (4 columns cq, positions
-    // pl*8..pl*8+7; rows past S clamped in bounds, their weight is 0).
-    const int p = threadIdx.x >> 2, qd = threadIdx.x & 3;
-    const int s = s0 + p;
-    uint4 b0 = make_uint4(0, 0, 0, 0), b1 = make_uint4(0, 0, 0, 0);
-    if (s < S) {
-        const uint8_t* kr = kvk + ((int64_t)s * Hkv + g) * kD + qd * 32;
-        b0 = *reinterpret_cast<const uint4*>(kr);
-        b1 = *reinterpret_cast<const uint4*>(kr + 16);
-    }
-    const int cq = threadIdx.x & 31, pl = threadIdx.x >> 5;
-    const int last = S - 1 - s0;               // last valid row of the chunk
+    __shared__ __align__(16) float vred[8][G][kD];   // V partial sums of the 8 position lanes
+    __shared__ float stat[G][2];
+    // ---- 1. loads: K words of the score thread (position p, quarter qd of
+    // D), V words of the partial-sum thread (4 columns cq, positions
+    // pl*8..pl*8+7), 4 q values per thread
+    const int p = tid >> 2, qd = tid & 3;
+    const uint8_t* kr = kvk + ((int64_t)(s0 + min(p, rowmax)) * Hkv + g) * kD + qd * 32;
+    const uint4 b0 = *reinterpret_cast<const uint4*>(kr);
+    const uint4 b1 = *reinterpret_cast<const uint4*>(kr + 16);
+    const int cq = tid & 31, pl = tid >> 5;
     uint32_t vw[8];
     {
         const uint8_t* vcol = kvv + ((int64_t)s0 * Hkv + g) * kD + cq * 4;
         const int64_t vstride = (int64_t)Hkv * kD;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t*>(vcol + (int64_t)min(pl * 8 + i, last) * vstride);
+        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t*>(vcol + (int64_t)min(pl * 8 + i, rowmax) * vstride);
     }
-    for (int i = threadIdx.x; i < G * kD; i += 256)
-        qs[i / kD][i % kD] = bf16_to_f32(q[((int64_t)m * Hq + g * G + i / kD) * kD + i % kD]);
+    constexpr int kQPer = (G * kD + 1023) / 1024;    // 4-value q loads per thread
+    uint2 qv[kQPer];
+#pragma unroll
+    for (int j = 0; j < kQPer; ++j) {
+        const int i = (j * 256 + tid) * 4;
+        qv[j] = i < G * kD ? *reinterpret_cast<const uint2*>(q + ((int64_t)m * Hq + g * G) * kD + i) : make_uint2(0, 0);
+    }
+    const int pos = *dpos + m;
+    if (pos < 0 || pos >= max_pos) return;
+    const int S = pos + 1;
+    if (s0 >= S) return;                       // uniform over the workgroup; not counted below
+    const int s = s0 + p;
+#pragma unroll
+    for (int j = 0; j < kQPer; ++j) {
+        const int i = (j * 256 + tid) * 4;
+        if (i < G * kD) {
+            float* d = &qs[0][0] + i;
+            d[0] = bf16_to_f32(qv[j].x & 0xFFFFu);
+            d[1] = bf16_to_f32(qv[j].x >> 16);
+            d[2] = bf16_to_f32(qv[j].y & 0xFFFFu);
+            d[3] = bf16_to_f32(qv[j].y >> 16);
+        }
+    }
     __syncthreads();
-    // ---- scores: thread = (position p, quarter qd of D)
+    // ---- 2a. scores
     {
         float acc[G];
 #pragma unroll
@@ -95,15 +114,15 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
             // per head (the 16 threads of a quarter read the same address)
 #pragma unroll 2
             for (int jj = 0; jj < 8; ++jj) {
-                uint32_t wj = w[0];
+                uint32_t wj = w[0];   // w[jj] by selects: no dynamic register index
 #pragma unroll
                 for (int t = 1; t < 8; ++t) wj = jj == t ? w[t] : wj;
                 const float k0 = e4m3_ref_decode(wj & 0xFFu), k1 = e4m3_ref_decode((wj >> 8) & 0xFFu);
                 const float k2 = e4m3_ref_decode((wj >> 16) & 0xFFu), k3 = e4m3_ref_decode(wj >> 24);
 #pragma unroll
                 for (int h = 0; h < G; ++h) {
-                    const float4 qv = *reinterpret_cast<const float4*>(&qs[h][qd * 32 + jj * 4]);
-                    acc[h] = fmaf(qv.x, k0, fmaf(qv.y, k1, fmaf(qv.z, k2, fmaf(qv.w, k3, acc[h]))));
+                    const float4 qf = *reinterpret_cast<const float4*>(&qs[h][qd * 32 + jj * 4]);
+                    acc[h] = fmaf(qf.x, k0, fmaf(qf.y, k1, fmaf(qf.z, k2, fmaf(qf.w, k3, acc[h]))));
                 }
             }
         }
@@ -122,11 +141,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
     }
     __syncthreads();
-    // ---- per head: chunk max, exp, sum (32 threads per head, 2 positions each)
-    __shared__ float stat[G][2];
+    // ---- 2b. per head: chunk max, exp, sum (32 threads per head, 2 positions each)
     {
-        const int j = threadIdx.x & 31;
-        for (int h = threadIdx.x >> 5; h < G; h += 8) {
+        const int j = tid & 31;
+        for (int h = tid >> 5; h < G; h += 8) {
             const float x0 = ps[h][j], x1 = ps[h][j + 32];
             float mx = fmaxf(x0, x1);
 #pragma unroll
@@ -144,9 +162,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
     }
     __syncthreads();
-    // ---- partial V sums: thread = 4 columns (cq) x 8 of the chunk's
-    // positions (pl), all G heads, from the V words loaded at entry.  The 8
-    // position lanes are summed through LDS.
+    // ---- 2c. partial V sums: thread = 4 columns (cq) x 8 of the chunk's
+    // positions (pl), all G heads; rows past S carry weight 0 (their bytes
+    // decode to finite values).  The 8 position lanes are summed through LDS.
     {
         float4 acc[G];
 #pragma unroll
@@ -164,11 +182,10 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                 acc[h].w = fmaf(w, v3, acc[h].w);
             }
         }
-        __shared__ __align__(16) float vred[8][G][kD];
 #pragma unroll
         for (int h = 0; h < G; ++h) *reinterpret_cast<float4*>(&vred[pl][h][cq * 4]) = acc[h];
         __syncthreads();
-        for (int i = threadIdx.x; i < G * kD; i += 256) {
+        for (int i = tid; i < G * kD; i += 256) {
             const int h = i / kD, col = i % kD;
             float sum = 0.0f;
 #pragma unroll
@@ -183,46 +200,93 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     }
 }
 
-// Workgroup (query head, token), thread = column: merges the chunk records,
+// Workgroup (query head h, token m), 256 threads: merges the chunk records,
 // o = sum_c exp(m_c - M) acc_c / sum_c exp(m_c - M) l_c with M = max_c m_c.
-// The chunk statistics are loaded in parallel (a thread per chunk) and the
-// column sums with many loads in flight.
-constexpr int kMaxChunks = 1024;   // max_pos <= 65536
-__global__ __launch_bounds__(128) void attn_final_kernel(const float* __restrict__ part, float* __restrict__ o,
+// Pass 1 loads every chunk's (m_c, l_c) at once (a thread per chunk); pass 2
+// has thread (column pair cp, chunk phase cq) sum the chunks c = cq mod 4
+// with all of its loads in flight, and the four phases meet in LDS.  The
+// output is fp32 o and/or the MXFP4 rows (oq, os) of bf16(o) (32-blocks of
+// 16 column pairs, the quantizer's rule).
+__global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict__ part, float* __restrict__ o,
+                                                         uint8_t* __restrict__ oq, uint8_t* __restrict__ os,
                                                          const int32_t* __restrict__ dpos, int Hq, int max_pos,
                                                          int nchunk) {
-    const int h = blockIdx.x, m = blockIdx.y, c = threadIdx.x;
+    const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
     const int pos = *dpos + m;
     if (pos < 0 || pos >= max_pos) return;
     const int n = pos / kChunk + 1;            // chunks holding positions 0..pos
     const float* rec = part + ((int64_t)m * Hq + h) * nchunk * kPart;
-    __shared__ float cw[kMaxChunks];           // chunk max, then its scale exp(m_c - M)
-    __shared__ float red[2];
+    __shared__ float cw[kMaxChunks];           // chunk max, then its weight exp(m_c - M)
+    __shared__ float red[4];
+    __shared__ __align__(8) float2 nred[4][64];
+    constexpr int kPer = kMaxChunks / 256;
+    float mc[kPer], lc[kPer];
     float gm = -INFINITY;
-    for (int i = c; i < n; i += kD) {
-        cw[i] = rec[(int64_t)i * kPart];
-        gm = fmaxf(gm, cw[i]);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int c = i * 256 + tid;
+        mc[i] = -INFINITY;
+        lc[i] = 0.0f;
+        if (c < n) {
+            const float2 st = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart);
+            mc[i] = st.x;
+            lc[i] = st.y;
+        }
+        gm = fmaxf(gm, mc[i]);
     }
+    const int lane = tid & 63, wave = tid >> 6;
     gm = mx::wave_reduce_dpp<true>(gm);
-    if ((c & 63) == 0) red[c >> 6] = gm;
+    if (lane == 0) red[wave] = gm;
     __syncthreads();
-    gm = fmaxf(red[0], red[1]);
-    float dpart = 0.0f;
-    for (int i = c; i < n; i += kD) {
-        const float w = expf(cw[i] - gm);
-        cw[i] = w;
-        dpart = fmaf(w, rec[(int64_t)i * kPart + 1], dpart);
+    gm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float den = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+        const int c = i * 256 + tid;
+        if (c < n) {
+            const float w = expf(mc[i] - gm);
+            cw[c] = w;
+            den = fmaf(w, lc[i], den);
+        }
     }
-    dpart = mx::wave_reduce_dpp<false>(dpart);
+    den = mx::wave_reduce_dpp<false>(den);
     __syncthreads();                           // red[] reads above are done
-    if ((c & 63) == 0) red[c >> 6] = dpart;
-    __syncthreads();
-    const float den = red[0] + red[1];
-    float num = 0.0f;
-    const float* col = rec + 4 + c;
+    if (lane == 0) red[wave] = den;
+    __syncthreads();                           // cw[] and red[] complete
+    den = (red[0] + red[1]) + (red[2] + red[3]);
+    // pass 2: thread = (column pair cp = lane, phase cq = wave)
+    float2 num = make_float2(0.0f, 0.0f);
+    const float* colp = rec + 4 + 2 * lane;
 #pragma unroll 16
-    for (int i = 0; i < n; ++i) num = fmaf(cw[i], col[(int64_t)i * kPart], num);
-    o[((int64_t)m * Hq + h) * kD + c] = num / den;
+    for (int c = wave; c < n; c += 4) {
+        const float2 a = *reinterpret_cast<const float2*>(colp + (int64_t)c * kPart);
+        const float w = cw[c];
+        num.x = fmaf(w, a.x, num.x);
+        num.y = fmaf(w, a.y, num.y);
+    }
+    nred[wave][lane] = num;
+    __syncthreads();
+    if (wave != 0) return;
+    num.x = (nred[0][lane].x + nred[1][lane].x) + (nred[2][lane].x + nred[3][lane].x);
+    num.y = (nred[0][lane].y + nred[1][lane].y) + (nred[2][lane].y + nred[3][lane].y);
+    const float r0 = num.x / den, r1 = num.y / den;
+    if (o) *reinterpret_cast<float2*>(o + ((int64_t)m * Hq + h) * kD + 2 * lane) = make_float2(r0, r1);
+    if (oq) {
+        // MXFP4 of bf16(o): a 32-block is 16 lanes; the quantizer's rule
+        const float v0 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r0));
+        const float v1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r1));
+        float am = fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1));
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+        const uint32_t code = mx::e8m0_code(am);
+        const float inv = mx::e8m0_inv_scale(code);
+        uint32_t byte = mx::e2m1_code(v0 * inv) | (mx::e2m1_code(v1 * inv) << 4);
+        byte |= (uint32_t)__shfl_down((int)byte, 1) << 8;
+        byte |= (uint32_t)__shfl_down((int)byte, 2) << 16;
+        const int64_t rowq = (int64_t)m * (Hq * kD / 2) + h * (kD / 2);
+        if ((lane & 3) == 0) *reinterpret_cast<uint32_t*>(oq + rowq + lane) = byte;
+        if ((lane & 15) == 0) os[(int64_t)m * (Hq * kD / 32) + h * (kD / 32) + lane / 16] = (uint8_t)code;
+    }
 }
 
 __global__ __launch_bounds__(256) void kv_write_kernel(const uint16_t* __restrict__ k, const uint16_t* __restrict__ v,
@@ -249,15 +313,20 @@ extern "C" size_t mxfp4_attn_decode_workspace_size(int M, int Hq, int max_pos) {
     return (size_t)((int64_t)M * Hq * nchunk * kPart * sizeof(float));
 }
 
-extern "C" int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
-                                 float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
-                                 size_t workspace_bytes, void* stream) {
-    MXH_REQUIRE(q && kvk && kvv && dpos && sc && o && workspace, "attn_decode: null pointer");
+extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
+                                    float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
+                                    int max_pos, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(q && kvk && kvv && dpos && sc && workspace, "attn_decode: null pointer");
+    MXH_REQUIRE(o || oq, "attn_decode: no output (o and oq both null)");
+    MXH_REQUIRE(!oq == !os, "attn_decode: oq and os go together");
     MXH_REQUIRE(D == kD, "attn_decode: head_dim D=%d (this build supports %d, as the reference's kernels)", D, kD);
     MXH_REQUIRE(M > 0 && M <= 65535 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "attn_decode: M=%d Hq=%d Hkv=%d", M, Hq, Hkv);
     MXH_REQUIRE(max_pos > 0 && max_pos <= kChunk * kMaxChunks, "attn_decode: max_pos=%d (1..%d)", max_pos,
                 kChunk * kMaxChunks);
     MXH_REQUIRE(((uintptr_t)kvk & 15) == 0 && ((uintptr_t)kvv & 3) == 0, "attn_decode: kv cache rows must be aligned");
+    MXH_REQUIRE(((uintptr_t)q & 7) == 0, "attn_decode: q must be 8-byte aligned");
+    MXH_REQUIRE(!o || ((uintptr_t)o & 7) == 0, "attn_decode: o must be 8-byte aligned");
+    MXH_REQUIRE(!oq || ((uintptr_t)oq & 3) == 0, "attn_decode: oq must be 4-byte aligned");
     MXH_REQUIRE(workspace_bytes >= mxfp4_attn_decode_workspace_size(M, Hq, max_pos) && ((uintptr_t)workspace & 15) == 0,
                 "attn_decode: workspace must be 16-byte aligned and hold mxfp4_attn_decode_workspace_size bytes");
     const int G = Hq / Hkv;
@@ -267,22 +336,30 @@ extern "C" int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_
     const dim3 gp(nchunk, Hkv, M);
     const uint16_t* qh = static_cast<const uint16_t*>(q);
     float* part = static_cast<float*>(workspace);
-#define MXH_ATTN_PARTIAL(GG)                                                                                          \
-    hipLaunchKernelGGL(attn_partial_kernel<GG>, gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, Hq, Hkv, max_pos, \
-                       nchunk, invsqrt)
+#define MXH_ATTN(GG)                                                                                         \
+    hipLaunchKernelGGL(attn_partial_kernel<GG>, gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, Hq, Hkv, \
+                       max_pos, nchunk, invsqrt)
     switch (G) {
-        case 1: MXH_ATTN_PARTIAL(1); break;
-        case 2: MXH_ATTN_PARTIAL(2); break;
-        case 4: MXH_ATTN_PARTIAL(4); break;
-        case 8: MXH_ATTN_PARTIAL(8); break;
-        case 16: MXH_ATTN_PARTIAL(16); break;
+        case 1: MXH_ATTN(1); break;
+        case 2: MXH_ATTN(2); break;
+        case 4: MXH_ATTN(4); break;
+        case 8: MXH_ATTN(8); break;
+        case 16: MXH_ATTN(16); break;
         default: MXH_REQUIRE(false, "attn_decode: Hq/Hkv=%d must be 1, 2, 4, 8 or 16", G);
     }
-#undef MXH_ATTN_PARTIAL
+#undef MXH_ATTN
     const int rc = mxh::launch_status("attn_decode (partials)");
     if (rc != MXFP4_OK) return rc;
-    hipLaunchKernelGGL(attn_final_kernel, dim3(Hq, M), dim3(kD), 0, st, part, o, dpos, Hq, max_pos, nchunk);
+    hipLaunchKernelGGL(attn_final_kernel, dim3(Hq, M), dim3(256), 0, st, part, o, oq, os, dpos, Hq, max_pos, nchunk);
     return mxh::launch_status("attn_decode (merge)");
+}
+
+extern "C" int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
+                                 float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
+                                 size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(o, "attn_decode: null pointer");
+    return mxfp4_attn_decode_mx(q, kvk, kvv, dpos, sc, o, nullptr, nullptr, M, Hq, Hkv, D, max_pos, workspace,
+                                workspace_bytes, stream);
 }
 
 extern "C" int mxfp4_kv_write(const void* k, const void* v, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos, int M,

@@ -15,11 +15,12 @@
 //   kernel (first occurrence owns the group, others exit): at M=9 speculative
 //   verify an expert shared by several tokens is streamed from HBM once,
 //   where the reference re-reads it per token.
-// * Each lane streams 16 contiguous bytes per MFMA step and its lane group
-//   (l/16) owns a contiguous run of 32-blocks of the row (block permutation
-//   is free because A and B lanes pair on the same K set), so scale bytes and
-//   data are contiguous per lane.  Weight loads for a K segment are issued
-//   before the MFMAs of the previous segment (software prefetch).
+// * Each lane loads 16 bytes (one 32-block) per MFMA step; at step s lane
+//   group g = l/16 takes block 4s + g, so the four lanes of a row read 64
+//   contiguous bytes per load instruction (a block permutation is free
+//   because A and B lanes pair on the same K set).  Weight loads for a K
+//   segment are issued before the MFMAs of the previous segment (software
+//   prefetch).
 // * The pointer tables travel by value in the kernel arguments, replacing the
 //   reference's host-blocking H2D table copy (src/ext/mxfp4_decode_binding.cpp:58).
 #include "mx_device.h"
@@ -28,7 +29,7 @@
 namespace {
 
 constexpr int kMaxT = MXFP4_MAX_TABLE;
-constexpr int kSeg = 8;  // MFMA K-steps (1024 K) per prefetch segment
+constexpr int kSeg = 4;  // MFMA K-steps (512 K) per prefetch segment
 
 struct HostTable {
     const uint8_t* wp[kMaxT];
@@ -101,7 +102,7 @@ struct SegCtx {
     const uint8_t* asrow;  // A_FP4: activation scale row
     const uint8_t* lq;     // A_SILU: LDS row of quantized h
     const uint8_t* lsc;    // A_SILU: LDS scale row
-    int cbase, steps, nch;
+    int g, steps, nch;   // lane group (block 4s + g at step s), steps, 32-blocks per row
     bool arow_ok;
 };
 
@@ -110,7 +111,7 @@ __device__ __forceinline__ void load_seg(SegBuf& sb, const SegCtx& cx, int s0) {
 #pragma unroll
     for (int j = 0; j < kSeg; ++j) {
         const int s = s0 + j;
-        const int c = cx.cbase + s;
+        const int c = 4 * s + cx.g;
         const bool ok = (s < cx.steps) && (c < cx.nch);
         sb.b[j] = ok ? *reinterpret_cast<const uint4*>(cx.wrow + c * 16) : make_uint4(0, 0, 0, 0);
         sb.bs[j] = ok ? (uint32_t)cx.srow[c] : 127u;
@@ -134,7 +135,7 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
                 aq = sb.a[j];
                 asc = sb.as[j];
             } else {
-                const int c = cx.cbase + s;
+                const int c = 4 * s + cx.g;
                 const bool ok = c < cx.nch;
                 aq = ok ? *reinterpret_cast<const uint4*>(cx.lq + c * 16) : make_uint4(0, 0, 0, 0);
                 asc = ok ? (uint32_t)cx.lsc[c] : 127u;
@@ -186,14 +187,13 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
     const int cnt = s_cnt;
 
     const int nch = a.Kp >> 5;            // 32-blocks per row
-    const int steps = (nch + 3) >> 2;     // MFMA K-steps; lane group g owns blocks [g*steps, g*steps+steps)
+    const int steps = (nch + 3) >> 2;     // MFMA K-steps; lane group g takes blocks g, g + 4, ...
     const int r = lane & 15;
     const int g = lane >> 4;
     const int n0 = blockIdx.x * (16 * NW) + wave * 16;
     const int nrow = min(n0 + r, a.N - 1);
     const uint8_t* wrow = wp + (int64_t)nrow * (a.Kp >> 1);
     const uint8_t* srow = ws + (int64_t)nrow * nch;
-    const int cbase = g * steps;
 
     uint8_t* sq = s_dyn;                              // [16][Kp/2]
     uint8_t* ssc = s_dyn + 16 * (a.Kp >> 1);          // [16][nch]
@@ -243,7 +243,7 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
         mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
         SegBuf s0buf, s1buf;
         const SegCtx cx{wrow, srow, arow, asrow, sq + r * (a.Kp >> 1), ssc + r * nch,
-                        cbase, steps, nch, arow_ok};
+                        g, steps, nch, arow_ok};
         load_seg<AMODE>(s0buf, cx, 0);
         for (int s0 = 0; s0 < steps; s0 += 2 * kSeg) {
             if (s0 + kSeg < steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
@@ -265,6 +265,69 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
             }
         }
         if (AMODE == A_SILU) __syncthreads();  // LDS tile reused by the next row tile
+    }
+}
+
+// Dense y (M, N) = A (M, Kp) W (N, Kp)^T for M <= 16 (lin_pq at decode
+// sizes).  A workgroup holds R row tiles of 16 weight rows x S K-parts, one
+// wave each: wave w takes row tile w % R and the MFMA K-steps [p*spw,
+// (p+1)*spw) of part p = w / R.  Splitting K gives a small-N projection (the
+// router's 128 rows, o_proj's 2048) enough waves to have all of its bytes in
+// flight at once; the S partial sums meet in LDS in a fixed order.
+template <int R, int S>
+__global__ __launch_bounds__(64 * R * S) void lin_small_kernel(const uint8_t* __restrict__ aq,
+                                                               const uint8_t* __restrict__ as,
+                                                               const uint8_t* __restrict__ wp,
+                                                               const uint8_t* __restrict__ ws, float* __restrict__ y,
+                                                               int M, int N, int Kp, int spw) {
+    __shared__ mx::v4f red[S > 1 ? S : 1][R][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int rt = wave % R, part = wave / R;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = (blockIdx.x * R + rt) * 16;
+    const int nch = Kp >> 5;
+    const int steps = (nch + 3) >> 2;
+    const int sb = part * spw;
+    const int se = min(steps, sb + spw);
+    mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (n0 < N && sb < se) {
+        // the part's blocks start at 4 * sb: shift the row pointers there
+        const int nrow = min(n0 + r, N - 1);
+        const int arow_i = min(r, M - 1);
+        const int64_t boff = 4 * (int64_t)sb;
+        const SegCtx cx{wp + (int64_t)nrow * (Kp >> 1) + boff * 16, ws + (int64_t)nrow * nch + boff,
+                        aq + (int64_t)arow_i * (Kp >> 1) + boff * 16, as + (int64_t)arow_i * nch + boff,
+                        nullptr, nullptr, g, se - sb, nch - (int)boff, r < M};
+        SegBuf s0buf, s1buf;
+        load_seg<A_FP4>(s0buf, cx, 0);
+        for (int s0 = 0; s0 < cx.steps; s0 += 2 * kSeg) {
+            if (s0 + kSeg < cx.steps) load_seg<A_FP4>(s1buf, cx, s0 + kSeg);
+            acc = compute_seg<A_FP4>(s0buf, cx, s0, acc);
+            if (s0 + kSeg >= cx.steps) break;
+            if (s0 + 2 * kSeg < cx.steps) load_seg<A_FP4>(s0buf, cx, s0 + 2 * kSeg);
+            acc = compute_seg<A_FP4>(s1buf, cx, s0 + kSeg, acc);
+        }
+    }
+    if constexpr (S > 1) {
+        red[part][rt][lane] = acc;
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int p = 1; p < S; ++p) {
+            const mx::v4f o = red[p][rt][lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += o[i];
+        }
+    }
+    // D[4*(l/16)+i][l%16]: token row, weight row
+    const int col = n0 + r;
+    if (col >= N) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        if (m < M) y[(int64_t)m * N + col] = acc[i];
     }
 }
 
@@ -345,32 +408,44 @@ int check_common(int E, int M, int N, int K, int Kp, const char* op) {
 }  // namespace
 
 namespace mxh {
-// Small-M lin_pq through the grouped GEMV (one group of M rows).
+int lin_small(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc, float* y, int M, int N,
+              int Kp, hipStream_t st);
+
+// Small-M lin_pq: launches of up to 16 activation rows, each with R row
+// tiles x S K-parts per workgroup, S the smallest power of two that gives
+// the launch about 1024 waves (at most 16, and at most one part per MFMA
+// K-step); R = 4 when K is not split.
 int lin_pq_gemv(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc,
                 float* y, int M, int N, int K, int Kp, hipStream_t st) {
-    GemvArgs a{};
-    a.E = 1;
-    a.map = MAP_PLAIN;
-    a.N = N;
-    a.K = K;
-    a.Kp = Kp;
-    a.aq = xq;
-    a.as = xsc;
-    a.out = y;
-    a.ld_out = N;
-    for (int c0 = 0; c0 < M; c0 += kMaxT) {
-        HostTable tab;
-        const int n = (M - c0) < kMaxT ? (M - c0) : kMaxT;
-        for (int i = 0; i < kMaxT; ++i) {
-            tab.wp[i] = wp;
-            tab.ws[i] = wsc;
-        }
-        a.T = n;
-        a.t0 = c0;
-        const int rc = launch_gemv(tab, a, A_FP4, st);
+    (void)K;
+    for (int m0 = 0; m0 < M; m0 += 16) {
+        const int rc = lin_small(xq + (int64_t)m0 * (Kp / 2), xsc + (int64_t)m0 * (Kp / 32), wp, wsc,
+                                 y + (int64_t)m0 * N, M - m0 < 16 ? M - m0 : 16, N, Kp, st);
         if (rc != MXFP4_OK) return rc;
     }
     return MXFP4_OK;
+}
+
+int lin_small(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc, float* y, int M, int N,
+              int Kp, hipStream_t st) {
+    const int tiles = (N + 15) / 16;
+    const int steps = (Kp / 32 + 3) / 4;
+    int S = 1;
+    while (S < 16 && 2 * S <= steps && (int64_t)tiles * S < 1024) S *= 2;
+    const int spw = (steps + S - 1) / S;
+    hipStream_t s = st;
+#define MXH_LIN_SMALL(R_, S_)                                                                                 \
+    hipLaunchKernelGGL((lin_small_kernel<R_, S_>), dim3((unsigned)((tiles + R_ - 1) / R_)), dim3(64 * R_ * S_), \
+                       0, s, xq, xsc, wp, wsc, y, M, N, Kp, spw)
+    switch (S) {
+        case 1: MXH_LIN_SMALL(4, 1); break;
+        case 2: MXH_LIN_SMALL(1, 2); break;
+        case 4: MXH_LIN_SMALL(1, 4); break;
+        case 8: MXH_LIN_SMALL(1, 8); break;
+        default: MXH_LIN_SMALL(1, 16); break;
+    }
+#undef MXH_LIN_SMALL
+    return launch_status("lin_pq_gemv");
 }
 }  // namespace mxh
 

@@ -45,4 +45,31 @@ __device__ __forceinline__ uint32_t e4m3_ref_encode(float v) {
     return sign | ((uint32_t)(eb & 15) << 3) | (uint32_t)(q & 7);
 }
 
+// torch's float -> float8_e4m3fn, the cache write of the reference's batch
+// step (runtime/model_runner_v2.py:256-257, k.to(torch.float8_e4m3fn)):
+// round to nearest even; magnitudes that round past 448 (above 464),
+// infinities and NaN give 0x7F, the format's NaN, with the input's sign;
+// below 2^-6 the subnormal codes q * 2^-9.
+__device__ __forceinline__ uint32_t e4m3_torch_encode(float v) {
+    const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
+    const float a = fabsf(v);
+    if (!(a <= 464.0f)) return sign | 0x7Fu;
+    if (a < 0.015625f) return sign | (uint32_t)(int)rintf(a * 512.0f);   // 0..8; 8 is the smallest normal
+    const uint32_t bits = __float_as_uint(a);
+    const float mant = __uint_as_float((bits & 0x7FFFFFu) | 0x3F800000u);   // [1, 2)
+    int q = (int)rintf((mant - 1.0f) * 8.0f);                             // exact product, RNE
+    uint32_t eb = (bits >> 23) - 120u;                                    // biased exponent e + 7
+    if (q == 8) {
+        q = 0;
+        ++eb;
+    }
+    return sign | (eb << 3) | (uint32_t)q;
+}
+
+// Cache codecs of the KV write: the decode extension's kv_write (0) or
+// torch's float8_e4m3fn conversion (1).
+__device__ __forceinline__ uint32_t e4m3_encode(float v, int codec) {
+    return codec ? e4m3_torch_encode(v) : e4m3_ref_encode(v);
+}
+
 }  // namespace kv

@@ -15,14 +15,17 @@
 //                          (the reference's q_norm / k_norm, result rounded to
 //                          bf16), half-layout RoPE (runtime/model_runner.py:
 //                          28-41, fp32 products, bf16 result), q out as bf16,
-//                          k and bf16(v) written as the reference's E4M3 KV
-//                          bytes at row dpos + m (src/ext/mxfp4_decode.cu:
-//                          437-489 codec).
-//   argmax_advance_kernel  greedy next token per row (logits[m].argmax(),
-//                          first maximum; runtime/decode_v2.py:71); then
-//                          advance_kernel moves the position, dpos += M.
-//                          Both stay on the device, so a captured step graph
-//                          can be replayed step after step.
+//                          k and bf16(v) written as E4M3 KV bytes at row
+//                          dpos + m, in the decode extension's kv_write codec
+//                          (src/ext/mxfp4_decode.cu:437-489, the graph
+//                          runner's write, runtime/model_runner_v3.py:98-101)
+//                          or in torch's float8_e4m3fn conversion (the batch
+//                          step's, runtime/model_runner_v2.py:256-257).
+//   argmax_kernel          greedy next token per row (logits[m].argmax(),
+//                          first maximum; runtime/decode_v2.py:71) over
+//                          slices of the row, and the position dpos += M,
+//                          both on the device, so a captured step graph can
+//                          be replayed step after step.
 #include "kv_codec.h"
 #include "mx_device.h"
 #include "mx_host.h"
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
                                                          const uint16_t* __restrict__ kw, float eps, float theta,
                                                          const int32_t* __restrict__ dpos, int Hq, int Hkv,
                                                          uint16_t* __restrict__ q_out, uint8_t* __restrict__ kvk,
-                                                         uint8_t* __restrict__ kvv, int max_pos) {
+                                                         uint8_t* __restrict__ kvv, int max_pos, int codec) {
     const int m = blockIdx.x;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -183,8 +186,8 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
             const int hv = h - Hq - Hkv;
             if (pos >= 0 && pos < max_pos) {
                 uint8_t* dst = kvv + ((int64_t)pos * Hkv + hv) * kD;
-                dst[lane] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(a)));
-                dst[lane + 64] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(b)));
+                dst[lane] = (uint8_t)kv::e4m3_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(a)), codec);
+                dst[lane + 64] = (uint8_t)kv::e4m3_encode(mx::bf16_to_f32(mx::f32_to_bf16_rne(b)), codec);
             }
             return;
         }
@@ -206,38 +209,80 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
             dst[lane + 64] = bb;
         } else if (pos >= 0 && pos < max_pos) {
             uint8_t* dst = kvk + ((int64_t)pos * Hkv + (h - Hq)) * kD;
-            dst[lane] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(ba));
-            dst[lane + 64] = (uint8_t)kv::e4m3_ref_encode(mx::bf16_to_f32(bb));
+            dst[lane] = (uint8_t)kv::e4m3_encode(mx::bf16_to_f32(ba), codec);
+            dst[lane + 64] = (uint8_t)kv::e4m3_encode(mx::bf16_to_f32(bb), codec);
         }
     }
 }
 
 // ------------------------------------------------------------------ greedy argmax
-// Workgroup per row: the first index of the maximum (NaNs never win).
-__global__ __launch_bounds__(256) void argmax_advance_kernel(const float* __restrict__ logits, int V, int M,
-                                                             int32_t* __restrict__ ids, int32_t* __restrict__ dpos) {
+// Workgroup (slice p of kArgSlice logits, row m): the first index of the
+// slice's maximum (NaNs never win) goes to the workspace; the workgroup that
+// finishes a row last (a counter per row) merges the row's slices, and the
+// one that finishes the last row advances dpos.  Every counter is put back
+// to zero by the workgroup that read it last, so the workspace needs one
+// zero fill when it is allocated and never again (graph replays included).
+constexpr int kArgPer = 16;                  // logits per thread
+constexpr int kArgSlice = 256 * kArgPer;     // logits per workgroup
+
+struct ArgWs {
+    uint32_t* cnt;   // (M) slices done per row, then 1 word: rows done
+    float* val;      // (M, P) slice maxima
+    int32_t* idx;    // (M, P) their indices
+};
+
+__device__ __forceinline__ void arg_better(float& best, int& idx, float ob, int oi) {
+    if (ob > best || (ob == best && oi < idx)) {
+        best = ob;
+        idx = oi;
+    }
+}
+
+__device__ __forceinline__ void arg_wave(float& best, int& idx) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) arg_better(best, idx, __shfl_xor(best, o), __shfl_xor(idx, o));
+}
+
+__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ logits, int V, int M,
+                                                     int32_t* __restrict__ ids, int32_t* __restrict__ dpos,
+                                                     ArgWs ws) {
     __shared__ float bv[4];
     __shared__ int bi[4];
-    const int m = blockIdx.x;
+    __shared__ int last;
+    const int p = blockIdx.x, m = blockIdx.y, P = gridDim.x;
     const float* row = logits + (int64_t)m * V;
+    const int base = p * kArgSlice;
+    // thread t holds logits base + 4 (i * 256 + t) + j, i < 4, j < 4: a
+    // float4 per i, all four loads issued before any is used
+    float v[kArgPer];
+    const bool vec = (V & 3) == 0;   // 16-byte aligned rows
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int e = base + 4 * (i * 256 + threadIdx.x);
+        if (vec && e + 4 <= V) {
+            const float4 f = *reinterpret_cast<const float4*>(row + e);
+            v[4 * i] = f.x;
+            v[4 * i + 1] = f.y;
+            v[4 * i + 2] = f.z;
+            v[4 * i + 3] = f.w;
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) v[4 * i + j] = e + j < V ? row[e + j] : -INFINITY;
+        }
+    }
     float best = -INFINITY;
     int idx = 0x7FFFFFFF;
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float x = row[i];
-        if (x > best) {   // strictly greater: the first maximum of this thread's stripe
-            best = x;
-            idx = i;
-        }
-    }
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ob = __shfl_xor(best, o);
-        const int oi = __shfl_xor(idx, o);
-        if (ob > best || (ob == best && oi < idx)) {
-            best = ob;
-            idx = oi;
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int e = base + 4 * (i * 256 + threadIdx.x) + j;
+            if (v[4 * i + j] > best) {   // strictly greater: indices rise along the scan
+                best = v[4 * i + j];
+                idx = e;
+            }
         }
-    }
+    arg_wave(best, idx);
     const int wave = threadIdx.x >> 6;
     if ((threadIdx.x & 63) == 0) {
         bv[wave] = best;
@@ -245,17 +290,41 @@ __global__ __launch_bounds__(256) void argmax_advance_kernel(const float* __rest
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
-            if (bv[w] > best || (bv[w] == best && bi[w] < idx)) {
-                best = bv[w];
-                idx = bi[w];
-            }
+        for (int w = 1; w < 4; ++w) arg_better(best, idx, bv[w], bi[w]);
+        ws.val[(int64_t)m * P + p] = best;
+        ws.idx[(int64_t)m * P + p] = idx;
+        __threadfence();
+        const uint32_t done = __hip_atomic_fetch_add(&ws.cnt[m], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = done == (uint32_t)(P - 1);
+    }
+    __syncthreads();
+    if (!last || wave != 0) return;
+    // the row's last workgroup: merge its P slices (wave 0)
+    const int lane = threadIdx.x & 63;
+    best = -INFINITY;
+    idx = 0x7FFFFFFF;
+    for (int q = lane; q < P; q += 64)
+        arg_better(best, idx, __hip_atomic_load(&ws.val[(int64_t)m * P + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                   __hip_atomic_load(&ws.idx[(int64_t)m * P + q], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    arg_wave(best, idx);
+    if (lane == 0) {
         ids[m] = idx == 0x7FFFFFFF ? 0 : idx;
+        __hip_atomic_store(&ws.cnt[m], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (dpos) {
+            __threadfence();
+            const uint32_t rows = __hip_atomic_fetch_add(&ws.cnt[M], 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            if (rows == (uint32_t)(M - 1)) {
+                *dpos += M;
+                __hip_atomic_store(&ws.cnt[M], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
     }
 }
 
-__global__ void advance_kernel(int32_t* dpos, int M) {
-    if (threadIdx.x == 0) *dpos += M;
+size_t argmax_ws_bytes(int M, int V) {
+    const int64_t P = (V + kArgSlice - 1) / kArgSlice;
+    const int64_t head = ((int64_t)(M + 1) * 4 + 255) / 256 * 256;
+    return (size_t)(head + 2 * (int64_t)M * P * 4);
 }
 
 }  // namespace
@@ -292,22 +361,35 @@ extern "C" int mxfp4_rmsnorm_quant(const void* x, const float* resid, const void
 
 extern "C" int mxfp4_qk_norm_rope_kv(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
                                      float theta, const int32_t* dpos, int M, int Hq, int Hkv, int D, void* q_out,
-                                     uint8_t* kvk, uint8_t* kvv, int max_pos, void* stream) {
+                                     uint8_t* kvk, uint8_t* kvv, int max_pos, int codec, void* stream) {
     MXH_REQUIRE(qkv && q_norm_w && k_norm_w && dpos && q_out && kvk && kvv, "qk_norm_rope_kv: null pointer");
+    MXH_REQUIRE(codec == 0 || codec == 1, "qk_norm_rope_kv: codec %d (0 kv_write's, 1 torch float8_e4m3fn)", codec);
     MXH_REQUIRE(D == kD, "qk_norm_rope_kv: D=%d (the reference's kernels assume 128)", D);
     MXH_REQUIRE(M > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0 && max_pos > 0, "qk_norm_rope_kv: M=%d Hq=%d Hkv=%d max_pos=%d", M,
                 Hq, Hkv, max_pos);
     hipLaunchKernelGGL(qk_rope_kv_kernel, dim3(M, (Hq + 2 * Hkv + 3) / 4), dim3(256), 0, mxh::as_stream(stream), qkv,
                        static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w), eps, theta, dpos,
-                       Hq, Hkv, static_cast<uint16_t*>(q_out), kvk, kvv, max_pos);
+                       Hq, Hkv, static_cast<uint16_t*>(q_out), kvk, kvv, max_pos, codec);
     return mxh::launch_status("qk_norm_rope_kv");
 }
 
-extern "C" int mxfp4_argmax_advance(const float* logits, int M, int V, int32_t* ids, int32_t* dpos, void* stream) {
-    MXH_REQUIRE(logits && ids, "argmax_advance: null pointer");
-    MXH_REQUIRE(M > 0 && V > 0, "argmax_advance: M=%d V=%d", M, V);
-    hipStream_t st = mxh::as_stream(stream);
-    hipLaunchKernelGGL(argmax_advance_kernel, dim3(M), dim3(256), 0, st, logits, V, M, ids, dpos);
-    if (dpos) hipLaunchKernelGGL(advance_kernel, dim3(1), dim3(64), 0, st, dpos, M);
+extern "C" size_t mxfp4_argmax_workspace_size(int M, int V) {
+    if (M <= 0 || V <= 0) return 0;
+    return argmax_ws_bytes(M, V);
+}
+
+extern "C" int mxfp4_argmax_advance(const float* logits, int M, int V, int32_t* ids, int32_t* dpos, void* ws,
+                                    size_t ws_bytes, void* stream) {
+    MXH_REQUIRE(logits && ids && ws, "argmax_advance: null pointer");
+    MXH_REQUIRE(M > 0 && M <= 65535 && V > 0, "argmax_advance: M=%d V=%d", M, V);
+    MXH_REQUIRE(ws_bytes >= argmax_ws_bytes(M, V), "argmax_advance: workspace of %zu bytes, %zu needed", ws_bytes,
+                argmax_ws_bytes(M, V));
+    MXH_REQUIRE(((uintptr_t)ws & 255) == 0, "argmax_advance: workspace must be 256-byte aligned");
+    const int P = (V + kArgSlice - 1) / kArgSlice;
+    const int64_t head = ((int64_t)(M + 1) * 4 + 255) / 256 * 256;
+    uint8_t* w = static_cast<uint8_t*>(ws);
+    ArgWs a{reinterpret_cast<uint32_t*>(w), reinterpret_cast<float*>(w + head),
+            reinterpret_cast<int32_t*>(w + head + (int64_t)M * P * 4)};
+    hipLaunchKernelGGL(argmax_kernel, dim3(P, M), dim3(256), 0, mxh::as_stream(stream), logits, V, M, ids, dpos, a);
     return mxh::launch_status("argmax_advance");
 }

@@ -19,8 +19,11 @@ memory, so one step can be captured in a HIP graph and replayed step after
 step (DecodeStep.capture).  MoE: M = 1 uses the fused one-launch layer with
 in-kernel routing on the bf16 activations (mxfp4_moe_decode_layer_routed);
 M > 1 uses route_topk + the drop-in grouped ops on MXFP4 activations, as
-forward_batch does.  The KV cache uses the reference's E4M3 byte codec
-(kv_write / attn_decode) with no extra scale.
+forward_batch does.  The KV cache holds E4M3 bytes with no extra scale, read
+by attn_decode's codec; they are written the way the matching reference
+step writes them: M = 1 with the decode extension's kv_write codec (the
+graph runner, runtime/model_runner_v3.py:98-101), M > 1 with torch's
+float8_e4m3fn conversion (forward_batch, runtime/model_runner_v2.py:256-257).
 """
 import ctypes
 from dataclasses import dataclass, field
@@ -156,6 +159,7 @@ class DecodeStep:
     def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda"):
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
+        self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
         c = cfg
         if c.head_dim != 128:
             raise RuntimeError("head_dim must be 128 (attention kernels)")
@@ -178,13 +182,14 @@ class DecodeStep:
         buf("qkv", (M, c.qkv_rows), f32)
         buf("q", (M, Hq, D), bf16)
         buf("sc", (M, Hq, self.max_pos), f32)
-        buf("att", (M, Hq, D), f32)
         buf("aq", (M, Hq * D // 2), u8)
         buf("as_", (M, Hq * D // 32), u8)
         buf("oproj", (M, H), f32)
         buf("glog", (M, c.n_experts), f32)
         buf("moe", (M, H), f32)
         buf("logits", (M, c.vocab), f32)
+        nb = self.lib.mxfp4_argmax_workspace_size(M, c.vocab)
+        buf("arg_ws", ((nb + 255) // 256 * 256,), u8)   # zero-filled once; each call leaves it so
         nb = self.lib.mxfp4_attn_decode_workspace_size(M, Hq, self.max_pos)
         buf("attn_ws", ((nb + 15) // 16 * 16,), u8)
         # KV cache of every layer: (L, max_pos, Hkv, D) E4M3 bytes
@@ -256,13 +261,12 @@ class DecodeStep:
             kvk, kvv = b.kvk[l], b.kvv[l]
             self._ck(lib.mxfp4_qk_norm_rope_kv(b.qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), c.rms_eps,
                                                c.rope_theta, b.dpos.data_ptr(), M, Hq, Hkv, D, b.q.data_ptr(),
-                                               kvk.data_ptr(), kvv.data_ptr(), self.max_pos, s), "qk_norm_rope_kv")
-            self._ck(lib.mxfp4_attn_decode(b.q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), b.dpos.data_ptr(),
-                                           b.sc.data_ptr(), b.att.data_ptr(), M, Hq, Hkv, D, self.max_pos,
-                                           b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode")
-            # o = attention.to(bf16) -> MXFP4 -> o_proj
-            self._ck(lib.mxfp4_quantize_rows(b.att.data_ptr(), 2, 2, Hq * D, M, Hq * D, Hq * D, b.aq.data_ptr(),
-                                             b.as_.data_ptr(), s), "quantize_rows")
+                                               kvk.data_ptr(), kvv.data_ptr(), self.max_pos, self.kv_codec, s),
+                     "qk_norm_rope_kv")
+            # attention, its output straight to MXFP4 of bf16(o) for o_proj
+            self._ck(lib.mxfp4_attn_decode_mx(b.q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), b.dpos.data_ptr(),
+                                              b.sc.data_ptr(), None, b.aq.data_ptr(), b.as_.data_ptr(), M, Hq, Hkv, D,
+                                              self.max_pos, b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode")
             self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
             # x = x + bf16(o); post-attention norm; router logits
             self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.oproj.data_ptr(), lw.post_norm.data_ptr(), c.rms_eps, M,
@@ -282,8 +286,8 @@ class DecodeStep:
                                          xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s),
                  "rmsnorm_quant")
         self._lin(b.yq, b.ys, m.lm_head, c.vocab, H, b.logits, s)
-        self._ck(lib.mxfp4_argmax_advance(b.logits.data_ptr(), M, c.vocab, b.ids.data_ptr(), b.dpos.data_ptr(), s),
-                 "argmax_advance")
+        self._ck(lib.mxfp4_argmax_advance(b.logits.data_ptr(), M, c.vocab, b.ids.data_ptr(), b.dpos.data_ptr(),
+                                          b.arg_ws.data_ptr(), b.arg_ws.numel(), s), "argmax_advance")
         self.x_final = xb
 
     def _moe_batch(self, ex, s):

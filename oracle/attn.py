@@ -14,6 +14,12 @@ exponent field 15 to 0x7F; the decoder reads subnormal codes as m * 2^-6 and
 exponent-15 codes as 448 * (1 + m/8).  tests/test_oracle_attn.py pins both
 against torch's OCP float8_e4m3fn where the two definitions agree and against
 closed forms where they do not.
+
+The reference's batch step writes its cache with torch instead
+(runtime/model_runner_v2.py:256-257, k.to(torch.float8_e4m3fn)), read back by
+the same attn_decode: e4m3_torch_encode restates that conversion (round to
+nearest even, 0x7F above 464 and for inf/NaN); tests/test_oracle_attn.py pins
+it against torch on every bf16 bit pattern.
 """
 import numpy as np
 
@@ -40,6 +46,28 @@ def e4m3_ref_encode(v):
     return np.where(a == 0, sign, out).astype(np.uint8)
 
 
+def e4m3_torch_encode(v):
+    """float32 array -> uint8 codes of torch's float -> float8_e4m3fn: the
+    nearest E4M3 value, ties to the even mantissa; subnormals q * 2^-9 below
+    2^-6; magnitudes above 464 (which round past the largest finite 448),
+    inf and NaN -> 0x7F; the sign bit is the input's."""
+    v = np.asarray(v, np.float32)
+    sign = ((v.view(np.uint32) >> 24) & 0x80).astype(np.int64)
+    a = np.abs(v).astype(np.float64)
+    with np.errstate(invalid="ignore", over="ignore"):
+        f, e = np.frexp(np.where(np.isfinite(a), a, 1.0))      # a = f * 2^e, f in [0.5, 1)
+        q = np.rint((2.0 * f - 1.0) * 8.0).astype(np.int64)    # mantissa of 2f in [1, 2)
+        eb = e.astype(np.int64) - 1 + 7
+        carry = q == 8
+        q = np.where(carry, 0, q)
+        eb = np.where(carry, eb + 1, eb)
+        normal = (eb << 3) | q
+        sub = np.rint(np.where(np.isfinite(a), a, 0.0) * 512.0).astype(np.int64)
+        code = np.where(a < 2.0 ** -6, sub, normal)
+        code = np.where(~(a <= 464.0), 0x7F, code)
+    return (sign | code).astype(np.uint8)
+
+
 def e4m3_ref_decode(b):
     """uint8 codes -> float32, the reference's e4m3_to_f32."""
     b = np.asarray(b, np.uint8).astype(np.int64)
@@ -50,9 +78,11 @@ def e4m3_ref_decode(b):
     return np.where(b & 0x80, -v, v).astype(np.float32)
 
 
-def kv_write_ref(k, v, kvk, kvv, base):
+def kv_write_ref(k, v, kvk, kvv, base, codec=0):
     """k, v (M, Hkv, D) float32 (bf16 values); writes rows base+m < max_pos of
-    the uint8 caches (max_pos, Hkv, D) in place; base < 0 writes nothing."""
+    the uint8 caches (max_pos, Hkv, D) in place; base < 0 writes nothing.
+    codec 0: the decode extension's kv_write encoder; 1: torch's."""
+    enc = e4m3_torch_encode if codec else e4m3_ref_encode
     kvk, kvv = np.asarray(kvk), np.asarray(kvv)
     M = k.shape[0]
     if base < 0:
@@ -60,8 +90,8 @@ def kv_write_ref(k, v, kvk, kvv, base):
     for m in range(M):
         pos = base + m
         if pos < kvk.shape[0]:
-            kvk[pos] = e4m3_ref_encode(k[m])
-            kvv[pos] = e4m3_ref_encode(v[m])
+            kvk[pos] = enc(k[m])
+            kvv[pos] = enc(v[m])
     return kvk, kvv
 
 

@@ -64,7 +64,7 @@ def argmax_ref(logits):
     return np.argmax(np.asarray(logits), axis=-1).astype(np.int32)
 
 
-def step_ref(w, cfg, ids, base, kvk, kvv, fused_moe, x_teacher=None):
+def step_ref(w, cfg, ids, base, kvk, kvv, fused_moe, x_teacher=None, kv_codec=0):
     """One step of M = len(ids) tokens at positions base..base+M-1.
 
     w: dict of numpy arrays (keys as DecodeStep's weights: embed, layers[l]
@@ -77,7 +77,10 @@ def step_ref(w, cfg, ids, base, kvk, kvv, fused_moe, x_teacher=None):
     residual stream after each layer as another implementation computed it;
     layer l > 0 and the head then start from x_teacher[l-1] / x_teacher[-1]
     instead of this function's own value (teacher forcing, so each layer is
-    compared on identical inputs).  Returns (logits (M, V) float64,
+    compared on identical inputs).  kv_codec: the cache encoder, 0 the decode
+    extension's kv_write (the graph runner, runtime/model_runner_v3.py:
+    98-101), 1 torch's float8_e4m3fn (forward_batch,
+    runtime/model_runner_v2.py:256-257).  Returns (logits (M, V) float64,
     [x after each layer] bf16 values)."""
     ids = np.asarray(ids)
     M = len(ids)
@@ -98,7 +101,7 @@ def step_ref(w, cfg, ids, base, kvk, kvv, fused_moe, x_teacher=None):
         qn = rms_norm_ref(q, lw["q_norm"], eps, bf16_input=False)
         kn = rms_norm_ref(k, lw["k_norm"], eps, bf16_input=False)
         qr, kr = rope_ref(qn, pos, cfg.rope_theta), rope_ref(kn, pos, cfg.rope_theta)
-        attn_ref.kv_write_ref(kr, bf16(v), kvk[l], kvv[l], base)
+        attn_ref.kv_write_ref(kr, bf16(v), kvk[l], kvv[l], base, kv_codec)
         o_att, _ = attn_ref.attn_decode_ref(qr, kvk[l], kvv[l], base)
         of = bf16(o_att.astype(np.float32)).reshape(M, Hq * D)
         aq, as_ = fmt.quantize_rows(of)

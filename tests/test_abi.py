@@ -46,6 +46,9 @@ def test_workspace_size(lib):
     # header + memos (4096 B), three h buffers of 8*24*32 words, three x buffers of 2048 words
     assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 4096 + 3 * (6144 + 2048) * 4
     assert lib.mxfp4_decode_stack_workspace_size(0, 2048, 768) == 0
+    # argmax: 256-byte counter head, then (M, P) maxima and indices, P = ceil(V / 4096) slices
+    assert lib.mxfp4_argmax_workspace_size(8, 151936) == 256 + 2 * 8 * 38 * 4
+    assert lib.mxfp4_argmax_workspace_size(0, 100) == 0
 
 
 @pytest.mark.parametrize("call,msg", [
@@ -68,6 +71,9 @@ def test_workspace_size(lib):
                                         1 << 20, None), "n_layers=0"),
     (lambda L: L.mxfp4_moe_decode_stack(16, 16, 16, 16, 2, 128, 8, 2048, 768, 16, None, None, 0, 256,
                                         4096, None), "workspace too small"),
+    (lambda L: L.mxfp4_argmax_advance(256, 2, 5000, 256, None, 256, 256 + 8, None), "workspace of"),
+    (lambda L: L.mxfp4_argmax_advance(256, 2, 5000, 256, None, 16, 4096, None), "256-byte aligned"),
+    (lambda L: L.mxfp4_argmax_advance(256, 2, 5000, 256, None, None, 4096, None), "null pointer"),
 ])
 def test_argument_checks_fail_on_host(lib, call, msg):
     rc = call(lib)

@@ -15,6 +15,7 @@ import torch
 
 from moe_fused_inference_amd import _lib
 from oracle import attn
+from oracle import mxfp4 as fmt
 from tests.gpu_helpers import DEV, assert_close, log, np_
 
 pytestmark = pytest.mark.gpu
@@ -91,7 +92,7 @@ def test_attn_decode_rows_past_the_cache_are_skipped(dext):
     dpos = torch.tensor([max_pos - 1], dtype=torch.int32, device=DEV)
     lib = _lib.load()
     wsb = lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
-    ws = torch.empty(wsb, dtype=torch.uint8, device=DEV)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
     _lib.check(lib.mxfp4_attn_decode(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(), sc.data_ptr(),
                                      o.data_ptr(), M, Hq, Hkv, D, max_pos, ws.data_ptr(), wsb,
                                      torch.cuda.current_stream().cuda_stream), "attn_decode")
@@ -141,3 +142,40 @@ def test_attn_decode_in_graph_follows_dpos(dext):
         assert np.array_equal(np_(kvk), ck) and np.array_equal(np_(kvv), cv)
         ref, _ = attn.attn_decode_ref(q.float().cpu().numpy(), ck, cv, pos)
         assert_close(np_(out), ref, what=f"graph replay at dpos={pos}")
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,max_pos,base", [(1, 32, 4, 4096, 4095), (4, 32, 4, 1000, 700), (3, 16, 1, 200, 0),
+                                                   (2, 8, 8, 128, 63)])
+def test_attn_decode_mx_quantized_output(M, Hq, Hkv, max_pos, base):
+    """The attention output written as MXFP4 rows of bf16(o) equals
+    mxfp4_quantize_rows (bf16 mode) of the fp32 output bit for bit, o itself
+    equals the plain entry point's bit for bit, on three calls in a row
+    that share one workspace."""
+    lib = _lib.load()
+    rng = np.random.default_rng(M * 1000 + base)
+    D = 128
+    kvk = torch.from_numpy(_cache(rng, max_pos, Hkv, D)).to(DEV)
+    kvv = torch.from_numpy(_cache(rng, max_pos, Hkv, D)).to(DEV)
+    dpos = torch.tensor([base], dtype=torch.int32, device=DEV)
+    sc = torch.zeros((M, Hq, max_pos), dtype=torch.float32, device=DEV)
+    wsb = lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    for call in range(3):
+        q = _bf16(rng.standard_normal((M, Hq, D)) * (1 + call)).to(DEV)
+        o1 = torch.zeros((M, Hq, D), dtype=torch.float32, device=DEV)
+        o2 = torch.zeros((M, Hq, D), dtype=torch.float32, device=DEV)
+        oq = torch.zeros((M, Hq * D // 2), dtype=torch.uint8, device=DEV)
+        os_ = torch.zeros((M, Hq * D // 32), dtype=torch.uint8, device=DEV)
+        _lib.check(lib.mxfp4_attn_decode(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(), sc.data_ptr(),
+                                         o1.data_ptr(), M, Hq, Hkv, D, max_pos, ws.data_ptr(), wsb, st), "attn_decode")
+        _lib.check(lib.mxfp4_attn_decode_mx(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(),
+                                            sc.data_ptr(), o2.data_ptr(), oq.data_ptr(), os_.data_ptr(), M, Hq, Hkv, D,
+                                            max_pos, ws.data_ptr(), wsb, st), "attn_decode_mx")
+        torch.cuda.synchronize()
+        live = [m for m in range(M) if base + m < max_pos]
+        assert torch.equal(o1[live], o2[live]), f"call {call}"
+        rq, rs = fmt.quantize_rows(fmt.bf16_round(np_(o2).reshape(M, Hq * D)))
+        assert np.array_equal(np_(oq)[live], rq[live]) and np.array_equal(np_(os_)[live], rs[live]), f"call {call}"
+        ref, _ = attn.attn_decode_ref(q.float().cpu().numpy(), np_(kvk), np_(kvv), base)
+        assert_close(np_(o2)[live], ref[live], what=f"attn_decode_mx call {call}")

@@ -50,6 +50,8 @@ def tiny():
 
 def run_steps(model, wnp, M, n_steps, fused):
     st = DecodeStep(model, CFG, M=M, max_pos=MAX_POS, device=DEV)
+    codec = st.kv_codec          # M = 1: kv_write's encoder (graph runner); M > 1: torch's (forward_batch)
+    assert codec == (0 if M == 1 else 1)
     st.fill_cache(CTX, seed=5)
     ids = np.array([(37 * (i + 1)) % CFG.vocab for i in range(M)], np.int32)
     st.set_state(ids, CTX)
@@ -71,14 +73,15 @@ def run_steps(model, wnp, M, n_steps, fused):
         what = f"M={M} step {step} pos {pos}"
         # teacher-forced: every layer and the head start from the GPU's own
         # residual stream, so each is compared on identical inputs
-        tf_logits, tf_xs = sref.step_ref(wnp, CFG, ids, pos, kvk.copy(), kvv.copy(), fused, x_teacher=xs)
+        tf_logits, tf_xs = sref.step_ref(wnp, CFG, ids, pos, kvk.copy(), kvv.copy(), fused, x_teacher=xs,
+                                         kv_codec=codec)
         for l in range(CFG.n_layers):
             assert_close(xs[l], tf_xs[l], 0.99999, 5e-3, what=f"{what} layer {l} residual (same input)")
         assert_close(logits, tf_logits, 0.9999, 1e-2, what=f"{what} logits (same input)")
         # free-running: the oracle's own chain end to end.  The final MXFP4
         # requantization of the normed residual turns a few bf16 flips of x
         # into whole-nibble (or whole-block scale) changes, so only cos is bound.
-        ref_logits, ref_xs = sref.step_ref(wnp, CFG, ids, pos, kvk, kvv, fused)
+        ref_logits, ref_xs = sref.step_ref(wnp, CFG, ids, pos, kvk, kvv, fused, kv_codec=codec)
         for l in range(CFG.n_layers):
             assert_close(xs[l], ref_xs[l], 0.9999, 1e-2, what=f"{what} layer {l} residual (own chain)")
         assert_close(logits, ref_logits, 0.999, 1.0, what=f"{what} logits (own chain)")
@@ -179,6 +182,55 @@ def test_rmsnorm_quant(resid):
     assert np.array_equal(np_(yq), q) and np.array_equal(np_(ys), s)
 
 
+@pytest.mark.parametrize("codec", [0, 1])
+def test_qk_norm_rope_kv(codec):
+    """Head RMSNorm + RoPE + KV write against oracle/step.py and the codecs
+    of oracle/attn.py on the same fp32 projections: V bytes exactly the
+    codec of bf16(v); q (bf16) and the K bytes up to the rsqrt / cos / sin
+    ulps of fp32 (a bf16 flip moves a K byte by at most one code)."""
+    from oracle import attn as aref
+    lib = _lib.load()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(21 + codec)
+    M, Hq, Hkv, D, max_pos, base = 3, 8, 2, 128, 300, 290
+    qkv = torch.randn((M, (Hq + 2 * Hkv) * D), generator=g, device=DEV) * 2
+    qkv[0, (Hq + Hkv) * D:(Hq + Hkv) * D + 4] = torch.tensor([464.0, 470.0, 1.0625, 2.0 ** -8 * 3], device=DEV)
+    qw = (1 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    dpos = torch.tensor([base], dtype=torch.int32, device=DEV)
+    q_out = torch.zeros((M, Hq, D), dtype=torch.bfloat16, device=DEV)
+    kvk = torch.zeros((max_pos, Hkv, D), dtype=torch.uint8, device=DEV)
+    kvv = torch.zeros((max_pos, Hkv, D), dtype=torch.uint8, device=DEV)
+    _lib.check(lib.mxfp4_qk_norm_rope_kv(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), 1e-6, 1e6, dpos.data_ptr(), M,
+                                         Hq, Hkv, D, q_out.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), max_pos, codec,
+                                         None), "qk_norm_rope_kv")
+    torch.cuda.synchronize()
+    x = np_(qkv)
+    pos = np.arange(base, base + M)
+    q = sref.rope_ref(sref.rms_norm_ref(x[:, :Hq * D].reshape(M, Hq, D), np_(qw.float()), 1e-6, bf16_input=False),
+                      pos, 1e6)
+    k = sref.rope_ref(sref.rms_norm_ref(x[:, Hq * D:(Hq + Hkv) * D].reshape(M, Hkv, D), np_(kw.float()), 1e-6,
+                                        bf16_input=False), pos, 1e6)
+    v = fmt.bf16_round(x[:, (Hq + Hkv) * D:].reshape(M, Hkv, D))
+    ck, cv = np.zeros((max_pos, Hkv, D), np.uint8), np.zeros((max_pos, Hkv, D), np.uint8)
+    aref.kv_write_ref(k, v, ck, cv, base, codec)          # rows past max_pos are skipped on both sides
+    assert np.array_equal(np_(kvv), cv)
+    assert_close(np_(q_out.float()), q, 0.99999, 2e-2, what="q after norm + RoPE")
+    gk = np_(kvk).astype(np.int64)
+    assert np.mean(gk == ck) >= 0.995 and np.abs(gk - ck).max() <= 1
+    if codec:
+        assert np_(kvv)[base, 0, :4].tolist() == [0x7E, 0x7F, 0x38, 0x06]   # tie to 448, past it, tie, subnormal
+    else:
+        assert np_(kvv)[base, 0, :4].tolist() == [0x7F, 0x7F, 0x39, 0x01]   # saturation, half away from zero
+
+
+def _argmax(lib, lg, ids, dpos, ws):
+    _lib.check(lib.mxfp4_argmax_advance(lg.data_ptr(), lg.shape[0], lg.shape[1], ids.data_ptr(),
+                                        dpos.data_ptr() if dpos is not None else None, ws.data_ptr(), ws.numel(),
+                                        None), "argmax")
+    torch.cuda.synchronize()
+
+
 def test_argmax_first_maximum():
     lib = _lib.load()
     lg = torch.zeros((3, 1000), dtype=torch.float32, device=DEV)
@@ -190,6 +242,36 @@ def test_argmax_first_maximum():
     lg[2, 4] = 1.0
     ids = torch.empty(3, dtype=torch.int32, device=DEV)
     dpos = torch.tensor([10], dtype=torch.int32, device=DEV)
-    _lib.check(lib.mxfp4_argmax_advance(lg.data_ptr(), 3, 1000, ids.data_ptr(), dpos.data_ptr(), None), "argmax")
-    torch.cuda.synchronize()
+    ws = torch.zeros(lib.mxfp4_argmax_workspace_size(3, 1000), dtype=torch.uint8, device=DEV)
+    _argmax(lib, lg, ids, dpos, ws)
     assert ids.tolist() == [17, 999, 4] and int(dpos.item()) == 13
+    assert int(ws[:16].count_nonzero()) == 0   # row counters back at zero
+
+
+@pytest.mark.parametrize("V", [151936, 4097, 12289, 1003])
+def test_argmax_slices_match_torch(V):
+    """Rows spanning several workgroup slices (ties across slices, a row
+    whose maximum is in the last partial slice, odd V on the scalar path),
+    three calls in a row on one workspace, dpos advanced once per call."""
+    lib = _lib.load()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(V)
+    M = 5
+    lg = torch.randn((M, V), generator=g, device=DEV)
+    lg[1, V // 3] = 50.0
+    lg[1, V - 1] = 50.0               # tie across slices: the first wins
+    lg[2, V - 1] = 60.0               # maximum at the very end
+    lg[3, :] = float("nan")
+    lg[3, V // 2] = -1.0              # one finite value among NaNs
+    lg[4] = lg[4].round()             # many exact ties
+    ws = torch.zeros(lib.mxfp4_argmax_workspace_size(M, V), dtype=torch.uint8, device=DEV)
+    dpos = torch.tensor([7], dtype=torch.int32, device=DEV)
+    ids = torch.empty(M, dtype=torch.int32, device=DEV)
+    lgn = np_(lg)
+    for call in range(3):
+        _argmax(lib, lg, ids, dpos, ws)
+        want = sref.argmax_ref(np.where(np.isnan(lgn), -np.inf, lgn))
+        assert np.array_equal(np_(ids), want), (call, np_(ids), want)
+        assert int(dpos.item()) == 7 + M * (call + 1)
+    head = (M + 1) * 4
+    assert int(ws[:head].count_nonzero()) == 0, "row counters not reset"

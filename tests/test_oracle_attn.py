@@ -114,3 +114,20 @@ def test_kv_write_ref_rows():
     attn.kv_write_ref(k, v, kvk, kvv, base=8)
     assert np.array_equal(kvk[8], attn.e4m3_ref_encode(k[0])) and np.array_equal(kvv[9], attn.e4m3_ref_encode(v[1]))
     assert not kvk[:8].any()
+
+
+def test_torch_encode_matches_torch_on_every_bf16_pattern():
+    """e4m3_torch_encode is torch's float -> float8_e4m3fn conversion, the
+    reference batch step's cache write: identical bytes on all 65536 bf16 bit
+    patterns (NaNs, infinities, subnormals, both zeros) and on random fp32."""
+    allv = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).float().numpy()
+    want = torch.from_numpy(allv).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    got = attn.e4m3_torch_encode(allv)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:10]
+    rng = np.random.default_rng(0)
+    f = (rng.standard_normal(200000) * np.exp2(rng.integers(-12, 10, 200000))).astype(np.float32)
+    f[:6] = [464.0, 464.00003, -464.0, 479.9, 2.0 ** -7 * 1.5, 2.0 ** -10]   # tie to 448, past it, subnormal ties
+    want = torch.from_numpy(f).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(attn.e4m3_torch_encode(f), want)
+    # and the closed forms: 448 is the largest finite code, ties go to the even mantissa
+    assert attn.e4m3_torch_encode(np.float32([448.0, 456.0, 1.0625, 1.1875]))[0:4].tolist() == [0x7E, 0x7E, 0x38, 0x3A]
