@@ -43,161 +43,181 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 constexpr int kPart = 132;       // floats per partial record: max, sum, 128 column sums, pad
 constexpr int kMaxChunks = 1024; // max_pos <= 65536
 
-// Workgroup (64-position chunk, kv head g, token m):
-//  1. the chunk's K and V rows and the group's q are loaded before anything
-//     waits (the position only masks; rows past max_pos are clamped), so the
-//     workgroup pays one memory latency;
-//  2. scores of all G query heads of the group (raw dot products also go to
-//     sc), per head the chunk max, exp(x - max) and sum, and the partial
-//     weighted sum of V -> one record per (token, head, chunk).
-template <int G>
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// D (16 x 16 fp32) += A (16 x 32 bf16) B (32 x 16 bf16); lane l holds row /
+// column l % 16 of A / B and 8 values of the reduction dimension, the same 8
+// for A and B (which 8 is immaterial as long as both sides agree); D[4*(l/16)
+// + i][l % 16] is element i of the lane's result.
+__device__ __forceinline__ mx::v4f mfma_bf16(uint4 a, uint4 b, mx::v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b), c,
+                                                   0, 0, 0);
+}
+
+// A cache byte (the reference's codec) as bf16 bits: every value of the
+// codec, 840 included, is a bf16 value, so this is exact.
+__device__ __forceinline__ uint32_t kv_bf16(uint32_t b) { return __float_as_uint(e4m3_ref_decode(b)) >> 16; }
+__device__ __forceinline__ uint32_t pack_bf16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
+__device__ __forceinline__ uint4 kv8_bf16(uint2 w) {
+    return make_uint4(pack_bf16(kv_bf16(w.x & 0xFFu), kv_bf16((w.x >> 8) & 0xFFu)),
+                      pack_bf16(kv_bf16((w.x >> 16) & 0xFFu), kv_bf16(w.x >> 24)),
+                      pack_bf16(kv_bf16(w.y & 0xFFu), kv_bf16((w.y >> 8) & 0xFFu)),
+                      pack_bf16(kv_bf16((w.y >> 16) & 0xFFu), kv_bf16(w.y >> 24)));
+}
+
+// Workgroup (64-position chunk, kv head g, MT consecutive tokens): R = 16*RT
+// query rows, row r = (token m0 + r / G, head g*G + r % G), all sharing the
+// chunk's K and V rows, which are loaded and decoded once.
+//  1. loads first: K bytes in the MFMA operand layout (wave w: positions
+//     16w..16w+15), V bytes likewise (wave w: columns 32w..32w+31, 8
+//     positions a lane), q rows to LDS; the position only masks (rows past
+//     max_pos are clamped), so the workgroup pays one memory latency;
+//  2. S = Q K^T on MFMA (bf16 q, bf16-exact K, fp32 accumulation), the raw
+//     scores to sc;
+//  3. per row the chunk max, p = exp(x - max) and the sum (LDS across waves);
+//  4. O = P V on MFMA with p split into bf16 high + low parts (the low part
+//     carries p - high exactly enough that the product is fp32-accurate);
+//  -> one record (max, sum, 128 column sums) per (token, head, chunk).
+template <int G, int RT>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q,
                                                            const uint8_t* __restrict__ kvk,
                                                            const uint8_t* __restrict__ kvv, float* __restrict__ sc,
                                                            float* __restrict__ part, const int32_t* __restrict__ dpos,
-                                                           int Hq, int Hkv, int max_pos, int nchunk, float invsqrt) {
-    const int m = blockIdx.z, g = blockIdx.y, chunk = blockIdx.x;
-    const int tid = threadIdx.x;
+                                                           int M, int Hq, int Hkv, int max_pos, int nchunk,
+                                                           float invsqrt) {
+    constexpr int R = 16 * RT;
+    constexpr int MT = R / G;
+    static_assert(R % G == 0 && MT >= 1, "rows hold whole tokens");
+    const int chunk = blockIdx.x, g = blockIdx.y, m0 = blockIdx.z * MT;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, lq = lane >> 4;
     const int s0 = chunk * kChunk;
     const int rowmax = max_pos - 1 - s0;       // last in-bounds row of the chunk (s0 < max_pos)
-    __shared__ __align__(16) float qs[G][kD];
-    __shared__ float ps[G][kChunk];
-    __shared__ __align__(16) float vred[8][G][kD];   // V partial sums of the 8 position lanes
-    __shared__ float stat[G][2];
-    // ---- 1. loads: K words of the score thread (position p, quarter qd of
-    // D), V words of the partial-sum thread (4 columns cq, positions
-    // pl*8..pl*8+7), 4 q values per thread
-    const int p = tid >> 2, qd = tid & 3;
-    const uint8_t* kr = kvk + ((int64_t)(s0 + min(p, rowmax)) * Hkv + g) * kD + qd * 32;
-    const uint4 b0 = *reinterpret_cast<const uint4*>(kr);
-    const uint4 b1 = *reinterpret_cast<const uint4*>(kr + 16);
-    const int cq = tid & 31, pl = tid >> 5;
-    uint32_t vw[8];
+    const int64_t rs = (int64_t)Hkv * kD;      // bytes per cache row
+    __shared__ __align__(16) uint16_t qs[R][kD + 8];         // 272-byte rows: conflict-free operand reads
+    __shared__ __align__(16) uint16_t phi[R][kChunk + 8];    // p, bf16 high part
+    __shared__ __align__(16) uint16_t plo[R][kChunk + 8];    // p - high, bf16
+    __shared__ float red[4][R];
+    __shared__ float rstat[2][R];
+    // ---- 1. loads
+    uint2 kraw[4];
     {
-        const uint8_t* vcol = kvv + ((int64_t)s0 * Hkv + g) * kD + cq * 4;
-        const int64_t vstride = (int64_t)Hkv * kD;
+        const uint8_t* kr = kvk + (int64_t)(s0 + min(wave * 16 + l16, rowmax)) * rs + g * kD + lq * 8;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) vw[i] = *reinterpret_cast<const uint32_t*>(vcol + (int64_t)min(pl * 8 + i, rowmax) * vstride);
+        for (int kt = 0; kt < 4; ++kt) kraw[kt] = *reinterpret_cast<const uint2*>(kr + kt * 32);
     }
-    constexpr int kQPer = (G * kD + 1023) / 1024;    // 4-value q loads per thread
-    uint2 qv[kQPer];
+    uint32_t vraw[2][2][8];
+    {
+        const uint8_t* vc = kvv + g * kD + wave * 32 + l16;
 #pragma unroll
-    for (int j = 0; j < kQPer; ++j) {
-        const int i = (j * 256 + tid) * 4;
-        qv[j] = i < G * kD ? *reinterpret_cast<const uint2*>(q + ((int64_t)m * Hq + g * G) * kD + i) : make_uint2(0, 0);
-    }
-    const int pos = *dpos + m;
-    if (pos < 0 || pos >= max_pos) return;
-    const int S = pos + 1;
-    if (s0 >= S) return;                       // uniform over the workgroup; not counted below
-    const int s = s0 + p;
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-    for (int j = 0; j < kQPer; ++j) {
-        const int i = (j * 256 + tid) * 4;
-        if (i < G * kD) {
-            float* d = &qs[0][0] + i;
-            d[0] = bf16_to_f32(qv[j].x & 0xFFFFu);
-            d[1] = bf16_to_f32(qv[j].x >> 16);
-            d[2] = bf16_to_f32(qv[j].y & 0xFFFFu);
-            d[3] = bf16_to_f32(qv[j].y >> 16);
-        }
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int t = 0; t < 8; ++t)
+                    vraw[c][kt][t] = vc[(int64_t)(s0 + min(kt * 32 + lq * 8 + t, rowmax)) * rs + c * 16];
     }
+    for (int i = tid; i < R * 16; i += 256) {
+        const int r = i >> 4, c = i & 15;
+        const int m = m0 + r / G;
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (m < M) v = *reinterpret_cast<const uint4*>(q + ((int64_t)m * Hq + g * G + r % G) * kD + c * 8);
+        *reinterpret_cast<uint4*>(&qs[r][c * 8]) = v;
+    }
+    // tokens m0..m0+MT-1 sit at positions base + m; those inside [0, max_pos) count
+    const int base = *dpos;
+    const int mv_lo = max(m0, -base);
+    const int mv_hi = min(min(M, m0 + MT) - 1, max_pos - 1 - base);
+    if (mv_hi < mv_lo || s0 > base + mv_hi) return;   // uniform: no token of this workgroup reaches the chunk
     __syncthreads();
-    // ---- 2a. scores
-    {
-        float acc[G];
+    // ---- 2. scores, wave = positions 16*wave + l16
+    mx::v4f sacc[RT];
 #pragma unroll
-        for (int h = 0; h < G; ++h) acc[h] = 0.0f;
-        if (s < S) {
-            const uint32_t w[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-            // 4 columns per step: their q values come from LDS as one float4
-            // per head (the 16 threads of a quarter read the same address)
-#pragma unroll 2
-            for (int jj = 0; jj < 8; ++jj) {
-                uint32_t wj = w[0];   // w[jj] by selects: no dynamic register index
+    for (int rt = 0; rt < RT; ++rt) sacc[rt] = mx::v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int t = 1; t < 8; ++t) wj = jj == t ? w[t] : wj;
-                const float k0 = e4m3_ref_decode(wj & 0xFFu), k1 = e4m3_ref_decode((wj >> 8) & 0xFFu);
-                const float k2 = e4m3_ref_decode((wj >> 16) & 0xFFu), k3 = e4m3_ref_decode(wj >> 24);
+    for (int kt = 0; kt < 4; ++kt) {
+        const uint4 kb = kv8_bf16(kraw[kt]);
 #pragma unroll
-                for (int h = 0; h < G; ++h) {
-                    const float4 qf = *reinterpret_cast<const float4*>(&qs[h][qd * 32 + jj * 4]);
-                    acc[h] = fmaf(qf.x, k0, fmaf(qf.y, k1, fmaf(qf.z, k2, fmaf(qf.w, k3, acc[h]))));
-                }
-            }
-        }
-        // sum the four quarters of D (lanes of a quad)
-#pragma unroll
-        for (int h = 0; h < G; ++h) {
-            acc[h] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[h]), 0xB1, 0xF, 0xF, true));
-            acc[h] += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(acc[h]), 0x4E, 0xF, 0xF, true));
-        }
-        if (qd == 0) {
-#pragma unroll
-            for (int h = 0; h < G; ++h) {
-                if (s < S) sc[((int64_t)m * Hq + g * G + h) * max_pos + s] = acc[h];
-                ps[h][p] = s < S ? acc[h] * invsqrt : -INFINITY;
-            }
-        }
+        for (int rt = 0; rt < RT; ++rt)
+            sacc[rt] = mfma_bf16(*reinterpret_cast<const uint4*>(&qs[rt * 16 + l16][kt * 32 + lq * 8]), kb, sacc[rt]);
     }
+    // ---- 3. softmax statistics
+    const int s = s0 + wave * 16 + l16;
+    float x[RT][4];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = rt * 16 + 4 * lq + i;
+            const int m = m0 + r / G;
+            const bool ok = m >= mv_lo && m <= mv_hi && s <= base + m;
+            if (ok) sc[((int64_t)m * Hq + g * G + r % G) * max_pos + s] = sacc[rt][i];
+            x[rt][i] = ok ? sacc[rt][i] * invsqrt : -INFINITY;
+            float mxv = x[rt][i];
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) mxv = fmaxf(mxv, __shfl_xor(mxv, o));
+            if (l16 == 0) red[wave][r] = mxv;
+        }
     __syncthreads();
-    // ---- 2b. per head: chunk max, exp, sum (32 threads per head, 2 positions each)
-    {
-        const int j = tid & 31;
-        for (int h = tid >> 5; h < G; h += 8) {
-            const float x0 = ps[h][j], x1 = ps[h][j + 32];
-            float mx = fmaxf(x0, x1);
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 32));
-            const float e0 = expf(x0 - mx), e1 = expf(x1 - mx);   // exp(-inf) = 0 past S
-            ps[h][j] = e0;
-            ps[h][j + 32] = e1;
-            float l = e0 + e1;
-#pragma unroll
-            for (int off = 16; off > 0; off >>= 1) l += __shfl_xor(l, off, 32);
-            if (j == 0) {
-                stat[h][0] = mx;
-                stat[h][1] = l;
-            }
-        }
-    }
+    if (tid < R) rstat[0][tid] = fmaxf(fmaxf(red[0][tid], red[1][tid]), fmaxf(red[2][tid], red[3][tid]));
     __syncthreads();
-    // ---- 2c. partial V sums: thread = 4 columns (cq) x 8 of the chunk's
-    // positions (pl), all G heads; rows past S carry weight 0 (their bytes
-    // decode to finite values).  The 8 position lanes are summed through LDS.
-    {
-        float4 acc[G];
 #pragma unroll
-        for (int h = 0; h < G; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const float v0 = e4m3_ref_decode(vw[i] & 0xFFu), v1 = e4m3_ref_decode((vw[i] >> 8) & 0xFFu);
-            const float v2 = e4m3_ref_decode((vw[i] >> 16) & 0xFFu), v3 = e4m3_ref_decode(vw[i] >> 24);
+        for (int i = 0; i < 4; ++i) {
+            const int r = rt * 16 + 4 * lq + i;
+            const float mr = rstat[0][r];
+            const float p = mr == -INFINITY ? 0.0f : expf(x[rt][i] - mr);   // exp(-inf) = 0 for masked positions
+            const uint16_t hi = mx::f32_to_bf16_rne(p);
+            phi[r][wave * 16 + l16] = hi;
+            plo[r][wave * 16 + l16] = mx::f32_to_bf16_rne(p - mx::bf16_to_f32(hi));
+            float sum = p;
 #pragma unroll
-            for (int h = 0; h < G; ++h) {
-                const float w = ps[h][pl * 8 + i];
-                acc[h].x = fmaf(w, v0, acc[h].x);
-                acc[h].y = fmaf(w, v1, acc[h].y);
-                acc[h].z = fmaf(w, v2, acc[h].z);
-                acc[h].w = fmaf(w, v3, acc[h].w);
-            }
+            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+            if (l16 == 0) red[wave][r] = sum;
+        }
+    __syncthreads();
+    if (tid < R) rstat[1][tid] = (red[0][tid] + red[1][tid]) + (red[2][tid] + red[3][tid]);
+    // ---- 4. O = P V, wave = columns 32*wave + 16c + l16
+    mx::v4f oacc[RT][2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) oacc[rt][0] = oacc[rt][1] = mx::v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+        uint4 vb[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const uint32_t* v = vraw[c][kt];
+            vb[c] = make_uint4(pack_bf16(kv_bf16(v[0]), kv_bf16(v[1])), pack_bf16(kv_bf16(v[2]), kv_bf16(v[3])),
+                               pack_bf16(kv_bf16(v[4]), kv_bf16(v[5])), pack_bf16(kv_bf16(v[6]), kv_bf16(v[7])));
         }
 #pragma unroll
-        for (int h = 0; h < G; ++h) *reinterpret_cast<float4*>(&vred[pl][h][cq * 4]) = acc[h];
-        __syncthreads();
-        for (int i = tid; i < G * kD; i += 256) {
-            const int h = i / kD, col = i % kD;
-            float sum = 0.0f;
+        for (int rt = 0; rt < RT; ++rt) {
+            const uint4 ah = *reinterpret_cast<const uint4*>(&phi[rt * 16 + l16][kt * 32 + lq * 8]);
+            const uint4 al = *reinterpret_cast<const uint4*>(&plo[rt * 16 + l16][kt * 32 + lq * 8]);
 #pragma unroll
-            for (int l = 0; l < 8; ++l) sum += vred[l][h][col];
-            float* rec = part + (((int64_t)m * Hq + g * G + h) * nchunk + chunk) * kPart;
-            rec[4 + col] = sum;
-            if (col == 0) {
-                rec[0] = stat[h][0];
-                rec[1] = stat[h][1];
+            for (int c = 0; c < 2; ++c) {
+                oacc[rt][c] = mfma_bf16(ah, vb[c], oacc[rt][c]);
+                oacc[rt][c] = mfma_bf16(al, vb[c], oacc[rt][c]);
             }
         }
     }
+    __syncthreads();                           // rstat[1]
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = rt * 16 + 4 * lq + i;
+            const int m = m0 + r / G;
+            if (m < mv_lo || m > mv_hi || s0 > base + m) continue;   // no record: the merge reads chunks up to the token's position
+            float* rec = part + (((int64_t)m * Hq + g * G + r % G) * nchunk + chunk) * kPart;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) rec[4 + wave * 32 + c * 16 + l16] = oacc[rt][c][i];
+            if (wave == 0 && l16 == 0) {
+                rec[0] = rstat[0][r];
+                rec[1] = rstat[1][r];
+            }
+        }
 }
 
 // Workgroup (query head h, token m), 256 threads: merges the chunk records,
@@ -324,7 +344,7 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     MXH_REQUIRE(max_pos > 0 && max_pos <= kChunk * kMaxChunks, "attn_decode: max_pos=%d (1..%d)", max_pos,
                 kChunk * kMaxChunks);
     MXH_REQUIRE(((uintptr_t)kvk & 15) == 0 && ((uintptr_t)kvv & 3) == 0, "attn_decode: kv cache rows must be aligned");
-    MXH_REQUIRE(((uintptr_t)q & 7) == 0, "attn_decode: q must be 8-byte aligned");
+    MXH_REQUIRE(((uintptr_t)q & 15) == 0, "attn_decode: q must be 16-byte aligned");
     MXH_REQUIRE(!o || ((uintptr_t)o & 7) == 0, "attn_decode: o must be 8-byte aligned");
     MXH_REQUIRE(!oq || ((uintptr_t)oq & 3) == 0, "attn_decode: oq must be 4-byte aligned");
     MXH_REQUIRE(workspace_bytes >= mxfp4_attn_decode_workspace_size(M, Hq, max_pos) && ((uintptr_t)workspace & 15) == 0,
@@ -333,20 +353,32 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     const int nchunk = (max_pos + kChunk - 1) / kChunk;
     const float invsqrt = 1.0f / sqrtf((float)D);
     hipStream_t st = mxh::as_stream(stream);
-    const dim3 gp(nchunk, Hkv, M);
+    // row tiles of 16 query rows per workgroup: all M*G rows up to 64
+    const int rows = M * G;
+    const int RT = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
+    const int MT = (16 * RT) / G > 0 ? (16 * RT) / G : 1;
+    MXH_REQUIRE(16 * RT >= G, "attn_decode: G=%d exceeds the 64 query rows of a workgroup", G);
+    const dim3 gp(nchunk, Hkv, (M + MT - 1) / MT);
     const uint16_t* qh = static_cast<const uint16_t*>(q);
     float* part = static_cast<float*>(workspace);
-#define MXH_ATTN(GG)                                                                                         \
-    hipLaunchKernelGGL(attn_partial_kernel<GG>, gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, Hq, Hkv, \
+#define MXH_ATTN(GG, RR)                                                                                           \
+    hipLaunchKernelGGL((attn_partial_kernel<GG, RR>), gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, M, Hq, Hkv, \
                        max_pos, nchunk, invsqrt)
+#define MXH_ATTN_G(GG)                  \
+    switch (RT) {                       \
+        case 1: MXH_ATTN(GG, 1); break; \
+        case 2: MXH_ATTN(GG, 2); break; \
+        default: MXH_ATTN(GG, 4); break; \
+    }
     switch (G) {
-        case 1: MXH_ATTN(1); break;
-        case 2: MXH_ATTN(2); break;
-        case 4: MXH_ATTN(4); break;
-        case 8: MXH_ATTN(8); break;
-        case 16: MXH_ATTN(16); break;
+        case 1: MXH_ATTN_G(1); break;
+        case 2: MXH_ATTN_G(2); break;
+        case 4: MXH_ATTN_G(4); break;
+        case 8: MXH_ATTN_G(8); break;
+        case 16: MXH_ATTN_G(16); break;
         default: MXH_REQUIRE(false, "attn_decode: Hq/Hkv=%d must be 1, 2, 4, 8 or 16", G);
     }
+#undef MXH_ATTN_G
 #undef MXH_ATTN
     const int rc = mxh::launch_status("attn_decode (partials)");
     if (rc != MXFP4_OK) return rc;
