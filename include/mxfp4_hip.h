@@ -367,6 +367,32 @@ int mxfp4_route_tables(const int32_t* ids, int M, int k, const uint8_t* gate_wp,
                        int64_t* gu_ws_tab, int64_t* dn_wp_tab, int64_t* dn_ws_tab, void* stream);
 
 /* ---------------------------------------------------------------------
+ * The MoE block of a batched decode step (M <= 16 tokens), two launches.
+ * Replaces the moe_gateup -> moe_down -> moe_combine chain of
+ * ModelRunnerV2.forward_batch (runtime/model_runner_v2.py:265-289; kernels
+ * src/ext/mxfp4_decode.cu:177-299) over weights stacked per layer as for
+ * mxfp4_moe_decode_layer, with the same arithmetic: MXFP4 activation rows,
+ * g and u in fp32, h = silu(g)*u quantized to MXFP4 per 32-block, down on
+ * MXFP4 h, the weighted sum of a token's E slots in fp32.  Each routed
+ * expert's weights are read once per call however many tokens share it.
+ *   xq, xs   MXFP4 rows of the normed activations, (M, H/2) and (M, H/32)
+ *            (mxfp4_prequant / mxfp4_rmsnorm_quant output), 16-byte aligned
+ *   ids, w   int32 / fp32 (M, E) expert ids and routing weights
+ *            (mxfp4_route_topk output); ids outside [0, n_experts)
+ *            contribute nothing
+ *   y        fp32 (M, H) MoE output
+ *   ws       mxfp4_moe_decode_batch_workspace_size(M, E, Mi) bytes, 16-byte
+ *            aligned (the per-slot MXFP4 h; nothing persists)
+ * Limits: 1 <= M <= 16, 1 <= E <= 8, H a multiple of 128, Mi of 32.  The
+ * sums match the drop-in chain up to fp32 summation order.
+ */
+size_t mxfp4_moe_decode_batch_workspace_size(int M, int E, int Mi);
+int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, const float* w,
+                           const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                           const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws, int n_experts,
+                           int M, int E, int H, int Mi, float* y, void* ws, size_t ws_bytes, void* stream);
+
+/* ---------------------------------------------------------------------
  * Grouped MoE over a batch of tokens (prefill, speculative verify).
  * Replaces ModelRunnerV2.moe_compute (runtime/model_runner_v2.py:108-122):
  * per expert e the rows of torch.where(topi == e) go through `forward` with

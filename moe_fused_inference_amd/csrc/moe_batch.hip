@@ -1,0 +1,298 @@
+// moe_batch.hip -- the MoE block of a batched decode step (M <= 16 tokens,
+// top-E routing) in two launches, for the forward_batch caller
+// (runtime/model_runner_v2.py:265-289: prequant of the normed rows, the
+// token-major tables, moe_gateup, moe_down, moe_combine).
+//
+//   batch_gateup_kernel  workgroup (32-row block rb of Mi, slot s): the slot
+//                        that first names an expert owns it and serves every
+//                        token routed to it (at most one slot per token), so
+//                        each routed expert's gate/up rows stream from HBM
+//                        once per step; 4 waves = gate/up x two 16-row tiles
+//                        on v_mfma_scale_f32_16x16x128_f8f6f4 (A = the
+//                        tokens' MXFP4 rows, B = the weight rows).  Epilogue:
+//                        h = silu(g) * u in fp32 and its MXFP4 32-block (the
+//                        32 rows are one block of down's K), written per slot
+//                        -- moe_down's own activation quantization
+//                        (src/ext/mxfp4_decode.cu:218-279), bit-exact to it
+//                        given g and u.
+//   batch_down_kernel    workgroup (16 output columns): 8 waves share out the
+//                        distinct experts (slot order); per expert, its down
+//                        rows for the columns times the h rows of its tokens,
+//                        weighted by the routing weights (moe_combine,
+//                        src/ext/mxfp4_decode.cu:285-299) into per-wave
+//                        token sums in LDS; the 8 wave sums are added in a
+//                        fixed order.  No gu / yd round trip through HBM and
+//                        no separate combine launch.
+//
+// The results match the drop-in chain up to fp32 summation order (the
+// combine adds a token's experts grouped by wave instead of in slot order).
+#include "mx_device.h"
+#include "mx_host.h"
+
+namespace {
+
+constexpr int kMaxTok = 16;     // tokens per step: one MFMA row tile
+constexpr int kMaxE = 8;        // slots per token (moe_combine's cap)
+constexpr int kMaxSlots = kMaxTok * kMaxE;
+constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment
+constexpr int kDownWaves = 8;
+
+struct BatchArgs {
+    const uint8_t* xq;   // (M, H/2) MXFP4 activation rows
+    const uint8_t* xs;   // (M, H/32)
+    const int32_t* ids;  // (M, E) expert ids, token-major slots
+    const float* w;      // (M, E) routing weights
+    const uint8_t* gwp;  // stacked experts: gate/up (n, Mi, H/2) + (n, Mi, H/32)
+    const uint8_t* gws;
+    const uint8_t* uwp;
+    const uint8_t* uws;
+    const uint8_t* dwp;  // down (n, H, Mi/2) + (n, H, Mi/32)
+    const uint8_t* dws;
+    int n_experts, M, E, H, Mi;
+    uint8_t* hq;         // (S, Mi/2) MXFP4 h per slot
+    uint8_t* hs;         // (S, Mi/32)
+    float* y;            // (M, H) fp32 MoE output
+};
+
+// One prefetch segment: weight (B) and activation (A) 16-byte blocks and
+// their scale bytes for kSegB MFMA K-steps.
+struct Seg {
+    uint4 b[kSegB];
+    uint32_t bs[kSegB];
+    uint4 a[kSegB];
+    uint32_t as[kSegB];
+};
+
+// Lane (row l%16, group q = l/16) takes 32-block 4*st + q at K-step st (64
+// contiguous bytes per row and load instruction); rows past the A rows
+// (tokens) or blocks past the row read zeros with scale code 127.
+__device__ __forceinline__ void load_seg(Seg& sg, const uint8_t* wrow, const uint8_t* srow, const uint8_t* arow,
+                                         const uint8_t* asrow, bool aok, int q, int st0, int steps, int nch) {
+#pragma unroll
+    for (int j = 0; j < kSegB; ++j) {
+        const int c = 4 * (st0 + j) + q;
+        const bool ok = (st0 + j < steps) && (c < nch);
+        sg.b[j] = ok ? *reinterpret_cast<const uint4*>(wrow + c * 16) : make_uint4(0, 0, 0, 0);
+        sg.bs[j] = ok ? (uint32_t)srow[c] : 127u;
+        sg.a[j] = (ok && aok) ? *reinterpret_cast<const uint4*>(arow + c * 16) : make_uint4(0, 0, 0, 0);
+        sg.as[j] = (ok && aok) ? (uint32_t)asrow[c] : 127u;
+    }
+}
+
+__device__ __forceinline__ mx::v4f mma_seg(const Seg& sg, int st0, int steps, mx::v4f acc) {
+#pragma unroll
+    for (int j = 0; j < kSegB; ++j)
+        if (st0 + j < steps) acc = mx::mfma16_fp4(sg.a[j], sg.b[j], acc, sg.as[j], sg.bs[j]);
+    return acc;
+}
+
+// The whole K loop of one 16 x 16 tile, two segments in flight.
+__device__ __forceinline__ mx::v4f kloop(const uint8_t* wrow, const uint8_t* srow, const uint8_t* arow,
+                                         const uint8_t* asrow, bool aok, int q, int steps, int nch) {
+    mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+    Seg s0, s1;
+    load_seg(s0, wrow, srow, arow, asrow, aok, q, 0, steps, nch);
+    for (int st = 0; st < steps; st += 2 * kSegB) {
+        if (st + kSegB < steps) load_seg(s1, wrow, srow, arow, asrow, aok, q, st + kSegB, steps, nch);
+        acc = mma_seg(s0, st, steps, acc);
+        if (st + kSegB >= steps) break;
+        if (st + 2 * kSegB < steps) load_seg(s0, wrow, srow, arow, asrow, aok, q, st + 2 * kSegB, steps, nch);
+        acc = mma_seg(s1, st + kSegB, steps, acc);
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
+    __shared__ int s_slot[kMaxTok];
+    __shared__ int s_cnt, s_own;
+    __shared__ float gu[2][kMaxTok][33];
+    const int rb = blockIdx.x, s = blockIdx.y;
+    const int S = a.M * a.E;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int e = a.ids[s];
+    // ---- the first slot naming expert e owns it and gathers its tokens
+    if (wave == 0) {
+        bool dup = false;
+        for (int j = lane; j < s; j += 64) dup |= a.ids[j] == e;
+        const bool any = __ballot(dup) != 0ull;
+        int cnt = 0;
+        if (!any) {
+            for (int j0 = s; j0 < S; j0 += 64) {
+                const int j = j0 + lane;
+                const bool mm = j < S && a.ids[j] == e;
+                const unsigned long long b = __ballot(mm);
+                if (mm && cnt + __popcll(b & ((1ull << lane) - 1ull)) < kMaxTok)
+                    s_slot[cnt + __popcll(b & ((1ull << lane) - 1ull))] = j;
+                cnt += __popcll(b);
+            }
+        }
+        if (lane == 0) {
+            s_own = any ? 0 : 1;
+            s_cnt = cnt < kMaxTok ? cnt : kMaxTok;
+        }
+    }
+    __syncthreads();
+    if (!s_own) return;
+    const int cnt = s_cnt;
+    const bool valid_e = e >= 0 && e < a.n_experts;   // other ids contribute h = 0
+    const int l16 = lane & 15, q = lane >> 4;
+    const int H = a.H, Mi = a.Mi;
+    const int proj = wave >> 1;
+    const int row = rb * 32 + (wave & 1) * 16 + l16;
+    const int64_t ee = valid_e ? e : 0;
+    const uint8_t* wrow = (proj ? a.uwp : a.gwp) + (ee * Mi + row) * (int64_t)(H / 2);
+    const uint8_t* srow = (proj ? a.uws : a.gws) + (ee * Mi + row) * (int64_t)(H / 32);
+    const bool aok = valid_e && l16 < cnt;
+    const int tok = aok ? s_slot[l16] / a.E : 0;
+    const uint8_t* arow = a.xq + (int64_t)tok * (H / 2);
+    const uint8_t* asrow = a.xs + (int64_t)tok * (H / 32);
+    const int nch = H / 32;
+    mx::v4f acc = kloop(wrow, srow, arow, asrow, aok, q, (nch + 3) / 4, nch);
+    mx::pin(acc);
+    // D[4q + i][l16]: token 4q + i of the group, weight row l16 of the tile
+#pragma unroll
+    for (int i = 0; i < 4; ++i) gu[proj][4 * q + i][(wave & 1) * 16 + l16] = acc[i];
+    __syncthreads();
+    // ---- h = silu(g) * u and its MXFP4 block: thread = (token tt, rows 2j, 2j+1)
+    const int tt = tid >> 4, j = tid & 15;
+    float h0 = 0.0f, h1 = 0.0f;
+    if (tt < cnt) {
+        h0 = mx::silu_mul(gu[0][tt][2 * j], gu[1][tt][2 * j]);
+        h1 = mx::silu_mul(gu[0][tt][2 * j + 1], gu[1][tt][2 * j + 1]);
+    }
+    float am = fmaxf(__builtin_fabsf(h0), __builtin_fabsf(h1));
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) am = fmaxf(am, __shfl_xor(am, o));
+    const uint32_t code = mx::e8m0_code(am);
+    const float inv = mx::e8m0_inv_scale(code);
+    uint32_t byte = mx::e2m1_code(h0 * inv) | (mx::e2m1_code(h1 * inv) << 4);
+    byte |= (uint32_t)__shfl_down((int)byte, 1) << 8;
+    byte |= (uint32_t)__shfl_down((int)byte, 2) << 16;
+    if (tt < cnt) {
+        const int64_t slot = s_slot[tt];
+        if ((j & 3) == 0) *reinterpret_cast<uint32_t*>(a.hq + slot * (Mi / 2) + rb * 16 + j) = byte;
+        if (j == 0) a.hs[slot * (Mi / 32) + rb] = (uint8_t)code;
+    }
+}
+
+__global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a) {
+    __shared__ int s_ids[kMaxSlots];
+    __shared__ int s_owner[kMaxSlots];
+    __shared__ int s_flag[kMaxSlots];
+    __shared__ int s_nown;
+    __shared__ int s_mem[kDownWaves][kMaxTok];
+    __shared__ float ypart[kDownWaves][kMaxTok][17];
+    const int cb = blockIdx.x;
+    const int S = a.M * a.E;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, q = lane >> 4;
+    if (tid < S) s_ids[tid] = a.ids[tid];
+    for (int i = tid; i < kDownWaves * kMaxTok * 17; i += 64 * kDownWaves) (&ypart[0][0][0])[i] = 0.0f;
+    __syncthreads();
+    // owners: slots whose expert no earlier slot names (slot order)
+    if (tid < S) {
+        const int e = s_ids[tid];
+        bool own = e >= 0 && e < a.n_experts;
+        for (int k = 0; k < tid && own; ++k) own = s_ids[k] != e;
+        s_flag[tid] = own ? 1 : 0;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int n = 0;
+        for (int j0 = 0; j0 < S; j0 += 64) {
+            const int j = j0 + lane;
+            const bool f = j < S && s_flag[j];
+            const unsigned long long b = __ballot(f);
+            if (f) s_owner[n + __popcll(b & ((1ull << lane) - 1ull))] = j;
+            n += __popcll(b);
+        }
+        if (lane == 0) s_nown = n;
+    }
+    __syncthreads();
+    const int nown = s_nown;
+    const int H = a.H, Mi = a.Mi;
+    const int nch = Mi / 32, steps = (nch + 3) / 4;
+    const int col = cb * 16 + l16;   // this lane's weight row of down = output column
+    // wave w: owners w, w + 8, ...
+    for (int k = wave; k < nown; k += kDownWaves) {
+        const int slot0 = s_owner[k];
+        const int e = s_ids[slot0];
+        // the owner's slots (one per token), in slot order
+        int cnt = 0;
+        for (int j0 = slot0; j0 < S; j0 += 64) {
+            const int j = j0 + lane;
+            const bool mm = j < S && s_ids[j] == e;
+            const unsigned long long b = __ballot(mm);
+            const int pos = cnt + __popcll(b & ((1ull << lane) - 1ull));
+            if (mm && pos < kMaxTok) s_mem[wave][pos] = j;
+            cnt += __popcll(b);
+        }
+        cnt = cnt < kMaxTok ? cnt : kMaxTok;
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): the wave's s_mem writes are visible to its lanes
+        __builtin_amdgcn_wave_barrier();
+        const bool aok = l16 < cnt;
+        const int mslot = aok ? s_mem[wave][l16] : 0;
+        const uint8_t* wrow = a.dwp + ((int64_t)e * H + col) * (Mi / 2);
+        const uint8_t* srow = a.dws + ((int64_t)e * H + col) * (Mi / 32);
+        const uint8_t* arow = a.hq + (int64_t)mslot * (Mi / 2);
+        const uint8_t* asrow = a.hs + (int64_t)mslot * (Mi / 32);
+        mx::v4f acc = kloop(wrow, srow, arow, asrow, aok, q, steps, nch);
+        // D[4q + i][l16]: member 4q + i, column l16; weighted into its token's sum
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 4 * q + i;
+            if (r < cnt) {
+                const int sl = s_mem[wave][r];
+                ypart[wave][sl / a.E][l16] = fmaf(a.w[sl], acc[i], ypart[wave][sl / a.E][l16]);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);
+        __builtin_amdgcn_wave_barrier();   // s_mem is rewritten by the next owner
+    }
+    __syncthreads();
+    for (int i = tid; i < a.M * 16; i += 64 * kDownWaves) {
+        const int m = i >> 4, c = i & 15;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDownWaves; ++w) v += ypart[w][m][c];
+        a.y[(int64_t)m * H + cb * 16 + c] = v;
+    }
+}
+
+}  // namespace
+
+extern "C" size_t mxfp4_moe_decode_batch_workspace_size(int M, int E, int Mi) {
+    if (M <= 0 || E <= 0 || Mi <= 0) return 0;
+    const size_t S = (size_t)M * E;
+    return S * (size_t)(Mi / 2) + S * (size_t)(Mi / 32);
+}
+
+extern "C" int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, const float* w,
+                                      const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                                      const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                                      int n_experts, int M, int E, int H, int Mi, float* y, void* ws,
+                                      size_t ws_bytes, void* stream) {
+    MXH_REQUIRE(xq && xs && ids && w && gate_wp && gate_ws && up_wp && up_ws && down_wp && down_ws && y && ws,
+                "moe_decode_batch: null pointer");
+    MXH_REQUIRE(M >= 1 && M <= kMaxTok, "moe_decode_batch: M=%d outside 1..%d", M, kMaxTok);
+    MXH_REQUIRE(E >= 1 && E <= kMaxE, "moe_decode_batch: E=%d outside 1..%d", E, kMaxE);
+    MXH_REQUIRE(n_experts >= 1, "moe_decode_batch: n_experts=%d", n_experts);
+    MXH_REQUIRE(H >= 128 && H % 128 == 0, "moe_decode_batch: H=%d must be a positive multiple of 128", H);
+    MXH_REQUIRE(Mi >= 32 && Mi % 32 == 0, "moe_decode_batch: Mi=%d must be a positive multiple of 32", Mi);
+    MXH_REQUIRE(ws_bytes >= mxfp4_moe_decode_batch_workspace_size(M, E, Mi),
+                "moe_decode_batch: workspace of %zu bytes, %zu needed", ws_bytes,
+                mxfp4_moe_decode_batch_workspace_size(M, E, Mi));
+    MXH_REQUIRE(((uintptr_t)ws & 15) == 0 && ((uintptr_t)xq & 15) == 0 && ((uintptr_t)gate_wp & 15) == 0 &&
+                    ((uintptr_t)up_wp & 15) == 0 && ((uintptr_t)down_wp & 15) == 0,
+                "moe_decode_batch: packed operands and the workspace must be 16-byte aligned");
+    const int S = M * E;
+    uint8_t* w8 = static_cast<uint8_t*>(ws);
+    BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
+                w8, w8 + (size_t)S * (Mi / 2), y};
+    hipStream_t st = mxh::as_stream(stream);
+    hipLaunchKernelGGL(batch_gateup_kernel, dim3(Mi / 32, S), dim3(256), 0, st, a);
+    const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
+    if (rc != MXFP4_OK) return rc;
+    hipLaunchKernelGGL(batch_down_kernel, dim3(H / 16), dim3(64 * kDownWaves), 0, st, a);
+    return mxh::launch_status("moe_decode_batch (down)");
+}

@@ -18,8 +18,9 @@ Every op is a kernel of this library; positions and token ids live in device
 memory, so one step can be captured in a HIP graph and replayed step after
 step (DecodeStep.capture).  MoE: M = 1 uses the fused one-launch layer with
 in-kernel routing on the bf16 activations (mxfp4_moe_decode_layer_routed);
-M > 1 uses route_topk + the drop-in grouped ops on MXFP4 activations, as
-forward_batch does.  The KV cache holds E4M3 bytes with no extra scale, read
+M > 1 uses route_topk + mxfp4_moe_decode_batch on MXFP4 activations, the
+arithmetic of forward_batch's moe_gateup -> moe_down -> moe_combine chain in
+two launches that read each routed expert once.  The KV cache holds E4M3 bytes with no extra scale, read
 by attn_decode's codec; they are written the way the matching reference
 step writes them: M = 1 with the decode extension's kv_write codec (the
 graph runner, runtime/model_runner_v3.py:98-101), M > 1 with torch's
@@ -203,12 +204,8 @@ class DecodeStep:
             E = c.top_k
             buf("rid", (M, E), i32)
             buf("rw", (M, E), f32)
-            buf("gu_wp", (M * 2 * E,), torch.int64)
-            buf("gu_ws", (M * 2 * E,), torch.int64)
-            buf("dn_wp", (M * E,), torch.int64)
-            buf("dn_ws", (M * E,), torch.int64)
-            buf("gu", (M * E, 2 * c.moe_inter), f32)
-            buf("yd", (M * E, H), f32)
+            nb = self.lib.mxfp4_moe_decode_batch_workspace_size(M, E, c.moe_inter)
+            buf("moe_ws", ((nb + 15) // 16 * 16,), u8)
         self.b = _Bufs(t)
 
     # ------------------------------------------------------------------ state
@@ -295,17 +292,11 @@ class DecodeStep:
         E, H, Mi = c.top_k, c.hidden, c.moe_inter
         self._ck(lib.mxfp4_route_topk(b.glog.data_ptr(), c.n_experts, M, c.n_experts, E, 1, b.rid.data_ptr(), None,
                                       b.rw.data_ptr(), s), "route_topk")
-        self._ck(lib.mxfp4_route_tables(b.rid.data_ptr(), M, E, ex.gate_wp.data_ptr(), ex.gate_ws.data_ptr(),
-                                        ex.up_wp.data_ptr(), ex.up_ws.data_ptr(), ex.down_wp.data_ptr(),
-                                        ex.down_ws.data_ptr(), c.n_experts, H, Mi, b.gu_wp.data_ptr(),
-                                        b.gu_ws.data_ptr(), b.dn_wp.data_ptr(), b.dn_ws.data_ptr(), s), "route_tables")
-        kh, km = (H + 31) // 32 * 32, (Mi + 31) // 32 * 32
-        self._ck(lib.mxfp4_moe_gateup_devtab(b.yq.data_ptr(), b.ys.data_ptr(), b.gu_wp.data_ptr(), b.gu_ws.data_ptr(),
-                                             b.gu.data_ptr(), E, M, Mi, H, kh, s), "moe_gateup_tab")
-        self._ck(lib.mxfp4_moe_down_devtab(b.gu.data_ptr(), b.dn_wp.data_ptr(), b.dn_ws.data_ptr(), b.yd.data_ptr(), E,
-                                           M, H, Mi, km, s), "moe_down_tab")
-        self._ck(lib.mxfp4_moe_combine(b.yd.data_ptr(), H, b.rw.data_ptr(), E, b.moe.data_ptr(), M, H, s),
-                 "moe_combine")
+        self._ck(lib.mxfp4_moe_decode_batch(b.yq.data_ptr(), b.ys.data_ptr(), b.rid.data_ptr(), b.rw.data_ptr(),
+                                            ex.gate_wp.data_ptr(), ex.gate_ws.data_ptr(), ex.up_wp.data_ptr(),
+                                            ex.up_ws.data_ptr(), ex.down_wp.data_ptr(), ex.down_ws.data_ptr(),
+                                            c.n_experts, M, E, H, Mi, b.moe.data_ptr(), b.moe_ws.data_ptr(),
+                                            b.moe_ws.numel(), s), "moe_decode_batch")
 
     def run_moe_only(self):
         """The step's 48 MoE blocks alone, on the buffers the last step left

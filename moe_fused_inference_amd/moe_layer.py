@@ -344,6 +344,34 @@ def route_tables(ids, experts):
     return gu_wp, gu_ws, dn_wp, dn_ws
 
 
+def decode_batch(xq, xs, ids, w, experts, out=None, ws=None):
+    """The MoE block of a batched decode step on MXFP4 activation rows
+    (forward_batch's moe_gateup -> moe_down -> moe_combine,
+    runtime/model_runner_v2.py:265-289) in two launches: xq (M, H/2) / xs
+    (M, H/32) uint8, ids int32 (M, E), w fp32 (M, E), experts a
+    StackedExperts.  Returns the fp32 (M, H) output."""
+    lib = _lib.load()
+    experts.check()
+    M, E = ids.shape
+    H, Mi = experts.hidden, experts.inter
+    if xq.shape != (M, H // 2) or xs.shape != (M, H // 32) or w.shape != (M, E):
+        raise RuntimeError("xq (M, H/2), xs (M, H/32), ids and w (M, E) shapes do not match")
+    if ids.dtype != torch.int32 or w.dtype != torch.float32:
+        raise RuntimeError("ids must be int32 and w float32")
+    if out is None:
+        out = torch.empty((M, H), dtype=torch.float32, device=xq.device)
+    if ws is None:
+        ws = torch.empty(lib.mxfp4_moe_decode_batch_workspace_size(M, E, Mi), dtype=torch.uint8, device=xq.device)
+    _lib.check(lib.mxfp4_moe_decode_batch(xq.data_ptr(), xs.data_ptr(), ids.contiguous().data_ptr(),
+                                          w.contiguous().data_ptr(), experts.gate_wp.data_ptr(),
+                                          experts.gate_ws.data_ptr(), experts.up_wp.data_ptr(),
+                                          experts.up_ws.data_ptr(), experts.down_wp.data_ptr(),
+                                          experts.down_ws.data_ptr(), experts.n_experts, M, E, H, Mi,
+                                          out.data_ptr(), ws.data_ptr(), ws.numel(),
+                                          torch.cuda.current_stream(xq.device).cuda_stream), "moe_decode_batch")
+    return out
+
+
 def prefill_workspace(T, topk, n_experts, H, Mi, device="cuda"):
     """Scratch memory for one moe_compute call of this shape (reusable by
     stream-ordered calls; nothing persists between calls)."""
