@@ -293,6 +293,20 @@ int mxfp4_embed_rows(const uint8_t* wp, const uint8_t* ws, int V, int K, const i
 int mxfp4_rmsnorm_quant(const void* x, const float* resid, const void* w, float eps, int M, int H,
                         void* x_out, void* y, uint8_t* yq, uint8_t* ys, void* stream);
 
+/* mxfp4_rmsnorm_lin_pq: mxfp4_rmsnorm_quant followed by mxfp4_lin_pq on its
+ * MXFP4 rows, in one launch: out (M, N) fp32 = MXFP4(rms_norm(x [+ resid]))
+ * . W^T for W packed (N, H/2) + (N, H/32) -- the decode step's input norm +
+ * q|k|v projection and post-attention norm + router
+ * (runtime/model_runner_v2.py:147-152, :185-187; RMSNorm
+ * runtime/model_runner.py:20-25).  No counterpart in the reference, which
+ * launches the two separately.  x_out, y, yq/ys are the rmsnorm_quant outputs
+ * and may each be NULL (x_out needs resid).  All outputs are bit-identical to
+ * the two separate calls.  H = 2048, 1 <= M <= 16; x, resid, norm_w, x_out,
+ * y, wp 16-byte aligned. */
+int mxfp4_rmsnorm_lin_pq(const void* x, const float* resid, const void* norm_w, float eps, int M, int H,
+                         void* x_out, void* y, uint8_t* yq, uint8_t* ys, const uint8_t* wp, const uint8_t* wsc,
+                         int N, float* out, void* stream);
+
 /* mxfp4_qk_norm_rope_kv: qkv fp32 (M, (Hq + 2 Hkv) * D) holds each token's q,
  * k and v projections side by side.  For token m at position *dpos + m:
  * q and k heads get RMSNorm with q_norm_w / k_norm_w (bf16 (D)) and the

@@ -43,6 +43,8 @@ SIGNATURES = {
                                       _c_i, _c_p, _c_sz, _c_p]),
     "mxfp4_embed_rows": (_c_i, [_c_p, _c_p, _c_i, _c_i, _c_p, _c_i, _c_p, _c_p]),
     "mxfp4_rmsnorm_quant": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "mxfp4_rmsnorm_lin_pq": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                    _c_p, _c_i, _c_p, _c_p]),
     "mxfp4_qk_norm_rope_kv": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_i, _c_i, _c_i, _c_i,
                                      _c_p, _c_p, _c_p, _c_i, _c_i, _c_p]),
     "mxfp4_argmax_workspace_size": (_c_sz, [_c_i, _c_i]),

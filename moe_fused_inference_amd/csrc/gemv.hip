@@ -331,6 +331,186 @@ __global__ __launch_bounds__(64 * R * S) void lin_small_kernel(const uint8_t* __
     }
 }
 
+// ---------------------------------------------------------------- RMSNorm -> lin_pq
+// The decode step's "x = x + bf16(o); h = rms_norm(x) -> MXFP4; y = lin_pq(h)"
+// (runtime/model_runner_v2.py:185-187 and :208 + :147-152; RMSNorm
+// runtime/model_runner.py:20-25) in one launch for H = 2048 and M <= 16 rows.
+// Every workgroup normalises the rows itself (threads 0..255, 8 elements a
+// thread, the arithmetic of mxfp4_rmsnorm_quant) into LDS and runs the
+// split-K GEMV of lin_small_kernel with its A operand read from there;
+// workgroup 0 also writes the residual, y and the MXFP4 rows to global
+// memory for the step's later kernels.  The weight loads of a wave's first
+// segment are issued before the norm, so they fly during it.
+constexpr int kNormH = 2048;
+
+struct NormLinArgs {
+    const uint16_t* x;     // (M, H) bf16 residual stream
+    const float* resid;    // (M, H) fp32 added as bf16 first (RESID)
+    const uint16_t* nw;    // (H) bf16 norm weight
+    float eps;
+    uint16_t* x_out;       // workgroup 0: bf16(x + bf16(resid)) (RESID), may be null
+    uint16_t* y;           // workgroup 0: the normed bf16 rows, may be null
+    uint8_t* yq;           // workgroup 0: their MXFP4 rows (M, H/2) + (M, H/32), may be null
+    uint8_t* ys;
+    const uint8_t* wp;     // (N, H/2) + (N, H/32) weight
+    const uint8_t* ws;
+    float* out;            // (M, N) fp32
+    int M, N, spw;
+};
+
+__device__ __forceinline__ void lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // LDS only: the weight loads stay in flight
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int R, int S, bool RESID>
+__global__ __launch_bounds__(64 * R * S) void norm_lin_kernel(NormLinArgs a) {
+    constexpr int H = kNormH, nch = H / 32, steps = nch / 4;
+    __shared__ __align__(16) uint8_t lq[16][H / 2];
+    __shared__ uint8_t lsc[16][nch];
+    __shared__ float red[4][4];
+    __shared__ mx::v4f redv[S > 1 ? S : 1][R][64];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int rt = wave % R, part = wave / R;
+    const int r = lane & 15;
+    const int g = lane >> 4;
+    const int n0 = (blockIdx.x * R + rt) * 16;
+    const int M = a.M;
+    const int sb = part * a.spw;
+    const int se = min(steps, sb + a.spw);
+    const bool act = n0 < a.N && sb < se;
+    const int nrow = min(n0 + r, a.N - 1);
+    const int arow = min(r, M - 1);
+    const int boff = 4 * sb;
+    const SegCtx cx{a.wp + (int64_t)nrow * (H / 2) + boff * 16, a.ws + (int64_t)nrow * nch + boff, nullptr, nullptr,
+                    &lq[arow][boff * 16], &lsc[arow][boff], g, se - sb, nch - boff, true};
+    SegBuf s0buf, s1buf;
+    if (act) load_seg<A_SILU>(s0buf, cx, 0);
+    // ---- the rows' norm, four rows a round
+    const bool w0 = blockIdx.x == 0;
+    for (int m0 = 0; m0 < M; m0 += 4) {
+        float v[4][8];
+        float ss[4] = {0.f, 0.f, 0.f, 0.f};
+        if (tid < 256) {
+            const int k0 = 8 * tid;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = m0 + j;
+                if (m >= M) continue;
+                const int64_t rb = (int64_t)m * H;
+                const uint4 q = *reinterpret_cast<const uint4*>(a.x + rb + k0);
+                const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    v[j][2 * i] = mx::bf16_to_f32((uint16_t)(wq[i] & 0xFFFFu));
+                    v[j][2 * i + 1] = mx::bf16_to_f32((uint16_t)(wq[i] >> 16));
+                }
+                if (RESID) {
+                    const float4 o0 = *reinterpret_cast<const float4*>(a.resid + rb + k0);
+                    const float4 o1 = *reinterpret_cast<const float4*>(a.resid + rb + k0 + 4);
+                    const float of[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+#pragma unroll
+                    for (int i = 0; i < 8; ++i)
+                        v[j][i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(v[j][i] + mx::bf16_to_f32(mx::f32_to_bf16_rne(of[i]))));
+                    if (w0 && a.x_out) {
+                        uint32_t xo[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            xo[i] = (uint32_t)mx::f32_to_bf16_rne(v[j][2 * i]) |
+                                    ((uint32_t)mx::f32_to_bf16_rne(v[j][2 * i + 1]) << 16);
+                        *reinterpret_cast<uint4*>(a.x_out + rb + k0) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
+                    }
+                }
+#pragma unroll
+                for (int i = 0; i < 8; ++i) ss[j] = fmaf(v[j][i], v[j][i], ss[j]);
+            }
+            // the sum over the 256 threads in mxfp4_rmsnorm_quant's order
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) ss[j] += __shfl_xor(ss[j], o);
+                if (lane == 0) red[j][wave] = ss[j];
+            }
+        }
+        lds_sync();
+        if (tid < 256) {
+            const int k0 = 8 * tid;
+            const uint4 wq4 = *reinterpret_cast<const uint4*>(a.nw + k0);
+            const uint32_t wq[4] = {wq4.x, wq4.y, wq4.z, wq4.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int m = m0 + j;
+                if (m >= M) continue;
+                const float var = ((red[j][0] + red[j][1]) + (red[j][2] + red[j][3])) / (float)H;
+                const float rr = 1.0f / sqrtf(var + a.eps);
+                float yv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float wi = mx::bf16_to_f32((uint16_t)(wq[i / 2] >> (16 * (i & 1))));
+                    const float t = mx::bf16_to_f32(mx::f32_to_bf16_rne(v[j][i] * rr));
+                    yv[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(t * wi));
+                }
+                float am = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) am = fmaxf(am, fabsf(yv[i]));
+                am = fmaxf(am, __shfl_xor(am, 1));
+                am = fmaxf(am, __shfl_xor(am, 2));
+                const uint32_t code = mx::e8m0_code(am);
+                const uint32_t nib = mx::e2m1_pack8(yv, mx::e8m0_inv_scale(code));
+                *reinterpret_cast<uint32_t*>(&lq[m][k0 / 2]) = nib;
+                if ((tid & 3) == 0) lsc[m][k0 / 32] = (uint8_t)code;
+                if (w0) {
+                    const int64_t rb = (int64_t)m * H;
+                    if (a.y) {
+                        uint32_t yo[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            yo[i] = (uint32_t)mx::f32_to_bf16_rne(yv[2 * i]) | ((uint32_t)mx::f32_to_bf16_rne(yv[2 * i + 1]) << 16);
+                        *reinterpret_cast<uint4*>(a.y + rb + k0) = make_uint4(yo[0], yo[1], yo[2], yo[3]);
+                    }
+                    if (a.yq) {
+                        *reinterpret_cast<uint32_t*>(a.yq + (int64_t)m * (H / 2) + k0 / 2) = nib;
+                        if ((tid & 3) == 0) a.ys[(int64_t)m * nch + k0 / 32] = (uint8_t)code;
+                    }
+                }
+            }
+        }
+        lds_sync();   // red[] is reused by the next round; the LDS rows are complete
+    }
+    // ---- the GEMV (lin_small_kernel's), A from LDS
+    mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+    if (act) {
+        for (int s0 = 0; s0 < cx.steps; s0 += 2 * kSeg) {
+            if (s0 + kSeg < cx.steps) load_seg<A_SILU>(s1buf, cx, s0 + kSeg);
+            acc = compute_seg<A_SILU>(s0buf, cx, s0, acc);
+            if (s0 + kSeg >= cx.steps) break;
+            if (s0 + 2 * kSeg < cx.steps) load_seg<A_SILU>(s0buf, cx, s0 + 2 * kSeg);
+            acc = compute_seg<A_SILU>(s1buf, cx, s0 + kSeg, acc);
+        }
+    }
+    if constexpr (S > 1) {
+        redv[part][rt][lane] = acc;
+        __syncthreads();
+        if (part != 0) return;
+#pragma unroll
+        for (int p = 1; p < S; ++p) {
+            const mx::v4f o = redv[p][rt][lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += o[i];
+        }
+    }
+    const int col = n0 + r;
+    if (col >= a.N) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = 4 * g + i;
+        if (m < M) a.out[(int64_t)m * a.N + col] = acc[i];
+    }
+}
+
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ yd, int ystride,
                                                       const float* __restrict__ w, int E,
                                                       float* __restrict__ out, int M, int N) {
@@ -531,4 +711,44 @@ extern "C" int mxfp4_moe_combine(const float* yd, int ystride, const float* w, i
     dim3 grid((unsigned)((N + 255) / 256), (unsigned)M);
     hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, mxh::as_stream(stream), yd, ystride, w, E, out, M, N);
     return mxh::launch_status("moe_combine");
+}
+
+extern "C" int mxfp4_rmsnorm_lin_pq(const void* x, const float* resid, const void* norm_w, float eps, int M, int H,
+                                    void* x_out, void* y, uint8_t* yq, uint8_t* ys, const uint8_t* wp,
+                                    const uint8_t* wsc, int N, float* out, void* stream) {
+    MXH_REQUIRE(x && norm_w && wp && wsc && out, "rmsnorm_lin_pq: null pointer");
+    MXH_REQUIRE(H == kNormH, "rmsnorm_lin_pq: H=%d (this kernel is built for %d)", H, kNormH);
+    MXH_REQUIRE(M >= 1 && M <= 16 && N > 0, "rmsnorm_lin_pq: M=%d (1..16) N=%d", M, N);
+    MXH_REQUIRE(!yq == !ys, "rmsnorm_lin_pq: yq and ys go together");
+    MXH_REQUIRE(resid || !x_out, "rmsnorm_lin_pq: x_out needs resid");
+    MXH_REQUIRE(((uintptr_t)x & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && (!resid || ((uintptr_t)resid & 15) == 0) &&
+                    (!x_out || ((uintptr_t)x_out & 15) == 0) && (!y || ((uintptr_t)y & 15) == 0) &&
+                    (!yq || ((uintptr_t)yq & 3) == 0) && ((uintptr_t)wp & 15) == 0,
+                "rmsnorm_lin_pq: x, resid, norm_w, x_out, y, wp must be 16-byte aligned, yq 4-byte");
+    const int tiles = (N + 15) / 16;
+    const int steps = kNormH / 128;
+    int S = 1;
+    while (S < 16 && 2 * S <= steps && (int64_t)tiles * S < 1024) S *= 2;
+    NormLinArgs a{static_cast<const uint16_t*>(x), resid, static_cast<const uint16_t*>(norm_w), eps,
+                  static_cast<uint16_t*>(x_out), static_cast<uint16_t*>(y), yq, ys, wp, wsc, out, M, N,
+                  (steps + S - 1) / S};
+    hipStream_t st = mxh::as_stream(stream);
+#define MXH_NORM_LIN(R_, S_)                                                                                       \
+    do {                                                                                                           \
+        if (resid)                                                                                                 \
+            hipLaunchKernelGGL((norm_lin_kernel<R_, S_, true>), dim3((unsigned)((tiles + R_ - 1) / R_)),          \
+                               dim3(64 * R_ * S_), 0, st, a);                                                      \
+        else                                                                                                       \
+            hipLaunchKernelGGL((norm_lin_kernel<R_, S_, false>), dim3((unsigned)((tiles + R_ - 1) / R_)),         \
+                               dim3(64 * R_ * S_), 0, st, a);                                                      \
+    } while (0)
+    switch (S) {
+        case 1: MXH_NORM_LIN(4, 1); break;
+        case 2: MXH_NORM_LIN(1, 2); break;
+        case 4: MXH_NORM_LIN(1, 4); break;
+        case 8: MXH_NORM_LIN(1, 8); break;
+        default: MXH_NORM_LIN(1, 16); break;
+    }
+#undef MXH_NORM_LIN
+    return mxh::launch_status("rmsnorm_lin_pq");
 }

@@ -161,6 +161,7 @@ class DecodeStep:
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
         self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
+        self.fused_norm = cfg.hidden == 2048 and self.M == 1   # at M > 1 the per-workgroup norm costs more than the launch it saves
         c = cfg
         if c.head_dim != 128:
             raise RuntimeError("head_dim must be 128 (attention kernels)")
@@ -232,6 +233,22 @@ class DecodeStep:
         self._ck(self.lib.mxfp4_lin_pq(xq.data_ptr(), xs.data_ptr(), w.wp.data_ptr(), w.ws.data_ptr(), out.data_ptr(),
                                        self.M, N, K, kp, s), "lin_pq")
 
+    def _norm_lin(self, x, resid, nw, x_out, keep, w, out, s):
+        """rms_norm(x [+ resid]) -> MXFP4 -> lin_pq(w) in one launch at M = 1
+        (H = 2048), else rmsnorm_quant + lin_pq.  keep:
+        also leave y and its MXFP4 rows in the step buffers."""
+        lib, c, b, M, H = self.lib, self.cfg, self.b, self.M, self.cfg.hidden
+        ptr = (lambda t: t.data_ptr() if t is not None else None)
+        if self.fused_norm:
+            self._ck(lib.mxfp4_rmsnorm_lin_pq(x.data_ptr(), ptr(resid), nw.data_ptr(), c.rms_eps, M, H, ptr(x_out),
+                                              ptr(b.y) if keep else None, ptr(b.yq) if keep else None,
+                                              ptr(b.ys) if keep else None, w.wp.data_ptr(), w.ws.data_ptr(), w.n,
+                                              out.data_ptr(), s), "rmsnorm_lin_pq")
+        else:
+            self._ck(lib.mxfp4_rmsnorm_quant(x.data_ptr(), ptr(resid), nw.data_ptr(), c.rms_eps, M, H, ptr(x_out),
+                                             b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s), "rmsnorm_quant")
+            self._lin(b.yq, b.ys, w, w.n, H, out, s)
+
     def run(self, on_layer=None):
         """Issue one step on the current stream.  on_layer(l, x, moe): an
         optional eager hook after each layer's MoE (x is the residual stream
@@ -244,17 +261,11 @@ class DecodeStep:
                                       b.x.data_ptr(), s), "embed_rows")
         xa, xb = b.x, b.x2          # residual stream ping-pong
         for l, lw in enumerate(m.layers):
-            # input norm (+ the previous layer's MoE residual)
-            if l == 0:
-                self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), None, lw.in_norm.data_ptr(), c.rms_eps, M, H, None,
-                                                 b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s), "rmsnorm_quant")
-            else:
-                self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.moe.data_ptr(), lw.in_norm.data_ptr(), c.rms_eps, M,
-                                                 H, xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(),
-                                                 s), "rmsnorm_quant")
+            # input norm (+ the previous layer's MoE residual) and the q|k|v projection
+            resid = b.moe if l > 0 else None
+            self._norm_lin(xa, resid, lw.in_norm, xb if l > 0 else None, False, lw.qkv, b.qkv, s)
+            if l > 0:
                 xa, xb = xb, xa
-            # attention
-            self._lin(b.yq, b.ys, lw.qkv, c.qkv_rows, H, b.qkv, s)
             kvk, kvv = b.kvk[l], b.kvv[l]
             self._ck(lib.mxfp4_qk_norm_rope_kv(b.qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), c.rms_eps,
                                                c.rope_theta, b.dpos.data_ptr(), M, Hq, Hkv, D, b.q.data_ptr(),
@@ -265,12 +276,9 @@ class DecodeStep:
                                               b.sc.data_ptr(), None, b.aq.data_ptr(), b.as_.data_ptr(), M, Hq, Hkv, D,
                                               self.max_pos, b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode")
             self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
-            # x = x + bf16(o); post-attention norm; router logits
-            self._ck(lib.mxfp4_rmsnorm_quant(xa.data_ptr(), b.oproj.data_ptr(), lw.post_norm.data_ptr(), c.rms_eps, M,
-                                             H, xb.data_ptr(), b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s),
-                     "rmsnorm_quant")
+            # x = x + bf16(o); post-attention norm (y, MXFP4 rows for the MoE); router logits
+            self._norm_lin(xa, b.oproj, lw.post_norm, xb, True, lw.gate, b.glog, s)
             xa, xb = xb, xa
-            self._lin(b.yq, b.ys, lw.gate, c.n_experts, H, b.glog, s)
             # MoE
             if M == 1:
                 self.moe_calls[l](s)

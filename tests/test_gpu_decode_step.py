@@ -182,6 +182,48 @@ def test_rmsnorm_quant(resid):
     assert np.array_equal(np_(yq), q) and np.array_equal(np_(ys), s)
 
 
+@pytest.mark.parametrize("M,N,resid", [(1, 5120, False), (1, 128, True), (3, 2048, True), (8, 5120, True),
+                                      (16, 20000, True), (5, 136, False)])
+def test_rmsnorm_lin_pq_equals_the_two_calls(M, N, resid):
+    """One launch of RMSNorm -> MXFP4 -> lin_pq gives exactly what
+    mxfp4_rmsnorm_quant followed by mxfp4_lin_pq give: the residual, y, the
+    MXFP4 rows and the projection, bit for bit (the same quantizer and the
+    same split-K GEMV, A read from LDS instead of HBM)."""
+    lib = _lib.load()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(M * 1000 + N)
+    H = 2048
+    x = (torch.randn((M, H), generator=g, device=DEV) * 3).bfloat16()
+    o = torch.randn((M, H), generator=g, device=DEV) if resid else None
+    nw = (1 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+    w = (torch.randn((N, H), generator=g, device=DEV) * 0.02).bfloat16()
+    wp = torch.empty((N, H // 2), dtype=torch.uint8, device=DEV)
+    ws = torch.empty((N, H // 32), dtype=torch.uint8, device=DEV)
+    _lib.check(lib.mxfp4_prequant(w.data_ptr(), H, N, H, H, wp.data_ptr(), ws.data_ptr(), None), "prequant")
+    outs = []
+    for fused in (False, True):
+        xo = torch.zeros_like(x)
+        y = torch.zeros_like(x)
+        yq = torch.zeros((M, H // 2), dtype=torch.uint8, device=DEV)
+        ys = torch.zeros((M, H // 32), dtype=torch.uint8, device=DEV)
+        out = torch.zeros((M, N), dtype=torch.float32, device=DEV)
+        op = o.data_ptr() if resid else None
+        xop = xo.data_ptr() if resid else None
+        if fused:
+            _lib.check(lib.mxfp4_rmsnorm_lin_pq(x.data_ptr(), op, nw.data_ptr(), 1e-6, M, H, xop, y.data_ptr(),
+                                                yq.data_ptr(), ys.data_ptr(), wp.data_ptr(), ws.data_ptr(), N,
+                                                out.data_ptr(), None), "rmsnorm_lin_pq")
+        else:
+            _lib.check(lib.mxfp4_rmsnorm_quant(x.data_ptr(), op, nw.data_ptr(), 1e-6, M, H, xop, y.data_ptr(),
+                                               yq.data_ptr(), ys.data_ptr(), None), "rmsnorm_quant")
+            _lib.check(lib.mxfp4_lin_pq(yq.data_ptr(), ys.data_ptr(), wp.data_ptr(), ws.data_ptr(), out.data_ptr(),
+                                        M, N, H, H, None), "lin_pq")
+        torch.cuda.synchronize()
+        outs.append((xo, y, yq, ys, out))
+    for name, a, b in zip(("x_out", "y", "yq", "ys", "out"), outs[0], outs[1]):
+        assert torch.equal(a, b), f"M={M} N={N} resid={resid}: {name} differs"
+
+
 @pytest.mark.parametrize("codec", [0, 1])
 def test_qk_norm_rope_kv(codec):
     """Head RMSNorm + RoPE + KV write against oracle/step.py and the codecs
