@@ -222,9 +222,11 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 
 // Workgroup (query head h, token m), 256 threads: merges the chunk records,
 // o = sum_c exp(m_c - M) acc_c / sum_c exp(m_c - M) l_c with M = max_c m_c.
-// Pass 1 loads every chunk's (m_c, l_c) at once (a thread per chunk); pass 2
-// has thread (column pair cp, chunk phase cq) sum the chunks c = cq mod 4
-// with all of its loads in flight, and the four phases meet in LDS.  The
+// Up to 64 chunks (context 4096): one pass, thread (column pair, chunk phase
+// cq) loads the statistics and column sums of the chunks c = cq mod 4 at
+// once.  Longer contexts: pass 1 loads every chunk's (m_c, l_c) (a thread per
+// chunk), pass 2 sums the column records with all loads in flight.  The four
+// phases meet in LDS.  The
 // output is fp32 o and/or the MXFP4 rows (oq, os) of bf16(o) (32-blocks of
 // 16 column pairs, the quantizer's rule).
 __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict__ part, float* __restrict__ o,
@@ -238,7 +240,52 @@ __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict
     const float* rec = part + ((int64_t)m * Hq + h) * nchunk * kPart;
     __shared__ float cw[kMaxChunks];           // chunk max, then its weight exp(m_c - M)
     __shared__ float red[4];
+    __shared__ float dred[4];
     __shared__ __align__(8) float2 nred[4][64];
+    const int lane = tid & 63, wave = tid >> 6;
+    float r0, r1;
+    if (n <= 64) {
+        // one pass: thread (column pair lane, phase wave) loads the statistics
+        // and column sums of chunks wave, wave + 4, ... all at once
+        constexpr int kF = 16;
+        float2 st[kF], cs[kF];
+#pragma unroll
+        for (int i = 0; i < kF; ++i) {
+            const int c = wave + 4 * i;
+            st[i] = make_float2(-INFINITY, 0.0f);
+            cs[i] = make_float2(0.0f, 0.0f);
+            if (c < n) {
+                st[i] = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart);
+                cs[i] = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart + 4 + 2 * lane);
+            }
+        }
+        float gm = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kF; ++i) gm = fmaxf(gm, st[i].x);
+        if (lane == 0) red[wave] = gm;
+        __syncthreads();
+        gm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        float den = 0.0f;
+        float2 num = make_float2(0.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < kF; ++i) {
+            if (wave + 4 * i < n) {
+                const float w = expf(st[i].x - gm);
+                den = fmaf(w, st[i].y, den);
+                num.x = fmaf(w, cs[i].x, num.x);
+                num.y = fmaf(w, cs[i].y, num.y);
+            }
+        }
+        nred[wave][lane] = num;
+        if (lane == 0) dred[wave] = den;
+        __syncthreads();
+        if (wave != 0) return;
+        den = (dred[0] + dred[1]) + (dred[2] + dred[3]);
+        num.x = (nred[0][lane].x + nred[1][lane].x) + (nred[2][lane].x + nred[3][lane].x);
+        num.y = (nred[0][lane].y + nred[1][lane].y) + (nred[2][lane].y + nred[3][lane].y);
+        r0 = num.x / den;
+        r1 = num.y / den;
+    } else {
     constexpr int kPer = kMaxChunks / 256;
     float mc[kPer], lc[kPer];
     float gm = -INFINITY;
@@ -254,7 +301,6 @@ __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict
         }
         gm = fmaxf(gm, mc[i]);
     }
-    const int lane = tid & 63, wave = tid >> 6;
     gm = mx::wave_reduce_dpp<true>(gm);
     if (lane == 0) red[wave] = gm;
     __syncthreads();
@@ -289,7 +335,9 @@ __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict
     if (wave != 0) return;
     num.x = (nred[0][lane].x + nred[1][lane].x) + (nred[2][lane].x + nred[3][lane].x);
     num.y = (nred[0][lane].y + nred[1][lane].y) + (nred[2][lane].y + nred[3][lane].y);
-    const float r0 = num.x / den, r1 = num.y / den;
+    r0 = num.x / den;
+    r1 = num.y / den;
+    }
     if (o) *reinterpret_cast<float2*>(o + ((int64_t)m * Hq + h) * kD + 2 * lane) = make_float2(r0, r1);
     if (oq) {
         // MXFP4 of bf16(o): a 32-block is 16 lanes; the quantizer's rule

@@ -60,7 +60,9 @@ def _cache(rng, max_pos, Hkv, D, scale=0.5):
 
 @pytest.mark.parametrize("M,Hq,Hkv,max_pos,base", [(1, 32, 4, 4096, 4095), (1, 32, 4, 4096, 0),
                                                   (9, 32, 4, 4096, 2000), (2, 8, 8, 256, 100),
-                                                  (3, 16, 1, 300, 250), (1, 4, 2, 128, 70)])
+                                                  (3, 16, 1, 300, 250), (1, 4, 2, 128, 70),
+                                                  # more than 64 chunks: the two-pass merge
+                                                  (2, 32, 4, 8192, 6000), (1, 8, 2, 8192, 8191)])
 def test_attn_decode_vs_oracle(dext, M, Hq, Hkv, max_pos, base):
     rng = np.random.default_rng(Hq * 7 + max_pos + base)
     D = 128
