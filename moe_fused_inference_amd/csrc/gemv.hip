@@ -389,8 +389,11 @@ __global__ __launch_bounds__(64 * R * S) void norm_lin_kernel(NormLinArgs a) {
                     &lq[arow][boff * 16], &lsc[arow][boff], g, se - sb, nch - boff, true};
     SegBuf s0buf, s1buf;
     if (act) load_seg<A_SILU>(s0buf, cx, 0);
-    // ---- the rows' norm, four rows a round
+    // ---- the rows' norm, four rows a round (the norm weight is loaded with
+    // the first rows, not after the reduction)
     const bool w0 = blockIdx.x == 0;
+    uint4 wq4 = make_uint4(0, 0, 0, 0);
+    if (tid < 256) wq4 = *reinterpret_cast<const uint4*>(a.nw + 8 * tid);
     for (int m0 = 0; m0 < M; m0 += 4) {
         float v[4][8];
         float ss[4] = {0.f, 0.f, 0.f, 0.f};
@@ -438,7 +441,6 @@ __global__ __launch_bounds__(64 * R * S) void norm_lin_kernel(NormLinArgs a) {
         lds_sync();
         if (tid < 256) {
             const int k0 = 8 * tid;
-            const uint4 wq4 = *reinterpret_cast<const uint4*>(a.nw + k0);
             const uint32_t wq[4] = {wq4.x, wq4.y, wq4.z, wq4.w};
 #pragma unroll
             for (int j = 0; j < 4; ++j) {

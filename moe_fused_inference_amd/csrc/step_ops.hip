@@ -88,11 +88,13 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const uint16_t* __restr
     const int64_t rb = (int64_t)m * H;
     const int nit = H / 2048;
     float v[kMaxIt][8];
+    uint4 wv[kMaxIt];   // the norm weight, loaded with x rather than after the reduction
     float ss = 0.0f;
 #pragma unroll
     for (int it = 0; it < kMaxIt; ++it) {
         if (it < nit) {
             const int k0 = 8 * threadIdx.x + 2048 * it;
+            wv[it] = *reinterpret_cast<const uint4*>(w + k0);
             const uint4 q = *reinterpret_cast<const uint4*>(x + rb + k0);
             const uint32_t wq[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
@@ -126,8 +128,7 @@ __global__ __launch_bounds__(256) void norm_quant_kernel(const uint16_t* __restr
     for (int it = 0; it < kMaxIt; ++it) {
         if (it < nit) {
             const int k0 = 8 * threadIdx.x + 2048 * it;
-            const uint4 wq4 = *reinterpret_cast<const uint4*>(w + k0);
-            const uint32_t wq[4] = {wq4.x, wq4.y, wq4.z, wq4.w};
+            const uint32_t wq[4] = {wv[it].x, wv[it].y, wv[it].z, wv[it].w};
             float yv[8];
 #pragma unroll
             for (int i = 0; i < 8; ++i) {
