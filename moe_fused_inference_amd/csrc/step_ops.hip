@@ -26,6 +26,7 @@
 //                          slices of the row, and the position dpos += M,
 //                          both on the device, so a captured step graph can
 //                          be replayed step after step.
+#include "head_rope.h"
 #include "kv_codec.h"
 #include "mx_device.h"
 #include "mx_host.h"
@@ -176,11 +177,7 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
     if (h >= nh) return;
     const int pos = *dpos + m;
     const float* row = qkv + (int64_t)m * nh * kD;
-    // inv_freq = 1 / theta^(2j/D) and the angle pos * inv_freq in fp32
-    // (runtime/model_runner.py:31-33); lane owns frequency j = lane
-    const float inv_freq = 1.0f / powf(theta, (float)(2 * lane) / (float)kD);
-    const float ang = (float)pos * inv_freq;
-    const float c = cosf(ang), s = sinf(ang);
+    const float2 cs = hr::rope_cs(theta, lane, pos);
     {
         const float a = row[h * kD + lane], b = row[h * kD + lane + 64];
         if (h >= Hq + Hkv) {   // v: bf16, then the KV byte
@@ -192,18 +189,9 @@ __global__ __launch_bounds__(256) void qk_rope_kv_kernel(const float* __restrict
             }
             return;
         }
-        // head RMSNorm on fp32: (x * rsqrt(mean(x^2) + eps)) * w, then bf16
-        float ss = fmaf(a, a, b * b);
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-        const float r = 1.0f / sqrtf(ss / (float)kD + eps);
         const uint16_t* nw = h < Hq ? qw : kw;
-        const float na = mx::bf16_to_f32(mx::f32_to_bf16_rne((a * r) * mx::bf16_to_f32(nw[lane])));
-        const float nb = mx::bf16_to_f32(mx::f32_to_bf16_rne((b * r) * mx::bf16_to_f32(nw[lane + 64])));
-        // RoPE, half layout: out = x * cos + rotate_half(x) * sin, fp32, to bf16
-        const float ra = __fadd_rn(__fmul_rn(na, c), __fmul_rn(-nb, s));
-        const float rb = __fadd_rn(__fmul_rn(nb, c), __fmul_rn(na, s));
-        const uint16_t ba = mx::f32_to_bf16_rne(ra), bb = mx::f32_to_bf16_rne(rb);
+        uint16_t ba, bb;
+        hr::norm_rope(a, b, mx::bf16_to_f32(nw[lane]), mx::bf16_to_f32(nw[lane + 64]), eps, cs, ba, bb);
         if (h < Hq) {
             uint16_t* dst = q_out + ((int64_t)m * Hq + h) * kD;
             dst[lane] = ba;
