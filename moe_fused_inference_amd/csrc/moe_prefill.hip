@@ -38,6 +38,7 @@
 // then one exchange with lane l^32, and the nibbles pack into 8-byte stores.
 #include <type_traits>
 
+#include "lds_dma.h"
 #include "mx_device.h"
 #include "mx_host.h"
 
@@ -147,6 +148,7 @@ struct GArgs {
     uint8_t* hs;             //             (P, Mi/32)
     uint16_t* yd;            // DOWN out: (P, H) bf16 at the pair's own index
     const uint16_t* scores;  // DOWN: (P) bf16 routing weights
+    int a_rows;              // rows of aq / as (T for gate/up, P for down)
 };
 
 struct StageRegs {
@@ -227,6 +229,84 @@ __device__ __forceinline__ int weight_row(int rho, int n0, int& proj) {
     }
     proj = 2;
     return n0 + rho;
+}
+
+// Epilogue of a 128 x 128 tile (acc[i][j] of the 2 x 2 wave layout):
+// gate/up -> h = silu(g)*u, fp16, MXFP4 rows in sorted pair order; down ->
+// bf16(bf16(y) * score) at the pair's own index.
+template <int MODE>
+__device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs& g, int n0, int off, int mt,
+                                              int mrows, int rbase, int wn, int lr, int h) {
+    // acc[i][j] element q of lane l: token wm*64 + 32i + l%32, weight row
+    // wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
+    if (MODE == MODE_GATEUP) {
+        const int fb = n0 + 32 * wn;           // first feature of this wave's 32-block
+        const int Mi = g.Nw;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int rloc = rbase + 32 * i + lr;
+            float v[16];
+            float amax = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                v[q] = mx::round_to_f16(mx::silu_mul(acc[i][0][q], acc[i][1][q]));
+                amax = fmaxf(amax, fabsf(v[q]));
+            }
+            amax = fmaxf(amax, __shfl_xor(amax, 32));
+            const uint32_t code = mx::e8m0_code(amax);
+            const float inv = mx::e8m0_inv_scale(code);
+            uint32_t piece[4];
+#pragma unroll
+            for (int q4 = 0; q4 < 4; ++q4) {
+                piece[q4] = 0;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) piece[q4] |= mx::e2m1_code(v[4 * q4 + r] * inv) << (4 * r);
+            }
+            // lane h holds features 8*q4 + 4h + 0..3 -> bytes 4*q4 + 2h, +1
+            const uint32_t send = h ? (piece[0] | (piece[1] << 16)) : (piece[2] | (piece[3] << 16));
+            const uint32_t recv = __shfl_xor(send, 32);
+            uint2 d;
+            if (h == 0) {
+                d.x = piece[0] | ((recv & 0xFFFFu) << 16);
+                d.y = piece[1] | ((recv >> 16) << 16);
+            } else {
+                d.x = (recv & 0xFFFFu) | (piece[2] << 16);
+                d.y = (recv >> 16) | (piece[3] << 16);
+            }
+            if (rloc < mrows && fb < Mi) {
+                const int64_t srow_i = off + mt + rloc;
+                *reinterpret_cast<uint2*>(g.hq + srow_i * (Mi >> 1) + (fb >> 1) + 8 * h) = d;
+                if (h == 0) g.hs[srow_i * (Mi >> 5) + (fb >> 5)] = (uint8_t)code;
+            }
+        }
+    } else {
+        const int H = g.Nw;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int rloc = rbase + 32 * i + lr;
+            if (rloc < mrows) {
+                const int p = g.pairs[off + mt + rloc];
+                const float sc = mx::bf16_to_f32(g.scores[p]);
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    const int cb = n0 + wn * 64 + 32 * j;   // 32-column block
+                    if (cb < H) {
+#pragma unroll
+                        for (int q4 = 0; q4 < 4; ++q4) {
+                            uint32_t b[4];
+#pragma unroll
+                            for (int r = 0; r < 4; ++r) {
+                                const float y = mx::bf16_to_f32(mx::f32_to_bf16_rne(acc[i][j][4 * q4 + r]));
+                                b[r] = mx::f32_to_bf16_rne(y * sc);
+                            }
+                            const uint2 d = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+                            *reinterpret_cast<uint2*>(g.yd + (int64_t)p * H + cb + 8 * q4 + 4 * h) = d;
+                        }
+                    }
+                }
+            }
+        }
+    }
 }
 
 template <int MODE, class W>
@@ -333,77 +413,173 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GArgs g, W w) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
 
-        // acc[i][j] element q of lane l: token wm*64 + 32i + l%32, weight row
-        // wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
-        if (MODE == MODE_GATEUP) {
-            const int fb = n0 + 32 * wn;           // first feature of this wave's 32-block
-            const int Mi = g.Nw;
+        tile_epilogue<MODE>(acc, g, n0, off, mt, mrows, wm * 64, wn, lr, h);
+        __syncthreads();   // LDS buffers are refilled by the next token tile
+    }
+}
+
+// ------------------------------------------------------------------ LDS-copy ring variant
+// Tiles of 256 tokens x 128 weight rows (a wave: 128 tokens x 64 rows), so an
+// expert's ~128-250 routed tokens take one pass over its weights: with
+// 128-token tiles half of the experts streamed their weights twice, the
+// second time for a handful of tokens.  The operands are copied global ->
+// LDS by buffer_load ... lds (no registers) into a ring of D_NST stages of
+// 128-wide K slices, two slices of copies in flight while a third is
+// multiplied.  LDS rows are 64 bytes with an XOR swizzle of their four
+// 16-byte chunks, so the 16 lanes of an operand read hit distinct bank
+// groups.  The epilogues are the 128 x 128 kernel's.  Requires Kp % 128 == 0.
+constexpr int DM = 256;                     // tokens per tile
+constexpr int DK = 128;                     // K per stage
+constexpr int DROWB = DK / 2;               // bytes per row per stage
+constexpr int D_A = DM * DROWB;             // 16 KB of token rows
+constexpr int D_W = BN * DROWB;             // 8 KB of weight rows
+constexpr int D_SA = DM * 4;                // 4 scale bytes per row
+constexpr int D_SW = BN * 4;
+constexpr int D_STAGE = D_A + D_W + D_SA + D_SW;
+constexpr int D_NST = 3;
+constexpr int D_COPIES = 8;                 // per wave per stage: 4 token-row, 2 weight-row, 2 scale copies
+
+__device__ __forceinline__ int dswz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+__device__ __forceinline__ uint32_t scale4(const uint8_t* p, int h) {
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(p);
+    return __builtin_amdgcn_perm(v, v, h ? 0x0C0C0301u : 0x0C0C0200u);   // byte ks = block 2ks + h
+}
+
+template <int MODE, class W>
+__global__ __launch_bounds__(256, 2) void grouped_gemm_dma_kernel(GArgs g, W w) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int e = blockIdx.y;
+    const int cnt = g.counts[e];
+    if (cnt == 0) return;
+    const int off = g.offs[e];
+    const int n0 = blockIdx.x * (MODE == MODE_GATEUP ? BN / 2 : BN);
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave >> 1, wn = wave & 1;
+    const int lr = lane & 31;
+    const int h = lane >> 5;
+    const uint32_t cbytes = (uint32_t)g.Kp >> 1, nch = (uint32_t)g.Kp >> 5;
+    const int nsteps = g.Kp / DK;
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(mx::lds_addr(smem));
+    const int slot = lane & 3;
+
+    // weight-row copies: 1 KB blocks 2*wave, 2*wave+1 of the W tile (16 rows
+    // each, all of one projection: projections change every 32 rows)
+    mx::v4u wrs[2];
+    uint32_t wvo[2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int rloc = wm * 64 + 32 * i + lr;
-                float v[16];
-                float amax = 0.0f;
+    for (int j = 0; j < 2; ++j) {
+        const int rho = 16 * (2 * wave + j) + (lane >> 2);
+        int proj;
+        const int rr = min(weight_row<MODE>(rho, n0, proj), g.Nw - 1);
+        wrs[j] = mx::buf_rsrc(w.p(e, proj), (int64_t)g.Nw * cbytes);
+        wvo[j] = (uint32_t)rr * cbytes + ((slot ^ dswz(rho)) << 4);
+    }
+    // scale copies: wave w copies the token rows' scales of rows 64w..64w+63
+    // and (lanes 0..31) the weight rows' of rows 32w..32w+31, one projection
+    uint32_t svo_w;
+    int wproj;
+    {
+        const int rr = min(weight_row<MODE>(32 * wave + (lane & 31), n0, wproj), g.Nw - 1);
+        svo_w = (uint32_t)rr * nch;
+    }
+    const mx::v4u srs_w = mx::buf_rsrc(w.s(e, wproj), (int64_t)g.Nw * nch);
+    const mx::v4u ars = mx::buf_rsrc(g.aq, (int64_t)g.a_rows * cbytes);
+    const mx::v4u asrs = mx::buf_rsrc(g.as, (int64_t)g.a_rows * nch);
+
+    for (int mt = 0; mt < cnt; mt += DM) {
+        const int mrows = min(DM, cnt - mt);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the previous tile's stores
+        uint32_t avo[4];
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    v[q] = mx::round_to_f16(mx::silu_mul(acc[i][0][q], acc[i][1][q]));
-                    amax = fmaxf(amax, fabsf(v[q]));
-                }
-                amax = fmaxf(amax, __shfl_xor(amax, 32));
-                const uint32_t code = mx::e8m0_code(amax);
-                const float inv = mx::e8m0_inv_scale(code);
-                uint32_t piece[4];
+        for (int j = 0; j < 4; ++j) {
+            const int ra = 16 * (4 * wave + j) + (lane >> 2);
+            const int r = min(ra, mrows - 1);
+            const int src = MODE == MODE_GATEUP ? g.pairs[off + mt + r] / g.topk : off + mt + r;
+            avo[j] = (uint32_t)src * cbytes + ((slot ^ dswz(ra)) << 4);
+        }
+        uint32_t svo_a;
+        {
+            const int r = min(64 * wave + lane, mrows - 1);
+            const int src = MODE == MODE_GATEUP ? g.pairs[off + mt + r] / g.topk : off + mt + r;
+            svo_a = (uint32_t)src * nch;
+        }
+
+        auto issue = [&](int stg, int k) {
+            const uint32_t buf = ring + stg * D_STAGE;
+            const uint32_t kofs = (uint32_t)k * DROWB;
 #pragma unroll
-                for (int q4 = 0; q4 < 4; ++q4) {
-                    piece[q4] = 0;
+            for (int j = 0; j < 4; ++j) mx::dma16(avo[j], ars, kofs, buf + (4 * wave + j) * 1024);
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) piece[q4] |= mx::e2m1_code(v[4 * q4 + r] * inv) << (4 * r);
-                }
-                // lane h holds features 8*q4 + 4h + 0..3 -> bytes 4*q4 + 2h, +1
-                const uint32_t send = h ? (piece[0] | (piece[1] << 16)) : (piece[2] | (piece[3] << 16));
-                const uint32_t recv = __shfl_xor(send, 32);
-                uint2 d;
-                if (h == 0) {
-                    d.x = piece[0] | ((recv & 0xFFFFu) << 16);
-                    d.y = piece[1] | ((recv >> 16) << 16);
-                } else {
-                    d.x = (recv & 0xFFFFu) | (piece[2] << 16);
-                    d.y = (recv >> 16) | (piece[3] << 16);
-                }
-                if (rloc < mrows && fb < Mi) {
-                    const int64_t srow_i = off + mt + rloc;
-                    *reinterpret_cast<uint2*>(g.hq + srow_i * (Mi >> 1) + (fb >> 1) + 8 * h) = d;
-                    if (h == 0) g.hs[srow_i * (Mi >> 5) + (fb >> 5)] = (uint8_t)code;
-                }
-            }
-        } else {
-            const int H = g.Nw;
+            for (int j = 0; j < 2; ++j) mx::dma16(wvo[j], wrs[j], kofs, buf + D_A + (2 * wave + j) * 1024);
+            const uint32_t ksc = (uint32_t)k * 4;
+            mx::dma4(svo_a, asrs, ksc, buf + D_A + D_W + 256 * wave);
+            if (lane < 32) mx::dma4(svo_w, srs_w, ksc, buf + D_A + D_W + D_SA + 128 * wave);
+        };
+
+        mx::v16f acc[4][2];
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int rloc = wm * 64 + 32 * i + lr;
-                if (rloc < mrows) {
-                    const int p = g.pairs[off + mt + rloc];
-                    const float sc = mx::bf16_to_f32(g.scores[p]);
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+#pragma unroll
+        for (int st = 0; st < D_NST - 1; ++st) issue(st, min(st, nsteps - 1));
+        const int key = dswz(lr);
+        for (int it = 0; it < nsteps; ++it) {
+            // this wave's copies of step it have landed (later steps' may still
+            // be in flight) and its reads of step it-1 are done; after the
+            // barrier every wave's.  Past the last step the copies re-read the
+            // last slice, so every step has the same count outstanding.
+            asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"((D_NST - 2) * D_COPIES) : "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            issue((it + D_NST - 1) % D_NST, min(it + D_NST - 1, nsteps - 1));
+            const uint8_t* cur = smem + (it % D_NST) * D_STAGE;
+            const uint8_t* la = cur;
+            const uint8_t* lw = cur + D_A;
+            const uint8_t* lsa = cur + D_A + D_W;
+            const uint8_t* lsw = lsa + D_SA;
+            uint32_t sa[4], sb[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sa[i] = scale4(lsa + (wm * 128 + i * 32 + lr) * 4, h);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) sb[j] = scale4(lsw + (wn * 64 + j * 32 + lr) * 4, h);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const int koff = ((2 * ks + h) ^ key) << 4;
+                uint4 af[4], bf[2];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    af[i] = *reinterpret_cast<const uint4*>(la + (wm * 128 + i * 32 + lr) * DROWB + koff);
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    bf[j] = *reinterpret_cast<const uint4*>(lw + (wn * 64 + j * 32 + lr) * DROWB + koff);
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
 #pragma unroll
                     for (int j = 0; j < 2; ++j) {
-                        const int cb = n0 + wn * 64 + 32 * j;   // 32-column block
-                        if (cb < H) {
-#pragma unroll
-                            for (int q4 = 0; q4 < 4; ++q4) {
-                                uint32_t b[4];
-#pragma unroll
-                                for (int r = 0; r < 4; ++r) {
-                                    const float y = mx::bf16_to_f32(mx::f32_to_bf16_rne(acc[i][j][4 * q4 + r]));
-                                    b[r] = mx::f32_to_bf16_rne(y * sc);
-                                }
-                                const uint2 d = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
-                                *reinterpret_cast<uint2*>(g.yd + (int64_t)p * H + cb + 8 * q4 + 4 * h) = d;
-                            }
-                        }
+                        if (ks == 0) acc[i][j] = mfma32<0>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 1) acc[i][j] = mfma32<1>(bf[j], af[i], acc[i][j], sb[j], sa[i]);
                     }
-                }
             }
         }
-        __syncthreads();   // LDS buffers are refilled by the next token tile
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the copies issued past the last step
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
+        // the wave's 128 token rows as two 64-row halves of the 128 x 128 epilogue
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+            mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]}, {acc[2 * half + 1][0], acc[2 * half + 1][1]}};
+            tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, wm * 128 + 64 * half, wn, lr, h);
+        }
+        __syncthreads();   // the ring is refilled by the next token tile
     }
 }
 
@@ -474,15 +650,17 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
                 "moe_prefill: x/out must be 16-byte and workspace 256-byte aligned");
     const WsLayout L = ws_layout(T, topk, n_exp, H, Mi);
     MXH_REQUIRE(ws_bytes >= L.total, "moe_prefill: workspace of %zu bytes < required %zu", ws_bytes, L.total);
-    static bool attr_set[2][2] = {{false, false}, {false, false}};
+    static bool attr_set[2][4] = {{false, false, false, false}, {false, false, false, false}};
     constexpr int tw = std::is_same<W, TableW>::value ? 1 : 0;
-    for (int m = 0; m < 2; ++m) {
+    for (int m = 0; m < 4; ++m) {
         if (attr_set[tw][m]) continue;
-        const void* fn = m == 0 ? reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_GATEUP, W>)
-                                : reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_DOWN, W>);
-        hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 2 * BUF_BYTES);
-        MXH_REQUIRE(e == hipSuccess, "moe_prefill: cannot reserve %d B of LDS: %s", 2 * BUF_BYTES,
-                    hipGetErrorString(e));
+        const void* fns[4] = {reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_GATEUP, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_DOWN, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_GATEUP, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_DOWN, W>)};
+        const int bytes = m < 2 ? 2 * BUF_BYTES : D_NST * D_STAGE;
+        hipError_t e = hipFuncSetAttribute(fns[m], hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        MXH_REQUIRE(e == hipSuccess, "moe_prefill: cannot reserve %d B of LDS: %s", bytes, hipGetErrorString(e));
         attr_set[tw][m] = true;
     }
     uint8_t* ws = static_cast<uint8_t*>(workspace);
@@ -511,8 +689,13 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     g.as = ws + L.xs;
     g.Kp = H;
     g.Nw = Mi;
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256), 2 * BUF_BYTES,
-                       st, g, w);
+    g.a_rows = T;
+    if (H % DK == 0)
+        hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256),
+                           D_NST * D_STAGE, st, g, w);
+    else
+        hipLaunchKernelGGL((grouped_gemm_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256),
+                           2 * BUF_BYTES, st, g, w);
     rc = mxh::launch_status("moe_prefill gate/up");
     if (rc != MXFP4_OK) return rc;
 
@@ -520,8 +703,13 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     g.as = ws + L.hs;
     g.Kp = Mi;
     g.Nw = H;
-    hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256), 2 * BUF_BYTES,
-                       st, g, w);
+    g.a_rows = P;
+    if (Mi % DK == 0)
+        hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256),
+                           D_NST * D_STAGE, st, g, w);
+    else
+        hipLaunchKernelGGL((grouped_gemm_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256),
+                           2 * BUF_BYTES, st, g, w);
     rc = mxh::launch_status("moe_prefill down");
     if (rc != MXFP4_OK) return rc;
 
