@@ -2,13 +2,15 @@
 //
 // y (M, N) fp32 = A (M, Kp) * W (N, Kp)^T, both operands packed E2M1 rows with
 // E8M0 32-block scales (the lin_pq contract, src/ext/mxfp4_decode.cu:135-170).
-// Used when Kp is a multiple of 256, M > 16 and the grid has at least 128 tiles.
+// Used when Kp is a multiple of 256 and M > 16.
 //
-// * Workgroup tile 256 x BN (BN = 256 here), NW = 8 waves in 2 (M) x 4 (N); a
-//   wave owns 128 x 64 as 4 x 2 v_mfma_scale_f32_32x32x64_f8f6f4
-//   accumulators.  (NW = 4, 128 x 128 per wave with the accumulators in AGPRs,
-//   would read a third less from LDS but does not fit the register file
-//   without spills.)
+// * Workgroup tile BM x BN with NW waves in 2 (M) x NW/2 (N).  For large
+//   grids 256 x 256 with 8 waves: a wave owns 128 x 64 as 4 x 2
+//   v_mfma_scale_f32_32x32x64_f8f6f4 accumulators.  (NW = 4, 128 x 128 per
+//   wave with the accumulators in AGPRs, would read a third less from LDS but
+//   does not fit the register file without spills.)  Smaller grids take
+//   128 x 128 or 64 x 64 tiles with 4 waves and a deeper ring (the launcher
+//   picks the instance); every instance runs the same MFMA chain per output.
 // * K step BK (BK/2 bytes of each operand row; BK = 256 here).  Global -> LDS
 //   with buffer_load_dwordx4 ... lds (no registers, no repacking): lane i of an
 //   instruction writes LDS bytes [16i, 16i+16) of a 1 KB block of whole rows.
@@ -37,10 +39,10 @@
 
 namespace {
 
-constexpr int BM = 256;
-
-template <int BN, int BK, int NW>
+template <int BM, int BN, int BK, int NW>
 struct Tile {
+    static constexpr int WM = BM / 2;                     // rows per wave (2 waves along M)
+    static constexpr int IM = WM / 32;                    // 32-row accumulator tiles per wave
     static constexpr int ROWB = BK / 2;                   // data bytes per row per step
     static constexpr int CPR = ROWB / 16;                 // 16-byte chunks per row
     static constexpr int RPB = 1024 / ROWB;               // rows per 1 KB copy block
@@ -103,9 +105,9 @@ struct CopyState {
     uint32_t vs;             // lane offset of scale copies
 };
 
-template <int BN, int BK, int NW>
+template <int BM, int BN, int BK, int NW>
 __device__ __forceinline__ CopyState copy_state(const G2Args& g, int m0, int n0) {
-    using T = Tile<BN, BK, NW>;
+    using T = Tile<BM, BN, BK, NW>;
     const int w = threadIdx.x >> 6;
     const int l = threadIdx.x & 63;
     const int64_t cbytes = g.Kp >> 1, nch = g.Kp >> 5;
@@ -135,9 +137,9 @@ __device__ __forceinline__ CopyState copy_state(const G2Args& g, int m0, int n0)
 // the next step are spread over the MFMA substeps of this one (a wave issues
 // in order, so copies issued in one burst hold back its MFMAs while the
 // memory pipeline accepts them).
-template <int BN, int BK, int NW>
+template <int BM, int BN, int BK, int NW>
 __device__ __forceinline__ void issue_part(const G2Args& g, const CopyState& c, uint32_t buf, int k0, int part) {
-    using T = Tile<BN, BK, NW>;
+    using T = Tile<BM, BN, BK, NW>;
     static_assert(T::A_CP % 2 == 0 && T::W_CP % 2 == 0, "even copy counts (swizzle key parity)");
     const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform: scalar selects below
     const uint32_t cbytes = g.Kp >> 1, nch = g.Kp >> 5;
@@ -172,10 +174,10 @@ __device__ __forceinline__ void issue_part(const G2Args& g, const CopyState& c, 
     }
 }
 
-template <int BN, int BK, int NW>
+template <int BM, int BN, int BK, int NW>
 __device__ __forceinline__ void issue_stage(const G2Args& g, const CopyState& c, uint32_t buf, int k0) {
 #pragma unroll
-    for (int q = 0; q < Tile<BN, BK, NW>::KS; ++q) issue_part<BN, BK, NW>(g, c, buf, k0, q);
+    for (int q = 0; q < Tile<BM, BN, BK, NW>::KS; ++q) issue_part<BM, BN, BK, NW>(g, c, buf, k0, q);
 }
 
 template <int OP>
@@ -201,10 +203,10 @@ __device__ __forceinline__ uint32_t scale_word(const uint8_t* srow, int h) {
 // wm*128 + i*32 + lr and wn*BN/4 + j*32 + lr, differ from lr by multiples of
 // 16, so their swizzle key is swz_key(lr): one LDS address per operand and
 // K-substep, the row offsets are immediates.
-template <int BN, int BK, int NW>
-__device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4][Tile<BN, BK, NW>::TN], const G2Args& g,
+template <int BM, int BN, int BK, int NW>
+__device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[Tile<BM, BN, BK, NW>::IM][Tile<BM, BN, BK, NW>::TN], const G2Args& g,
                                           const CopyState& cs, uint32_t nxt, int k_next) {
-    using T = Tile<BN, BK, NW>;
+    using T = Tile<BM, BN, BK, NW>;
     constexpr int TN = T::TN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -212,42 +214,49 @@ __device__ __forceinline__ void mfma_step(const uint8_t* cur, mx::v16f (&acc)[4]
     const int lr = lane & 31;
     const int h = lane >> 5;
     const int key = swz_key<T::CPR>(lr);
-    const uint8_t* la = cur + (wm * 128 + lr) * T::ROWB;
+    const uint8_t* la = cur + (wm * T::WM + lr) * T::ROWB;
     const uint8_t* lw = cur + T::A_BYTES + (wn * T::WCOLS + lr) * T::ROWB;
-    const uint8_t* lsa = cur + T::A_BYTES + T::W_BYTES + (wm * 128 + lr) * T::SCB;
+    const uint8_t* lsa = cur + T::A_BYTES + T::W_BYTES + (wm * T::WM + lr) * T::SCB;
     const uint8_t* lsw = cur + T::A_BYTES + T::W_BYTES + BM * T::SCB + (wn * T::WCOLS + lr) * T::SCB;
-    uint32_t sa[4], sb[TN];
+    uint32_t sa[T::IM], sb[TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sa[i] = scale_word<T::SCB>(lsa + i * 32 * T::SCB, h);
+    for (int i = 0; i < T::IM; ++i) sa[i] = scale_word<T::SCB>(lsa + i * 32 * T::SCB, h);
 #pragma unroll
     for (int j = 0; j < TN; ++j) sb[j] = scale_word<T::SCB>(lsw + j * 32 * T::SCB, h);
+    // operand registers of two substeps: the reads of substep ks+1 are issued
+    // before the MFMAs of substep ks, so their LDS latency hides under them
+    uint4 af[2][T::IM], bf[2][TN];
+    auto load = [&](int ks, int r) {
+        const int koff = ((2 * ks + h) ^ key) << 4;
+#pragma unroll
+        for (int i = 0; i < T::IM; ++i) af[r][i] = *reinterpret_cast<const uint4*>(la + koff + i * 32 * T::ROWB);
+#pragma unroll
+        for (int j = 0; j < TN; ++j) bf[r][j] = *reinterpret_cast<const uint4*>(lw + koff + j * 32 * T::ROWB);
+    };
+    load(0, 0);
 #pragma unroll
     for (int ks = 0; ks < T::KS; ++ks) {
         // keep each substep's copies, operand reads and MFMAs together (the
         // scheduler would otherwise hoist every copy ahead of the MFMAs)
         __builtin_amdgcn_sched_barrier(0);
-        issue_part<BN, BK, NW>(g, cs, nxt, k_next, ks);
-        const int koff = ((2 * ks + h) ^ key) << 4;
-        uint4 af[4], bf[TN];
+        issue_part<BM, BN, BK, NW>(g, cs, nxt, k_next, ks);
+        if (ks + 1 < T::KS) load(ks + 1, (ks + 1) & 1);
+        const int r = ks & 1;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *reinterpret_cast<const uint4*>(la + koff + i * 32 * T::ROWB);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) bf[j] = *reinterpret_cast<const uint4*>(lw + koff + j * 32 * T::ROWB);
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < T::IM; ++i)
 #pragma unroll
             for (int j = 0; j < TN; ++j) {
-                if (ks == 0) acc[i][j] = mfma32<0>(af[i], bf[j], acc[i][j], sa[i], sb[j]);
-                if (ks == 1) acc[i][j] = mfma32<1>(af[i], bf[j], acc[i][j], sa[i], sb[j]);
-                if (ks == 2) acc[i][j] = mfma32<2>(af[i], bf[j], acc[i][j], sa[i], sb[j]);
-                if (ks == 3) acc[i][j] = mfma32<3>(af[i], bf[j], acc[i][j], sa[i], sb[j]);
+                if (ks == 0) acc[i][j] = mfma32<0>(af[r][i], bf[r][j], acc[i][j], sa[i], sb[j]);
+                if (ks == 1) acc[i][j] = mfma32<1>(af[r][i], bf[r][j], acc[i][j], sa[i], sb[j]);
+                if (ks == 2) acc[i][j] = mfma32<2>(af[r][i], bf[r][j], acc[i][j], sa[i], sb[j]);
+                if (ks == 3) acc[i][j] = mfma32<3>(af[r][i], bf[r][j], acc[i][j], sa[i], sb[j]);
             }
     }
 }
 
-template <int BN, int BK, int NSTAGE, int NW>
+template <int BM, int BN, int BK, int NSTAGE, int NW>
 __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
-    using T = Tile<BN, BK, NW>;
+    using T = Tile<BM, BN, BK, NW>;
     constexpr int TN = T::TN;
     static_assert(NSTAGE >= 2 && NSTAGE * T::STAGE <= 160 * 1024, "LDS ring");
     __shared__ __align__(16) uint8_t ring[NSTAGE * T::STAGE];
@@ -272,18 +281,18 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
     const int h = lane >> 5;
     const int nsteps = g.Kp / BK;
 
-    mx::v16f acc[4][TN];
+    mx::v16f acc[T::IM][TN];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < T::IM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const CopyState cs = copy_state<BN, BK, NW>(g, m0, n0);
+    const CopyState cs = copy_state<BM, BN, BK, NW>(g, m0, n0);
     const uint32_t ring_lds = __builtin_amdgcn_readfirstlane(lds_addr(ring));   // LDS byte address of the ring
 #pragma unroll
-    for (int s = 0; s < NSTAGE - 1; ++s) issue_stage<BN, BK, NW>(g, cs, ring_lds + s * T::STAGE, min(s, nsteps - 1) * BK);
+    for (int s = 0; s < NSTAGE - 1; ++s) issue_stage<BM, BN, BK, NW>(g, cs, ring_lds + s * T::STAGE, min(s, nsteps - 1) * BK);
 
     for (int it0 = 0; it0 < nsteps; it0 += NSTAGE) {
 #pragma unroll
@@ -301,7 +310,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
                 asm volatile("" ::: "memory");
                 // MFMAs on this step's stage; the stage step it-1 used is
                 // refilled with step it+NSTAGE-1, spread over the substeps
-                mfma_step<BN, BK, NW>(ring + s * T::STAGE, acc, g, cs, ring_lds + ((s + NSTAGE - 1) % NSTAGE) * T::STAGE,
+                mfma_step<BM, BN, BK, NW>(ring + s * T::STAGE, acc, g, cs, ring_lds + ((s + NSTAGE - 1) % NSTAGE) * T::STAGE,
                                   min(it + NSTAGE - 1, nsteps - 1) * BK);
             }
         }
@@ -311,7 +320,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
     // LDS can be handed to another workgroup
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < T::IM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             if constexpr (NW == 4) mx::pin_acc(acc[i][j]);
@@ -319,14 +328,14 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
         }
     // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < T::IM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
             const int col = n0 + wn * T::WCOLS + j * 32 + lr;
             if (col >= g.N) continue;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
+                const int row = m0 + wm * T::WM + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
                 if (row < g.M) g.y[(int64_t)row * g.N + col] = acc[i][j][e];
             }
         }
@@ -352,17 +361,14 @@ void xcd_blocks(G2Args& g) {
 }  // namespace
 
 namespace mxh {
-// The 256 x 256 tile pays off when the grid fills at least half the CUs
-// (measured on MI355X: 4096 x 4096 x 2048 in 29.8 us against 36.9 us for the
-// 128 x 128 register-staged GEMM; 1024 x 4096 x 2048, 64 tiles, is faster there).
+// Any M > 16 with Kp a multiple of 256 (the buffer descriptors address each
+// operand with 32-bit byte offsets, hence the size bound).
 bool lin_pq_gemm2_supported(int M, int N, int Kp) {
-    const int64_t tiles = (int64_t)((M + BM - 1) / BM) * ((N + 255) / 256);
-    // buffer descriptors address each operand with 32-bit byte offsets
     const bool fits = (int64_t)M * (Kp / 2) < (1ll << 32) && (int64_t)N * (Kp / 2) < (1ll << 32);
-    return M > 16 && N > 0 && Kp >= 256 && (Kp % 256) == 0 && tiles >= 128 && fits;
+    return M > 16 && N > 0 && Kp >= 256 && (Kp % 256) == 0 && fits;
 }
 
-template <int BN, int BK, int NSTAGE, int NW>
+template <int BM, int BN, int BK, int NSTAGE, int NW>
 int launch_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const uint8_t* wsc, float* y, int M, int N,
                  int Kp, hipStream_t st) {
     MXH_REQUIRE(Kp % BK == 0, "lin_pq_gemm2: Kp=%d is not a multiple of %d", Kp, BK);
@@ -370,7 +376,7 @@ int launch_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const
     g.tiles_m = (M + BM - 1) / BM;
     g.tiles_n = (N + BN - 1) / BN;
     xcd_blocks(g);
-    hipLaunchKernelGGL((gemm2_kernel<BN, BK, NSTAGE, NW>), dim3(8 * g.per_xcd), dim3(64 * NW), 0, st, g);
+    hipLaunchKernelGGL((gemm2_kernel<BM, BN, BK, NSTAGE, NW>), dim3(8 * g.per_xcd), dim3(64 * NW), 0, st, g);
     return launch_status("lin_pq_gemm2");
 }
 
@@ -380,6 +386,20 @@ int lin_pq_gemm2(const uint8_t* xq, const uint8_t* xsc, const uint8_t* wp, const
                 "lin_pq: packed operands must be 16-byte aligned");
     MXH_REQUIRE(((uintptr_t)xsc & 3) == 0 && ((uintptr_t)wsc & 3) == 0,
                 "lin_pq: scale rows must be 4-byte aligned");
-    return launch_gemm2<256, 256, 2, 8>(xq, xsc, wp, wsc, y, M, N, Kp, st);
+    // Tile by grid size: 256 x 256 (2 stages) when it gives at least 128
+    // tiles; else 128 x 128 (4 stages) when that gives at least 192; else
+    // 64 x 64 with 8 stages, i.e. up to 7 K-steps of copies in flight, so a
+    // small grid pays about one memory latency instead of one per K-step --
+    // or with 4 stages (two workgroups per CU) when one per CU would take
+    // two rounds.  Measured on MI355X: 512 x 1536 x 2048 in 6.5 us against
+    // 11.1 us for the 128 x 128 register-staged GEMM; all tiles give the same
+    // bits (the same MFMA chain per output).
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    const int64_t t64 = (int64_t)((M + 63) / 64) * ((N + 63) / 64);
+    if (t256 >= 128) return launch_gemm2<256, 256, 256, 2, 8>(xq, xsc, wp, wsc, y, M, N, Kp, st);
+    if (t128 >= 192) return launch_gemm2<128, 128, 256, 4, 4>(xq, xsc, wp, wsc, y, M, N, Kp, st);
+    if (t64 > 256) return launch_gemm2<64, 64, 256, 4, 4>(xq, xsc, wp, wsc, y, M, N, Kp, st);
+    return launch_gemm2<64, 64, 256, 8, 4>(xq, xsc, wp, wsc, y, M, N, Kp, st);
 }
 }  // namespace mxh

@@ -30,6 +30,9 @@ LIN_SHAPES = [(1, 32, 64), (1, 768, 2048), (1, 2048, 768), (3, 128, 100), (1, 40
               (2, 2048, 2048), (16, 64, 96), (17, 64, 256), (128, 128, 256), (200, 300, 1000),
               (129, 257, 40), (512, 1536, 2048), (300, 520, 768), (2048, 2048, 768),
               (2048, 4096, 512), (2000, 4000, 768),   # these two on the 256 x 256 tile GEMM
+              # ragged edges on the 128 x 128 ring (192 tiles) and the 4-stage 64 x 64 ring (270 tiles);
+              # (512, 1536, 2048), (17, 64, 256) and (300, 520, 768) run on the 8-stage 64 x 64 ring
+              (1000, 3000, 512), (1100, 900, 1024),
               # small-M split-K GEMV: K in 16 / 8 / 4 parts, unsplit with 4 row tiles, odd step count
               (1, 128, 2048), (1, 2048, 4096), (1, 5120, 2048), (3, 20000, 2048), (5, 1000, 4160),
               (8, 136, 2048), (40, 48, 96)]
