@@ -114,13 +114,14 @@ __device__ __forceinline__ void load_seg(SegBuf& sb, const SegCtx& cx, int s0) {
         const int c = 4 * s + cx.g;
         const bool ok = (s < cx.steps) && (c < cx.nch);
         sb.b[j] = ok ? *reinterpret_cast<const uint4*>(cx.wrow + c * 16) : make_uint4(0, 0, 0, 0);
-        sb.bs[j] = ok ? (uint32_t)cx.srow[c] : 127u;
         if (AMODE == A_FP4) {
             const bool aok = ok && cx.arow_ok;
             sb.a[j] = aok ? *reinterpret_cast<const uint4*>(cx.arow + c * 16) : make_uint4(0, 0, 0, 0);
-            sb.as[j] = aok ? (uint32_t)cx.asrow[c] : 127u;
         }
     }
+    static_assert(kSeg == 4, "mx::seg_scales covers 4 K-steps");
+    mx::seg_scales(sb.bs, cx.srow, true, cx.g, s0, cx.steps, cx.nch);
+    if (AMODE == A_FP4) mx::seg_scales(sb.as, cx.asrow, cx.arow_ok, cx.g, s0, cx.steps, cx.nch);
 }
 
 template <int AMODE>

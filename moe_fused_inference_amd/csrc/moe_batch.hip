@@ -34,7 +34,7 @@ namespace {
 constexpr int kMaxTok = 16;     // tokens per step: one MFMA row tile
 constexpr int kMaxE = 8;        // slots per token (moe_combine's cap)
 constexpr int kMaxSlots = kMaxTok * kMaxE;
-constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment
+constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment (mx::seg_scales covers 4)
 constexpr int kDownWaves = 8;
 
 struct BatchArgs {
@@ -63,34 +63,6 @@ struct Seg {
     uint32_t as[kSegB];
 };
 
-// The scale bytes 4*(st0 + j) + q, j < kSegB, of one row: bytes [4*st0,
-// 4*st0 + 16) of the row hold them all, so when that span lies inside the
-// row one 16-byte load (or two 8-byte loads on 8-byte aligned rows) replaces
-// the four byte loads; byte j of the lane is byte q of dword j.
-__device__ __forceinline__ void load_scales(uint32_t out[kSegB], const uint8_t* srow, bool ok, int q, int st0,
-                                            int steps, int nch) {
-    const uint8_t* p = srow + 4 * st0;
-    const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-    if (ok && 4 * st0 + 16 <= nch && (ad & 7) == 0) {
-        uint32_t d[4];
-        if ((ad & 15) == 0) {
-            const uint4 v = *reinterpret_cast<const uint4*>(p);
-            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-        } else {
-            const uint2 v0 = *reinterpret_cast<const uint2*>(p), v1 = *reinterpret_cast<const uint2*>(p + 8);
-            d[0] = v0.x; d[1] = v0.y; d[2] = v1.x; d[3] = v1.y;
-        }
-#pragma unroll
-        for (int j = 0; j < kSegB; ++j) out[j] = (st0 + j < steps) ? (d[j] >> (8 * q)) & 0xFFu : 127u;
-    } else {
-#pragma unroll
-        for (int j = 0; j < kSegB; ++j) {
-            const int c = 4 * (st0 + j) + q;
-            out[j] = (ok && st0 + j < steps && c < nch) ? (uint32_t)srow[c] : 127u;
-        }
-    }
-}
-
 // Lane (row l%16, group q = l/16) takes 32-block 4*st + q at K-step st (64
 // contiguous bytes per row and load instruction); rows past the A rows
 // (tokens) or blocks past the row read zeros with scale code 127.
@@ -103,8 +75,8 @@ __device__ __forceinline__ void load_seg(Seg& sg, const uint8_t* wrow, const uin
         sg.b[j] = ok ? *reinterpret_cast<const uint4*>(wrow + c * 16) : make_uint4(0, 0, 0, 0);
         sg.a[j] = (ok && aok) ? *reinterpret_cast<const uint4*>(arow + c * 16) : make_uint4(0, 0, 0, 0);
     }
-    load_scales(sg.bs, srow, true, q, st0, steps, nch);
-    load_scales(sg.as, asrow, aok, q, st0, steps, nch);
+    mx::seg_scales(sg.bs, srow, true, q, st0, steps, nch);
+    mx::seg_scales(sg.as, asrow, aok, q, st0, steps, nch);
 }
 
 __device__ __forceinline__ mx::v4f mma_seg(const Seg& sg, int st0, int steps, mx::v4f acc) {

@@ -85,6 +85,38 @@ __device__ __forceinline__ uint32_t e2m1_pack8(const float v[8], float inv) {
     return r;
 }
 
+// ---------------------------------------------------------------- scale loads
+// MFMA K-steps st0 .. st0+3 of a lane in group q (block 4*st + q at step st)
+// need the scale bytes 4*(st0 + j) + q, j < 4, of one row: bytes [4*st0,
+// 4*st0 + 16) of the row hold them all, so when that span lies inside the
+// row one 16-byte load (or two 8-byte loads on 8-byte aligned rows) replaces
+// the four byte loads; byte j of the lane is byte q of dword j.
+__device__ __forceinline__ void seg_scales(uint32_t out[4], const uint8_t* srow, bool ok, int q, int st0,
+                                           int steps, int nch) {
+    const uint8_t* p = srow + 4 * st0;
+    const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
+    if (ok && 4 * st0 + 16 <= nch && (ad & 7) == 0) {
+        uint32_t d[4];
+        if ((ad & 15) == 0) {
+            const uint4 v = *reinterpret_cast<const uint4*>(p);
+            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
+        } else {
+            const uint2 v0 = *reinterpret_cast<const uint2*>(p), v1 = *reinterpret_cast<const uint2*>(p + 8);
+            d[0] = v0.x; d[1] = v0.y; d[2] = v1.x; d[3] = v1.y;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) out[j] = (st0 + j < steps) ? (d[j] >> (8 * q)) & 0xFFu : 127u;
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int c = 4 * (st0 + j) + q;
+            out[j] = (ok && st0 + j < steps && c < nch) ? (uint32_t)srow[c] : 127u;
+        }
+    }
+}
+
+// Out-of-range steps or blocks, and !ok, give code 127 (scale 1, zero data).
+
 // ---------------------------------------------------------------- FP4 decode
 // E2M1 nibble -> fp32 (used by reference-style epilogues and tests only).
 __device__ __forceinline__ float e2m1_value(uint32_t c) {
