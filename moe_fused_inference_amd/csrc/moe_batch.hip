@@ -15,13 +15,15 @@
 //                        -- moe_down's own activation quantization
 //                        (src/ext/mxfp4_decode.cu:218-279), bit-exact to it
 //                        given g and u.
-//   batch_down_kernel    workgroup (16 output columns): 8 waves share out the
+//   batch_down_kernel    workgroup (16 output columns): 12 waves share out the
 //                        distinct experts (slot order); per expert, its down
 //                        rows for the columns times the h rows of its tokens,
 //                        weighted by the routing weights (moe_combine,
 //                        src/ext/mxfp4_decode.cu:285-299) into per-wave
-//                        token sums in LDS; the 8 wave sums are added in a
-//                        fixed order.  No gu / yd round trip through HBM and
+//                        token sums in LDS; the 12 wave sums are added in a
+//                        fixed order.  (150 VGPRs: 3 waves per SIMD, so 12
+//                        waves fit one CU; each wave walks a third fewer
+//                        experts than with 8.)  No gu / yd round trip through HBM and
 //                        no separate combine launch.
 //
 // The results match the drop-in chain up to fp32 summation order (the
@@ -35,7 +37,7 @@ constexpr int kMaxTok = 16;     // tokens per step: one MFMA row tile
 constexpr int kMaxE = 8;        // slots per token (moe_combine's cap)
 constexpr int kMaxSlots = kMaxTok * kMaxE;
 constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment (mx::seg_scales covers 4)
-constexpr int kDownWaves = 8;
+constexpr int kDownWaves = 12;   // 3 waves per SIMD at 150 VGPRs
 
 struct BatchArgs {
     const uint8_t* xq;   // (M, H/2) MXFP4 activation rows
