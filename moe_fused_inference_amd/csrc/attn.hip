@@ -401,9 +401,11 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     const int nchunk = (max_pos + kChunk - 1) / kChunk;
     const float invsqrt = 1.0f / sqrtf((float)D);
     hipStream_t st = mxh::as_stream(stream);
-    // row tiles of 16 query rows per workgroup: all M*G rows up to 64
+    // row tiles of 16 query rows per workgroup, at most 2: more token groups
+    // (workgroups) rather than more rows each -- 4 tiles halved the grid at
+    // M = 8 and took 9 % longer
     const int rows = M * G;
-    const int RT = rows <= 16 ? 1 : (rows <= 32 ? 2 : 4);
+    const int RT = rows <= 16 ? 1 : 2;
     const int MT = (16 * RT) / G > 0 ? (16 * RT) / G : 1;
     MXH_REQUIRE(16 * RT >= G, "attn_decode: G=%d exceeds the 64 query rows of a workgroup", G);
     const dim3 gp(nchunk, Hkv, (M + MT - 1) / MT);
@@ -415,8 +417,7 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
 #define MXH_ATTN_G(GG)                  \
     switch (RT) {                       \
         case 1: MXH_ATTN(GG, 1); break; \
-        case 2: MXH_ATTN(GG, 2); break; \
-        default: MXH_ATTN(GG, 4); break; \
+        default: MXH_ATTN(GG, 2); break; \
     }
     switch (G) {
         case 1: MXH_ATTN_G(1); break;
