@@ -378,7 +378,10 @@ def bench_step(torch, layers, M, steps=128):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    st.check_status()                     # raises if a fused layer's bounded wait expired in any step
     end_pos = int(st.b.dpos.item())
+    if end_pos != 4096:
+        raise RuntimeError(f"decode step: position after the timed steps is {end_pos}, expected 4096")
     moe_graph = st.capture_fn(st.run_moe_only)
     reps = 10
     e0.record()
@@ -387,6 +390,7 @@ def bench_step(torch, layers, M, steps=128):
     e1.record()
     torch.cuda.synchronize()
     ms_moe = e0.elapsed_time(e1) / reps
+    st.check_status()
     del graph, moe_graph, st, model
     return {"M": M, "steps": steps, "context_end": end_pos, "ms_per_step": round(ms, 3),
             "tok_per_s": round(M * 1e3 / ms, 1), "moe_ms_per_step": round(ms_moe, 3),

@@ -407,7 +407,7 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     const int rows = M * G;
     const int RT = rows <= 16 ? 1 : 2;
     const int MT = (16 * RT) / G > 0 ? (16 * RT) / G : 1;
-    MXH_REQUIRE(16 * RT >= G, "attn_decode: G=%d exceeds the 64 query rows of a workgroup", G);
+    MXH_REQUIRE(16 * RT >= G, "attn_decode: G=%d exceeds the 32 query rows of a workgroup", G);
     const dim3 gp(nchunk, Hkv, (M + MT - 1) / MT);
     const uint16_t* qh = static_cast<const uint16_t*>(q);
     float* part = static_cast<float*>(workspace);

@@ -2,15 +2,18 @@
 // fused decode kernels (one layer per launch, and several layers per launch).
 //
 // There is no bf16 x FP4 MFMA, so a bf16 (or fp32) activation is split into
-// kTerms E4M3 terms hi + mid + lo, each with its own E8M0 32-block scale, that
-// sum back to the value to about 12 significant bits (exactly for bf16).  The
-// terms are rows 0..2 of the A operand of v_mfma_scale_f32_16x16x128_f8f6f4.
+// kTerms E4M3 terms hi + mid + lo, each with its own E8M0 32-block scale.  The
+// terms sum back to the value with an error of at most about 2^-12 of the
+// block's largest magnitude: a value far below its block's amax (more than
+// ~2^17 below it) can fall under every term's scale and drop out.  The terms
+// are rows 0..2 of the A operand of v_mfma_scale_f32_16x16x128_f8f6f4.
 #pragma once
 #include "mx_device.h"
 
 namespace dl {
 
-constexpr int kSpinLimit = 1 << 22;   // polls of one word (~0.2 s)
+constexpr int kSpinLimit = 1 << 22;   // polls per wait: about 1.3 s of polling (one round trip of ~0.3 us
+                                      // each, s_sleep 1 between them) before the wait gives up
 constexpr int kTerms = 3;             // E4M3 terms per activation value
 constexpr int kMaxE = 8;
 constexpr int kRecWords = 32;         // words per (slot, 32-block) record of h: one per value,
@@ -54,7 +57,7 @@ __device__ __forceinline__ float quad_max(float v) {
 // aligned) into kTerms E4M3 terms: word8[t] receives the 8 E4M3 bytes of term
 // t and codes (byte t) the term's E8M0 scale code.  Each term is the E4M3
 // rounding of what the previous terms left over, so the terms sum to the value
-// up to the last term's rounding (exact for bf16 inputs).
+// up to the last term's rounding, relative to the block amax (about 2^-12 of it).
 __device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint32_t& codes) {
     codes = 0;
 #pragma unroll

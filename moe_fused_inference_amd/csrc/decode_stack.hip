@@ -578,6 +578,17 @@ extern "C" int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const f
     MXH_REQUIRE(nA + nB <= n_cu && nA + nB <= kMaxWg,
                 "moe_decode_stack: E*Mi/32 + H/32 = %d workgroups, more than the %d CUs (one resident workgroup per CU)",
                 nA + nB, n_cu);
+    const int steps = (Mi / 32 + 3) / 4;
+    const void* kern = steps <= 6 ? (strict ? reinterpret_cast<const void*>(&decode_stack_kernel<true, 6>)
+                                            : reinterpret_cast<const void*>(&decode_stack_kernel<false, 6>))
+                                  : (strict ? reinterpret_cast<const void*>(&decode_stack_kernel<true, 8>)
+                                            : reinterpret_cast<const void*>(&decode_stack_kernel<false, 8>));
+    int per_cu = 0;
+    MXH_REQUIRE(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) == hipSuccess,
+                "moe_decode_stack: occupancy query failed");
+    // every workgroup waits on others, so the whole grid must be resident at once
+    MXH_REQUIRE((int64_t)per_cu * n_cu >= nA + nB,
+                "moe_decode_stack: %d workgroups but only %d x %d can be resident at once", nA + nB, per_cu, n_cu);
     StackArgs a{};
     a.layers = static_cast<const StackLayer*>(layer_table);
     a.ids = ids;
@@ -600,7 +611,6 @@ extern "C" int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const f
     a.xwords = x_words(H);
     a.ws = static_cast<uint8_t*>(workspace);
     hipStream_t st = mxh::as_stream(stream);
-    const int steps = (Mi / 32 + 3) / 4;
     const dim3 grid(nA + nB), block(256);
     if (steps <= 6) {
         if (strict) hipLaunchKernelGGL((decode_stack_kernel<true, 6>), grid, block, 0, st, a);

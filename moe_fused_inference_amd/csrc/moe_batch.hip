@@ -215,7 +215,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     const int H = a.H, Mi = a.Mi;
     const int nch = Mi / 32, steps = (nch + 3) / 4;
     const int col = cb * 16 + l16;   // this lane's weight row of down = output column
-    // wave w: owners w, w + 8, ...
+    // wave w: owners w, w + kDownWaves, ...
     for (int k = wave; k < nown; k += kDownWaves) {
         const int slot0 = s_owner[k];
         const int e = s_ids[slot0];

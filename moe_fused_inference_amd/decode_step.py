@@ -32,7 +32,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
-from .moe_layer import RoutedLayerCall, StackedExperts, workspace as layer_workspace
+from .moe_layer import RoutedLayerCall, StackedExperts, layer_status, workspace as layer_workspace
 
 
 @dataclass
@@ -305,6 +305,26 @@ class DecodeStep:
                                             ex.up_ws.data_ptr(), ex.down_wp.data_ptr(), ex.down_ws.data_ptr(),
                                             c.n_experts, M, E, H, Mi, b.moe.data_ptr(), b.moe_ws.data_ptr(),
                                             b.moe_ws.numel(), s), "moe_decode_batch")
+
+    def check_status(self):
+        """Raise if a fused MoE layer of the steps issued so far (eager or
+        graph replays) reported an expired bounded wait.  Its output is then
+        garbage: the down workgroups that stopped waiting never wrote their
+        columns, so the step would add a stale MoE output.  The workspace is
+        re-initialised before raising, as the fused layer's contract asks.
+        Synchronises the device (reads the flag)."""
+        if self.M != 1:
+            return   # the batched MoE (route_topk + moe_decode_batch) has no cross-workgroup waits
+        torch.cuda.synchronize()
+        flag = layer_status(self.layer_ws)
+        if flag != 0:
+            c = self.cfg
+            _lib.check(self.lib.mxfp4_decode_layer_reset(self.layer_ws.data_ptr(), c.top_k, c.hidden, c.moe_inter,
+                                                         torch.cuda.current_stream().cuda_stream),
+                       "decode_layer_reset")
+            torch.cuda.synchronize()
+            raise RuntimeError(f"decode step: a fused MoE layer's bounded wait expired (flag {flag}); "
+                               "the step's outputs are invalid (workspace re-initialised)")
 
     def run_moe_only(self):
         """The step's 48 MoE blocks alone, on the buffers the last step left

@@ -3,7 +3,7 @@
 ``get_ext()`` returns the ``mxfp4_linear_ext`` surface (``forward``) and
 ``get_decode_ext()`` the ``mxfp4_decode_ext`` surface (``prequant``,
 ``lin_pq``, ``moe_gateup``, ``moe_down``, ``moe_combine``, ``moe_gateup_tab``,
-``moe_down_tab``; ``attn_decode`` / ``kv_write`` are not built yet and raise).
+``moe_down_tab``, ``attn_decode`` and ``kv_write``).
 Names, argument order, argument meaning, output shapes/dtypes and the
 argument checks (RuntimeError with the reference's messages) follow the
 pybind bindings src/ext/mxfp4_binding.cpp:21-50 and

@@ -48,6 +48,17 @@ def lin_pq_ref(xq, xsc, wp, wsc):
     return gemm_ref(fmt.dequant_rows(xq, xsc), fmt.dequant_rows(wp, wsc))
 
 
+def lin_pq_ref_chunked(xq, xsc, wp, wsc, rows=8192):
+    """lin_pq_ref over row chunks of W (float64 dequant of one chunk at a
+    time) for very tall weights such as a 151,936-row lm_head."""
+    a = fmt.dequant_rows(xq, xsc).astype(np.float64)
+    out = np.empty((a.shape[0], wp.shape[0]), np.float64)
+    for r0 in range(0, wp.shape[0], rows):
+        w = fmt.dequant_rows(wp[r0:r0 + rows], wsc[r0:r0 + rows]).astype(np.float64)
+        out[:, r0:r0 + rows] = a @ w.T
+    return out
+
+
 def forward_ref(x, wp, wsc):
     kp = wp.shape[1] * 2
     xq, xsc = forward_act_quant_ref(x, kp)

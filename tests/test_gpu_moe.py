@@ -115,15 +115,18 @@ def _zipf_topi(rng, M, E, n_exp, s=1.1, beta=1.0):
     return np.stack(out)
 
 
-@pytest.mark.parametrize("beta", [0.5, 1.5])
+@pytest.mark.parametrize("beta", [0.0, 0.5, 0.75, 1.0, 1.5])
 def test_spec_verify_m9_grouped(dext, beta):
-    """M = 1 + 8 draft tokens, Zipf-biased routing: experts shared between
+    """Config 4: M = 1 + 8 draft tokens, router logits N(0,1) + beta * log
+    p_Zipf(1.1) over a seeded permutation of all 128 experts (beta = 0:
+    uniform routing, the most distinct experts); experts shared between
     tokens are grouped inside the kernel; results per (token, slot) entry."""
     E, M = 8, 9
-    rng = np.random.default_rng(int(beta * 10))
-    topi = _zipf_topi(rng, M, E, 48, beta=beta)
+    rng = np.random.default_rng(int(beta * 100))
+    topi = _zipf_topi(rng, M, E, 128, beta=beta)
     distinct = sorted(set(topi.reshape(-1).tolist()))
-    log(f"  beta={beta}: {len(distinct)} distinct experts over {M * E} slots")
+    log(f"  beta={beta}: {len(distinct)} distinct experts of 128 over {M * E} slots")
+    assert max(distinct) < 128 and len(distinct) >= E
     ex = Experts(dext, distinct)
     g = torch.Generator(device=DEV)
     g.manual_seed(1)
