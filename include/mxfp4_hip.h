@@ -406,6 +406,20 @@ int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, const int32_t* 
                            const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws, int n_experts,
                            int M, int E, int H, int Mi, float* y, void* ws, size_t ws_bytes, void* stream);
 
+/* mxfp4_moe_decode_batch_noalloc: mxfp4_moe_decode_batch with its h staged
+ * in a fixed scratch array of the library (139,264 bytes per GPU, held until
+ * the process ends) instead of a caller workspace.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops).  It calls no allocator.  Limits as
+ * mxfp4_moe_decode_batch plus Mi <= 2048; larger shapes return MXFP4_EINVAL.
+ * Every call on one GPU shares that GPU's scratch: calls that overlap in time
+ * on one GPU (different streams, no ordering) race and give wrong results;
+ * stream-ordered calls are safe.  Nothing is kept between calls. */
+int mxfp4_moe_decode_batch_noalloc(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, const float* w,
+                                   const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                                   const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                                   int n_experts, int M, int E, int H, int Mi, float* y, void* stream);
+
 /* ---------------------------------------------------------------------
  * Grouped MoE over a batch of tokens (prefill, speculative verify).
  * Replaces ModelRunnerV2.moe_compute (runtime/model_runner_v2.py:108-122):

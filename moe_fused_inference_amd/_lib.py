@@ -62,6 +62,8 @@ SIGNATURES = {
     "mxfp4_moe_decode_batch_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
     "mxfp4_moe_decode_batch": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i,
                                       _c_i, _c_i, _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_moe_decode_batch_noalloc": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i,
+                                              _c_i, _c_i, _c_i, _c_i, _c_p, _c_p]),
     "mxfp4_moe_prefill_workspace_size": (_c_sz, [_c_i, _c_i, _c_i, _c_i, _c_i]),
     "mxfp4_moe_prefill": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                  _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz, _c_p]),

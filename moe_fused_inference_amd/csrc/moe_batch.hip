@@ -28,6 +28,8 @@
 //
 // The results match the drop-in chain up to fp32 summation order (the
 // combine adds a token's experts grouped by wave instead of in slot order).
+#include <mutex>
+
 #include "mx_device.h"
 #include "mx_host.h"
 
@@ -261,6 +263,63 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     }
 }
 
+// Scratch of mxfp4_moe_decode_batch_noalloc: the per-slot MXFP4 h of up to
+// kMaxSlots slots at Mi <= kNoAllocMaxMi, 139,264 bytes.  One copy per GPU,
+// held until the process ends; host code addresses it only through the
+// pointer hipGetSymbolAddress returns for the current device.
+constexpr int kNoAllocMaxMi = 2048;
+constexpr size_t kScratchBytes = (size_t)kMaxSlots * (kNoAllocMaxMi / 2 + kNoAllocMaxMi / 32);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.
+int scratch_on_current_device(void** out) {
+    int dev = -1;
+    MXH_REQUIRE(hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < kMaxDevices,
+                "moe_decode_batch_noalloc: no usable current device (%d)", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        MXH_REQUIRE(e == hipSuccess && p != nullptr, "moe_decode_batch_noalloc: hipGetSymbolAddress: %s",
+                    hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return MXFP4_OK;
+}
+
+int check_batch_args(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, const float* w,
+                     const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp, const uint8_t* up_ws,
+                     const uint8_t* down_wp, const uint8_t* down_ws, int n_experts, int M, int E, int H, int Mi,
+                     const float* y) {
+    MXH_REQUIRE(xq && xs && ids && w && gate_wp && gate_ws && up_wp && up_ws && down_wp && down_ws && y,
+                "moe_decode_batch: null pointer");
+    MXH_REQUIRE(M >= 1 && M <= kMaxTok, "moe_decode_batch: M=%d outside 1..%d", M, kMaxTok);
+    MXH_REQUIRE(E >= 1 && E <= kMaxE, "moe_decode_batch: E=%d outside 1..%d", E, kMaxE);
+    MXH_REQUIRE(n_experts >= 1, "moe_decode_batch: n_experts=%d", n_experts);
+    MXH_REQUIRE(H >= 128 && H % 128 == 0, "moe_decode_batch: H=%d must be a positive multiple of 128", H);
+    MXH_REQUIRE(Mi >= 32 && Mi % 32 == 0, "moe_decode_batch: Mi=%d must be a positive multiple of 32", Mi);
+    MXH_REQUIRE(((uintptr_t)xq & 15) == 0 && ((uintptr_t)gate_wp & 15) == 0 && ((uintptr_t)up_wp & 15) == 0 &&
+                    ((uintptr_t)down_wp & 15) == 0,
+                "moe_decode_batch: packed operands and the workspace must be 16-byte aligned");
+    return MXFP4_OK;
+}
+
+// The two launches, h staged in w8 (S*(Mi/2) + S*(Mi/32) bytes, 16-byte aligned).
+int launch_batch(const BatchArgs& a, hipStream_t st) {
+    const int S = a.M * a.E;
+    hipLaunchKernelGGL(batch_gateup_kernel, dim3(a.Mi / 32, S), dim3(256), 0, st, a);
+    const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
+    if (rc != MXFP4_OK) return rc;
+    hipLaunchKernelGGL(batch_down_kernel, dim3(a.H / 16), dim3(64 * kDownWaves), 0, st, a);
+    return mxh::launch_status("moe_decode_batch (down)");
+}
+
 }  // namespace
 
 extern "C" size_t mxfp4_moe_decode_batch_workspace_size(int M, int E, int Mi) {
@@ -274,27 +333,42 @@ extern "C" int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, cons
                                       const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
                                       int n_experts, int M, int E, int H, int Mi, float* y, void* ws,
                                       size_t ws_bytes, void* stream) {
-    MXH_REQUIRE(xq && xs && ids && w && gate_wp && gate_ws && up_wp && up_ws && down_wp && down_ws && y && ws,
-                "moe_decode_batch: null pointer");
-    MXH_REQUIRE(M >= 1 && M <= kMaxTok, "moe_decode_batch: M=%d outside 1..%d", M, kMaxTok);
-    MXH_REQUIRE(E >= 1 && E <= kMaxE, "moe_decode_batch: E=%d outside 1..%d", E, kMaxE);
-    MXH_REQUIRE(n_experts >= 1, "moe_decode_batch: n_experts=%d", n_experts);
-    MXH_REQUIRE(H >= 128 && H % 128 == 0, "moe_decode_batch: H=%d must be a positive multiple of 128", H);
-    MXH_REQUIRE(Mi >= 32 && Mi % 32 == 0, "moe_decode_batch: Mi=%d must be a positive multiple of 32", Mi);
+    const int rc = check_batch_args(xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M,
+                                    E, H, Mi, y);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE(ws, "moe_decode_batch: null pointer");
     MXH_REQUIRE(ws_bytes >= mxfp4_moe_decode_batch_workspace_size(M, E, Mi),
                 "moe_decode_batch: workspace of %zu bytes, %zu needed", ws_bytes,
                 mxfp4_moe_decode_batch_workspace_size(M, E, Mi));
-    MXH_REQUIRE(((uintptr_t)ws & 15) == 0 && ((uintptr_t)xq & 15) == 0 && ((uintptr_t)gate_wp & 15) == 0 &&
-                    ((uintptr_t)up_wp & 15) == 0 && ((uintptr_t)down_wp & 15) == 0,
-                "moe_decode_batch: packed operands and the workspace must be 16-byte aligned");
+    MXH_REQUIRE(((uintptr_t)ws & 15) == 0, "moe_decode_batch: packed operands and the workspace must be 16-byte aligned");
     const int S = M * E;
     uint8_t* w8 = static_cast<uint8_t*>(ws);
-    BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
-                w8, w8 + (size_t)S * (Mi / 2), y};
-    hipStream_t st = mxh::as_stream(stream);
-    hipLaunchKernelGGL(batch_gateup_kernel, dim3(Mi / 32, S), dim3(256), 0, st, a);
-    const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
+    const BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
+                      w8, w8 + (size_t)S * (Mi / 2), y};
+    return launch_batch(a, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_decode_batch_noalloc(const uint8_t* xq, const uint8_t* xs, const int32_t* ids,
+                                              const float* w, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                              const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                              const uint8_t* down_ws, int n_experts, int M, int E, int H, int Mi,
+                                              float* y, void* stream) {
+    const int rc = check_batch_args(xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M,
+                                    E, H, Mi, y);
     if (rc != MXFP4_OK) return rc;
-    hipLaunchKernelGGL(batch_down_kernel, dim3(H / 16), dim3(64 * kDownWaves), 0, st, a);
-    return mxh::launch_status("moe_decode_batch (down)");
+    MXH_REQUIRE(Mi <= kNoAllocMaxMi, "moe_decode_batch_noalloc: Mi=%d exceeds the %d of its fixed scratch", Mi,
+                kNoAllocMaxMi);
+    MXH_REQUIRE(mxfp4_moe_decode_batch_workspace_size(M, E, Mi) <= kScratchBytes,
+                "moe_decode_batch_noalloc: %zu bytes of h exceed the %zu-byte scratch",
+                mxfp4_moe_decode_batch_workspace_size(M, E, Mi), kScratchBytes);
+    void* sp = nullptr;
+    const int rs = scratch_on_current_device(&sp);
+    if (rs != MXFP4_OK) return rs;
+    // Every h row the down kernel reads is written by the gate/up kernel of the
+    // same call, so nothing in the scratch has to start at zero.
+    const int S = M * E;
+    uint8_t* w8 = static_cast<uint8_t*>(sp);
+    const BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
+                      w8, w8 + (size_t)S * (Mi / 2), y};
+    return launch_batch(a, mxh::as_stream(stream));
 }
