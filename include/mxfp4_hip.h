@@ -256,13 +256,16 @@ int mxfp4_moe_decode_layer_routed(const void* x, const float* logits, int norm, 
  *   workspace    mxfp4_decode_stack_workspace_size(E, H, Mi) bytes, 256-byte
  *                aligned, initialised once by mxfp4_decode_stack_reset; it
  *                needs no reset between launches or graph replays.
- * The launch's E*Mi/32 + H/32 workgroups (256 at E=8, H=2048, Mi=768) run
- * one per CU and must all be resident at once: the call fails with
- * MXFP4_EINVAL when the GPU has fewer CUs, and no other kernel may occupy
- * the GPU meanwhile.  Every internal wait is bounded and an expired one is
- * reported by mxfp4_decode_stack_status.  Results are bit-identical to
- * n_layers chained mxfp4_moe_decode_layer launches.  Other limits as
- * mxfp4_moe_decode_layer.
+ * The launch's 256 workgroups run one per CU (slot s of the routing on XCD
+ * s, the XCD's 32 CUs in two sets that compute alternate layers) and must
+ * all be resident at once: the call fails with MXFP4_EINVAL unless the GPU
+ * has 256 CUs (MI355X: 8 XCDs of 32), and no other kernel may occupy the GPU
+ * meanwhile.  Every internal wait is bounded and an expired one is reported
+ * by mxfp4_decode_stack_status.  Results are bit-identical to n_layers
+ * chained mxfp4_moe_decode_layer launches.  Limits: E <= 8, H a multiple of
+ * 512 up to 2048, Mi a multiple of 32 up to 1024.  The workspace holds a
+ * 2 KB header and two buffers of 8-byte words, 8 * (2*Mi + 2*H) each (sizes
+ * rounded up to 32 words).
  */
 size_t mxfp4_decode_stack_workspace_size(int E, int H, int Mi);
 int mxfp4_decode_stack_reset(void* workspace, int E, int H, int Mi, void* stream);

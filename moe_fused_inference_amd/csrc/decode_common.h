@@ -88,6 +88,41 @@ __device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint3
     }
 }
 
+// max over the 8 lanes of a half row: the quad maximum, then the other quad's
+// through the half-row mirror (DPP)
+__device__ __forceinline__ float oct_max(float v) {
+    v = quad_max(v);
+    return fmaxf(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
+}
+
+// Splits 4 consecutive values of a 32-block (8 lanes per block, aligned to 8
+// lanes) into kTerms E4M3 terms, with split8's arithmetic: word4[t] receives
+// the 4 E4M3 bytes of term t and codes (byte t) the term's E8M0 scale code.
+__device__ __forceinline__ void split4(float v[4], uint32_t word4[kTerms], uint32_t& codes) {
+    codes = 0;
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+        float am = fmaxf(fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1])),
+                         fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
+        am = oct_max(am);
+        const uint32_t code = e4m3_block_code(am);
+        const float sc = e8m0_value(code);
+        mx::v2s p = {0, 0};
+        p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v[0], v[1], sc, false);
+        p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v[2], v[3], sc, true);
+        const uint32_t word = ((uint32_t)(uint16_t)p[0]) | ((uint32_t)(uint16_t)p[1] << 16);
+        typedef float v2f __attribute__((ext_vector_type(2)));
+        const v2f d0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, sc, false);
+        const v2f d1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp8(word, sc, true);
+        v[0] -= d0[0];
+        v[1] -= d0[1];
+        v[2] -= d1[0];
+        v[3] -= d1[1];
+        word4[t] = word;
+        codes |= code << (8 * t);
+    }
+}
+
 // max over lanes 0..15 and over 16..31 (each row of 16 lanes), then of both
 // rows, for a value held by lanes 0..31: DPP within rows, readlane across.
 __device__ __forceinline__ float max32(float v) {

@@ -6,53 +6,62 @@
 //     x_{l+1} = bf16(x_l + bf16(y_l))
 // -- the reference's per-layer MoE step (runtime/model_runner_v2.py:185-208,
 // kernels src/ext/mxfp4_decode.cu:24-50,177-299) applied layer after layer,
-// on un-quantized bf16 activations in fp32 like the one-layer kernel
-// (decode_layer.hip).  The routing of every layer (ids, w) is an input, so
-// the kernel can fetch layer l+1's expert weights while layer l is still
-// being computed: the launch streams weights at HBM rate instead of paying a
-// launch and a cold weight burst per layer.
+// on un-quantized bf16 activations in fp32 with exactly the arithmetic of the
+// one-layer kernel (decode_layer.hip), so the results equal chained one-layer
+// launches bit for bit.  The routing of every layer (ids, w) is an input, so
+// layer l+1's expert weights stream while layer l is still being computed.
 //
-// Workgroups keep one role for the whole launch (the one-layer kernel's
-// split):
-//   [0, nA)        gate/up tile (slot s, 32 intermediate rows) of every layer:
-//                  wait for x_l, h = silu(g)*u, publish h_l (E4M3 terms);
-//   [nA, nA+nB)    down + combine, 32 output columns of every layer: wait for
-//                  h_l, y, x_{l+1} = bf16(x_l + bf16(y)), publish x_{l+1}.
-// A gate/up workgroup issues layer l+1's weight loads right after its layer-l
-// MFMAs, a down workgroup right after its layer-l MFMAs, so both weight
-// streams run under the other phase and the hand-offs.  With STRICT the loads
-// of layer l are issued only once x_l is complete (down workgroups then wait
-// for x_l as well): the timing of a model whose routing depends on x_l.
+// Placement.  MI355X has 8 XCDs of 32 CUs, each XCD with its own L2, and
+// deals the workgroups of a 256-workgroup grid to the XCDs round-robin, 32
+// each; a workgroup takes a CU.  Slot s of the top-E routing lives on XCD s
+// (read from the XCC id register).  The XCD's workgroups j = blockIdx.x / 8
+// form two sets by the parity of j, and set p computes the layers l with
+// l % 2 == p: while one set runs a layer's hand-offs the other set streams
+// the weights of its next layer into registers.  A poll from a CU comes back
+// only after the loads that CU already has in flight (measured: a same-XCD
+// hand-off takes ~0.23 us on a CU with nothing in flight and ~3 us behind a
+// layer's worth of prefetch, while streaming on other CUs costs it nothing),
+// so a workgroup issues the loads of its next layer (l+2) only after the last
+// poll of layer l.  Within its set, workgroup jj = j / 2 (0..15) takes the
+// gate/up row tiles jj, jj+16, jj+32, .. of the slot's 2*Mi/16 tiles (gate
+// tiles first) and the down rows (output columns) [jj*H/16, (jj+1)*H/16).
 //
-// Hand-offs.  As in the one-layer kernel a published 32-bit word is its own
-// flag (kEmpty = not yet): h words carry three E4M3 term bytes (+ the terms'
-// codes in byte 3 of a record's first three words), x words carry the bf16
-// value in their low half (high half 0, so never kEmpty).  Producers store with
-// agent-scope atomic stores; consumers poll with agent-scope loads.  Each
-// value has three buffers, used round robin by a per-workgroup layer count
-// ("memo", read at entry, + L stored at exit; all workgroups agree on it):
-// layer count c publishes into buffer c%3 and then empties its words of
-// buffer (c-1)%3, which is published into again at layer c+2.  That is safe:
-// the readers of (c-1)%3 were the consumers of layer c-1, which the producer
-// has already waited for (a gate/up workgroup at layer c has all of x_c,
-// which the down workgroups publish after reading h_{c-1}; a down workgroup
-// at layer c has all of h_c, which the gate/up workgroups publish after
-// reading x_c).  Before each publish a producer waits for its earlier stores
-// (s_waitcnt vmcnt(0)), so the empties of layer c are visible before anything
-// of layer c+1 is, hence before any consumer polls (c+2)%3 -- a layer after
-// they were issued, so the wait is normally free.  No reset is needed between
-// launches.
+// One layer, per workgroup; each of its four waves owns a quarter of the
+// gate/up K range and a share of every other step:
+//   1. x_l: poll this XCD's copy of x_l (bf16, published by the other set in
+//      the previous layer) for the wave's K quarter; E4M3 terms into LDS;
+//   2. gate/up MFMAs; the four waves' partial sums meet in LDS; publish the
+//      raw g or u values of the workgroup's tiles (fp32);
+//   3. poll the slot's g/u for the wave's share of the 32-blocks of h;
+//      h = silu(g) * u and its E4M3 terms into LDS (barrier: all of h);
+//   4. down MFMAs on the wave's column tiles; publish y_s per column (fp32);
+//   5. poll y_t of every slot t for the wave's share of the workgroup's
+//      columns; y = sum_t w_t y_t (the one-layer kernel's order), x_{l+1} =
+//      bf16(x_l + bf16(y)); publish x_{l+1} for those columns into this XCD's
+//      copy;
+//   6. barrier, then issue the weight loads of layer l+2.
+// Every XCD computes all of x_{l+1}, so the x and g/u hand-offs stay inside
+// one L2 (plain stores, agent-scope loads that hit the local L2) and only the
+// per-slot y crosses XCDs (fan-in of 8 producers per consumer).  With STRICT
+// a layer's loads are issued only once the wave has x_l: the timing of
+// routing that depends on x.
 //
-// Co-residency.  The grid (E*Mi/32 + H/32 = 256 workgroups at the headline
-// shape) must be resident at once: every workgroup waits on others of every
-// layer.  Each workgroup takes more than half of a CU's LDS, so it has a CU
-// to itself, and the host refuses a grid larger than the CU count.  (With two
-// workgroups on a CU -- a gate/up and a down workgroup -- the down
-// workgroup's polls were seen to miss a published word for up to a second
-// while its CU neighbour was polling, which stalled the whole chain.)  Every
-// wait is bounded (kSpinLimit polls); on expiry, or when another workgroup
-// has set the error flag, a thread stops waiting, the results are garbage and
-// the flag stays set until the workspace is reset.
+// Hand-off words.  Every published value travels in a 64-bit word (value,
+// tag), written and read as one single-copy-atomic access; the tag is the
+// layer count (a memo per (slot, j) in the workspace, read at entry, + L at
+// exit; all workgroups agree on it), never 0.  A consumer waits until every
+// word carries the expected tag, so no buffer is ever emptied and no store
+// completion is ever waited for.  Two buffers per kind, used by alternate
+// layers, suffice: a producer writes layer c+2 into the buffer of layer c
+// only after it has (transitively) seen every consumer of layer c finish.
+//
+// Co-residency.  The 256 workgroups must be resident at once (each waits on
+// others of every layer): each takes more than half of a CU's LDS, so a CU
+// holds one, and the host refuses the launch unless the occupancy query
+// allows the whole grid on a 256-CU device.  Every wait is bounded
+// (kSpinLimit polls); on expiry, or when another workgroup has set the error
+// flag, a wave stops waiting, the results are garbage and the flag stays set
+// until the workspace is reset.
 #include "decode_common.h"
 #include "mx_host.h"
 
@@ -60,13 +69,22 @@ namespace {
 
 using namespace dl;
 
+constexpr int kXcds = 8;              // XCDs = slots
+constexpr int kPerXcd = 32;           // CUs (workgroups) per XCD
+constexpr int kPerSet = kPerXcd / 2;  // workgroups per set (two sets, alternate layers)
+constexpr int kGrid = kXcds * kPerXcd;
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kMaxNT = 8;             // gate/up tiles per workgroup (Mi <= 1024)
+constexpr int kLdsLayers = 128;       // layers whose routing and weight pointers are staged in LDS
+constexpr int kRecBytes = 112;        // LDS record of 32 values: 3 x 32 term bytes, codes at 96..98
+
 // workspace layout (bytes)
 constexpr int kCfgOff = 0;            // int32 config word written by reset
 constexpr int kErrOff = 256;          // int32 error flag
 constexpr int kMemoOff = 1024;        // int32 layer count per workgroup
-constexpr int kMaxWg = 768;
-constexpr int kBufOff = kMemoOff + 4 * kMaxWg;   // h buffers, then x buffers (uint32 words)
-constexpr int kNBuf = 3;              // buffers per value, used round robin by layer count
+constexpr int kBufOff = kMemoOff + 4 * kGrid;
+constexpr int kNBuf = 2;              // buffers per kind, alternate layers
 
 struct StackLayer {
     const uint8_t* wp[3];   // gate, up, down packed data of the layer's experts (stacked)
@@ -85,39 +103,73 @@ struct StackArgs {
     int64_t wp_stride_dn, ws_stride_dn;   // bytes between experts (down)
     int n_layers, n_experts, E, H, Mi;
     int cfg;                    // expected workspace config word
-    int hwords;                 // words between consecutive h buffers
-    int xwords;                 // words between consecutive x buffers
+    int gu_q, part_q, x_q;      // 64-bit words per XCD (g/u, x) / per slot (y) of one buffer
+    int64_t buf_q;              // 64-bit words of one buffer (all kinds, all XCDs)
     uint8_t* ws;
 };
 
 __host__ __device__ constexpr int stack_cfg(int E, int H, int Mi) {
-    return 0x5B000000 | (E << 16) | ((H / 512) << 12) | (Mi / 32);
+    return 0x5D000000 | (E << 16) | ((H / 512) << 12) | (Mi / 32);
 }
 
-union Smem {
-    struct {                                       // gate/up workgroups
-        uint4 zero[2];
-        uint8_t x8[kTerms][2048];
-        uint8_t xsc[kTerms][64];
-        float red[4][4][16];
-    } a;
-    struct {                                       // down workgroups
-        uint4 zero[2];
-        uint32_t code127[4];
-        uint8_t h8[kMaxE * kTerms * 1024];
-        uint32_t hsc[kMaxE * 32];
-        float red[4][32];
-    } b;
-    uint8_t one_per_cu[84 * 1024];                 // more than half of a CU's LDS: one workgroup per CU
+// 64-bit words of one buffer: g/u (2*Mi per XCD), y (H per slot), x (H per XCD)
+__host__ __device__ constexpr int gu_words(int Mi) { return ((2 * Mi + 31) / 32) * 32; }
+__host__ __device__ constexpr int part_words(int H) { return ((H + 31) / 32) * 32; }
+__host__ __device__ constexpr int x_words(int H) { return ((H + 31) / 32) * 32; }
+__host__ __device__ constexpr int64_t buf_words(int H, int Mi) {
+    return (int64_t)kXcds * (gu_words(Mi) + part_words(H) + x_words(H));
+}
+
+struct Route {
+    int32_t ids[kLdsLayers];            // this slot's expert per layer
+    float w[kLdsLayers][kMaxE];         // every slot's combine weight per layer
+    const uint8_t* ptr[kLdsLayers][6];  // the layer's six stacked weight pointers
 };
 
-__device__ __forceinline__ void set_error(const StackArgs& a) {
-    __hip_atomic_store(reinterpret_cast<int*>(a.ws + kErrOff), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+union Smem {
+    struct {
+        uint4 zero[2];
+        uint32_t code127[4];
+        uint8_t xr[64 * kRecBytes];             // x_l in E4M3 terms, 32-value records (H/32 <= 64)
+        uint8_t hr[32 * kRecBytes];             // h_l in E4M3 terms (Mi/32 <= 32)
+        uint16_t xb[2048];                      // x_l in bf16 (the combine's residual)
+        float hs[1024];                         // h_l (fp32), split source
+        float red[kWaves][kMaxNT][16];          // gate/up partial sums: wave x tile x row
+        Route rt;
+    } s;
+    uint8_t one_per_cu[84 * 1024];              // more than half of a CU's LDS: one workgroup per CU
+};
+
+// Error flag bits: a bounded wait expired, the workspace belongs to another shape.
+constexpr int kErrWait = 1, kErrCfg = 2;
+
+__device__ __forceinline__ void set_error(const StackArgs& a, int bits = kErrWait) {
+    __hip_atomic_fetch_or(reinterpret_cast<int*>(a.ws + kErrOff), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ bool error_set(const StackArgs& a) {
     return __hip_atomic_load(reinterpret_cast<const int*>(a.ws + kErrOff), __ATOMIC_RELAXED,
                              __HIP_MEMORY_SCOPE_AGENT) != 0;
+}
+
+// A wave-uniform pointer held in SGPRs (buffer descriptors must be uniform).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+    const uint64_t v = (uint64_t)(uintptr_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)hi << 32) | lo));
+}
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const uint8_t* p, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(uniform_ptr(p)), (short)0, bytes, 0x00020000);
+}
+
+// Loads of the read-only routing arrays and layer table through the
+// constant address space (scalar loads) for layers past the LDS copy.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p, int i) {
+    typedef const __attribute__((address_space(4))) T* cptr;
+    return ((cptr)(uintptr_t)p)[i];
 }
 
 // Workgroup barrier for LDS only: waits for this wave's LDS operations, not
@@ -129,27 +181,45 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
-// Waits for every outstanding global memory operation of this wave: makes
-// the agent-scope stores issued so far visible before any later store.
-__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Publish / poll of (value, tag) words.  Publishing to this XCD's L2 only
+// (consumers on the same XCD) is a plain store; to the device (consumers on
+// other XCDs) an agent-scope store, written through to the coherence point.
+// Polls are agent-scope loads: they see a line dirty in the local L2 and
+// fetch anything else from the coherence point.
+__device__ __forceinline__ void put_local(uint64_t* p, uint32_t value, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void put_device(uint64_t* p, uint32_t value, uint32_t tag) {
+    __hip_atomic_store(p, ((uint64_t)tag << 32) | value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// A whole 64-bit word (lo, hi) to this XCD's L2.
+__device__ __forceinline__ void put_word(uint64_t* p, uint32_t lo, uint32_t hi) {
+    __hip_atomic_store(p, ((uint64_t)hi << 32) | lo, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
 
-// Bounded poll of N 16-byte groups at byte offsets off[i] of buffer rs until
-// none of their words is kEmpty; every round reloads all groups with the
-// agent-scope cache policy (one round trip per check: a one-word probe
-// before the full reload would cost a second one).  `live` false (an earlier
-// wait failed): one load, no wait.  Returns false on expiry or when the error
-// flag is set.
-template <int N>
-__device__ __forceinline__ bool poll_groups(const StackArgs& a, __amdgpu_buffer_rsrc_t rs,
-                                            const int (&off)[N], v4u (&v)[N], bool live) {
+// The 16-bit tag of a layer count's x words: 1..65535, never 0 (the reset
+// value); two layer counts two apart (the previous use of a buffer) differ.
+__device__ __forceinline__ uint32_t tag16(uint32_t tag) { return tag % 65535u + 1u; }
+
+typedef uint32_t v2u __attribute__((ext_vector_type(2)));
+
+// Bounded poll of N 64-bit words per lane -- byte offsets off[i] of the region
+// of descriptor rs, lanes with ok[i] false take nothing -- until each carries
+// `tag` in bits 32 + TSH and up; w[i] = the words.  Agent-scope 8-byte loads
+// (single-copy atomic: value and tag always come from the same store).  `live`
+// false (an earlier wait failed): one load, no wait.  Returns false on expiry
+// or when the error flag is set.
+template <int N, int TSH = 0>
+__device__ __forceinline__ bool poll_words(const StackArgs& a, __amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[N],
+                                           const bool (&ok)[N], uint32_t tag, v2u (&w)[N], bool live) {
     int spins = 0;
     while (true) {
 #pragma unroll
-        for (int i = 0; i < N; ++i) v[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], 0, 16);
-        if (!live) return false;
+        for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_raw_buffer_load_b64(rs, off[i], 0, 16);
         bool pending = false;
 #pragma unroll
-        for (int i = 0; i < N; ++i) pending |= (v[i].x == kEmpty) | (v[i].y == kEmpty) | (v[i].z == kEmpty) | (v[i].w == kEmpty);
+        for (int i = 0; i < N; ++i) pending |= ok[i] && (w[i].y >> TSH) != tag;
+        if (!live) return false;
         if (__builtin_amdgcn_ballot_w64(pending) == 0) return true;   // the wave polls as one
         if (++spins >= kSpinLimit || ((spins & 255) == 0 && error_set(a))) return false;
         __builtin_amdgcn_s_sleep(1);
@@ -157,392 +227,470 @@ __device__ __forceinline__ bool poll_groups(const StackArgs& a, __amdgpu_buffer_
     }
 }
 
-// x_l (H <= 2048 bf16) from the x buffer: thread t waits for words 8t..8t+7
-// and returns their values packed as 8 bf16 (threads past H read zeros).
-__device__ __forceinline__ bool wait_x(const StackArgs& a, const uint32_t* xb, uint4& xq, bool live) {
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(xb), (short)0,
-                                                                        a.H * 4, 0x00020000);
-    const int t8 = min(8 * (int)threadIdx.x, a.H - 8);   // threads past H re-poll the last group
-    const int off[2] = {t8 * 4, t8 * 4 + 16};
-    v4u v[2];
-    const bool ok = poll_groups<2>(a, rs, off, v, live);
-    const bool in = 8 * (int)threadIdx.x < a.H;
-    xq.x = in ? (v[0].x & 0xFFFFu) | (v[0].y << 16) : 0u;
-    xq.y = in ? (v[0].z & 0xFFFFu) | (v[0].w << 16) : 0u;
-    xq.z = in ? (v[1].x & 0xFFFFu) | (v[1].y << 16) : 0u;
-    xq.w = in ? (v[1].z & 0xFFFFu) | (v[1].w << 16) : 0u;
-    return ok;
+// poll_words for (value, 32-bit tag) words: v[i] = the values
+template <int N>
+__device__ __forceinline__ bool poll_tagged(const StackArgs& a, __amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[N],
+                                            const bool (&ok)[N], uint32_t tag, uint32_t (&v)[N], bool live) {
+    v2u w[N];
+    const bool r = poll_words<N>(a, rs, off, ok, tag, w, live);
+#pragma unroll
+    for (int i = 0; i < N; ++i) v[i] = w[i].x;
+    return r;
 }
 
-template <bool STRICT, int MS>
-__global__ __launch_bounds__(256, 1) void decode_stack_kernel(StackArgs a) {
-    __shared__ __align__(16) Smem sm;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t region(const uint64_t* p, int words) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(p), (short)0, words * 8, 0x00020000);
+}
+
+// Splits 8 consecutive values (a quarter of a 32-block; the 4 lanes of a quad
+// hold one block) into the LDS record layout: term t's bytes at
+// rec + 32t + `pos`, the block's codes at rec + 96 + t (written by the quad's
+// first lane).  Same arithmetic as split8 everywhere else.
+__device__ __forceinline__ void split8_to_record(float v[8], uint8_t* rec, int pos) {
+    uint64_t w8[kTerms];
+    uint32_t codes;
+    split8(v, w8, codes);
+#pragma unroll
+    for (int t = 0; t < kTerms; ++t) {
+        *reinterpret_cast<uint64_t*>(rec + 32 * t + pos) = w8[t];
+        if ((threadIdx.x & 3) == 0) rec[96 + t] = (uint8_t)(codes >> (8 * t));
+    }
+}
+
+__device__ __forceinline__ uint32_t xcc_id() {
+    uint32_t v;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 16)" : "=s"(v));
+    return v & 0xFu;
+}
+
+// NT: gate/up tiles per workgroup (Mi/128 rounded up to even); MS: down K
+// steps bound; KB4: Mi/32 a multiple of 4 (down scale bytes in aligned dwords).
+template <bool STRICT, int MS, bool KB4, int NT>
+__global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) {
+    __shared__ __align__(16) Smem smu;
+    auto& sm = smu.s;
 
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int cw = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave 0..3
     const int r = lane & 15;
     const int g = lane >> 4;
     const int rr = r < kTerms ? r : 0;
-    const int nblk_mi = a.Mi >> 5;
-    const int nA = a.E * nblk_mi;
     const int bid = blockIdx.x;
+    // The dispatcher deals workgroups to the 8 XCDs round-robin, but the XCD
+    // of workgroup 0 varies between dispatches (it follows the previous
+    // dispatch in a graph replay), so the slot is the XCD this workgroup runs
+    // on, and bid / 8 numbers the 32 workgroups of each XCD.  (Were the deal
+    // not a rotation, a (slot, j) pair would go missing and the bounded waits
+    // on its outputs would set the error flag.)
+    const int s = (int)__builtin_amdgcn_readfirstlane(xcc_id());   // slot = XCD
+    const int j = bid / kXcds;                 // workgroup within the XCD
+    const int par = j & 1;                     // its set: layers l with l % 2 == par
+    const int jj = j >> 1;                     // workgroup within the set
     const int L = a.n_layers;
     const int E = a.E;
     const int H = a.H;
-    int* memo = reinterpret_cast<int*>(a.ws + kMemoOff) + bid;
-    const int c0 = __builtin_amdgcn_readfirstlane(*memo);   // uniform: buffer selects stay scalar
+    const int Mi = a.Mi;
+    if (s >= E) return;                        // no slot on this XCD
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoOff) + s * kPerXcd + j;
+    const uint32_t c0 = (uint32_t)__builtin_amdgcn_readfirstlane(*memo);
     const bool cfg_ok = *reinterpret_cast<const int*>(a.ws + kCfgOff) == a.cfg;
     if (!cfg_ok) {
-        if (threadIdx.x == 0) set_error(a);
+        if (threadIdx.x == 0) set_error(a, kErrCfg);
         return;
     }
-    uint32_t* hbuf = reinterpret_cast<uint32_t*>(a.ws + kBufOff);
-    uint32_t* xbuf = hbuf + kNBuf * a.hwords;
-    bool live = true;   // this thread's waits have all succeeded
+    uint64_t* bufs = reinterpret_cast<uint64_t*>(a.ws + kBufOff);
+    // kind bases within buffer b: g/u of XCD s, y of slot t, x of XCD s
+    auto gu_base = [&](int b) { return bufs + b * a.buf_q + (int64_t)s * a.gu_q; };
+    auto part_base = [&](int b, int t) { return bufs + b * a.buf_q + (int64_t)kXcds * a.gu_q + (int64_t)t * a.part_q; };
+    auto x_base = [&](int b) {
+        return bufs + b * a.buf_q + (int64_t)kXcds * (a.gu_q + a.part_q) + (int64_t)s * a.x_q;
+    };
 
-    if (bid < nA) {
-        // ================================================= gate / up
-        const int s = bid % E;
-        const int jb = bid / E;
-        const int j0 = jb * 32;
-        const int hb = H >> 5;
-        const int bpw = hb >> 2;
-        const int sa = bpw >> 2;
-        const int k0 = threadIdx.x * 8;
-        const int blk0 = bpw * wave + sa * g;
-        if (threadIdx.x < 2) sm.a.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
+    // routing and weight pointers of the first kLdsLayers layers
+    {
+        const int nl = min(L, kLdsLayers);
+        for (int i = threadIdx.x; i < nl * kMaxE; i += kThreads) {
+            const int l = i / kMaxE, k = i % kMaxE;
+            sm.rt.w[l][k] = k < E ? a.w[l * E + k] : 0.0f;
+        }
+        for (int i = threadIdx.x; i < nl; i += kThreads) sm.rt.ids[i] = a.ids[i * E + s];
+        for (int i = threadIdx.x; i < nl * 6; i += kThreads)
+            sm.rt.ptr[i / 6][i % 6] = reinterpret_cast<const uint8_t* const*>(a.layers)[i];
+        if (threadIdx.x < 2) sm.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
+        if (threadIdx.x == 2) sm.code127[0] = 0x7F7F7F7Fu;
+        __syncthreads();
+    }
+    auto route_id = [&](int l) -> int {
+        int e = __builtin_amdgcn_readfirstlane(l < kLdsLayers ? sm.rt.ids[l] : ld_const(a.ids, l * E + s));
+        return e < 0 ? 0 : (e >= a.n_experts ? a.n_experts - 1 : e);   // memory safety only
+    };
+    auto route_w = [&](int l, int t) -> float { return l < kLdsLayers ? sm.rt.w[l][t] : ld_const(a.w, l * E + t); };
+    auto route_ptr = [&](int l, int k) -> const uint8_t* {
+        return l < kLdsLayers ? sm.rt.ptr[l][k]
+                              : ld_const(reinterpret_cast<const uint8_t* const*>(a.layers), 6 * l + k);
+    };
 
-        uint4 bq[4][4];
-        uint32_t bsc4[4];
-        auto load_w = [&](int l) {
-            int e = __builtin_amdgcn_readfirstlane(a.ids[l * E + s]);
-            e = e < 0 ? 0 : (e >= a.n_experts ? a.n_experts - 1 : e);   // memory safety only
-            const StackLayer* ly = a.layers + l;
-            const uint8_t* gw = ly->wp[0] + (int64_t)e * a.wp_stride_gu;
-            const uint8_t* gs = ly->ws[0] + (int64_t)e * a.ws_stride_gu;
-            const uint8_t* uw = ly->wp[1] + (int64_t)e * a.wp_stride_gu;
-            const uint8_t* us = ly->ws[1] + (int64_t)e * a.ws_stride_gu;
+    const int hb = H >> 5;                     // 32-blocks along H
+    const int ntile = Mi >> 3;                 // gate + up tiles of 16 rows (2*Mi/16)
+    const int ncol = H >> 4;                   // down and combine columns per workgroup
+    const int c0d = jj * ncol;
+    const int nct = ncol >> 4;                 // down column tiles per workgroup (1..8)
+    const int kb = Mi >> 5;                    // 32-blocks along Mi
+    const int steps = (kb + 3) >> 2;           // down K steps
+
+    // ---- gate/up weights: K quarter cw (blocks bpw*cw ..) of tiles jj + 16m.
+    // Offsets of tiles past the last are out of the descriptor's range: their
+    // loads return zeros without touching memory.
+    constexpr uint32_t kNone = 0x80000000u;
+    const int bpw = hb >> 2;
+    const int sa = bpw >> 2;
+    const int blk0 = bpw * cw + sa * g;
+    uint4 bq[NT][4];
+    uint32_t bslo[NT], bshi[NT];
+    uint32_t woff[NT], soff[NT];
+    bool tup[NT];
 #pragma unroll
-            for (int G = 0; G < 4; ++G) {
-                const int row = j0 + 16 * (G & 1) + r;
-                const uint8_t* wrow = ((G < 2) ? gw : uw) + (int64_t)row * (H >> 1);
-                const uint8_t* srow = ((G < 2) ? gs : us) + (int64_t)row * hb;
+    for (int m = 0; m < NT; ++m) {
+        const int t = jj + kPerSet * m;
+        const bool ok = t < ntile;
+        tup[m] = t >= (ntile >> 1);
+        const int row = 16 * (tup[m] ? t - (ntile >> 1) : t) + r;
+        woff[m] = ok ? (uint32_t)(row * (H >> 1) + blk0 * 16) : kNone;
+        soff[m] = ok ? (uint32_t)(row * hb + (blk0 & ~3)) : kNone;
+    }
+    const uint32_t shi = (uint32_t)(min((blk0 & ~3) + 4, hb - 4) - (blk0 & ~3));
+    // valid = false: a zero-extent descriptor, so the loads return zeros
+    // without touching memory
+    auto load_gu = [&](int l, bool valid) {
+        const int e = route_id(l);
+        const int wbytes = valid ? Mi * (H >> 1) : 0, sbytes = valid ? Mi * hb : 0;
+        const __amdgpu_buffer_rsrc_t rw[2] = {rsrc(route_ptr(l, 0) + (int64_t)e * a.wp_stride_gu, wbytes),
+                                              rsrc(route_ptr(l, 1) + (int64_t)e * a.wp_stride_gu, wbytes)};
+        const __amdgpu_buffer_rsrc_t rs[2] = {rsrc(route_ptr(l, 3) + (int64_t)e * a.ws_stride_gu, sbytes),
+                                              rsrc(route_ptr(l, 4) + (int64_t)e * a.ws_stride_gu, sbytes)};
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int blk = min(blk0 + i, hb - 1);
-                    bq[G][i] = ld_sel(reinterpret_cast<const uint4*>(wrow + blk * 16), i < sa, make_uint4(0, 0, 0, 0));
-                }
-                const int d0 = blk0 & ~3;
-                const uint32_t lo = *reinterpret_cast<const uint32_t*>(srow + d0);
-                const uint32_t hi = *reinterpret_cast<const uint32_t*>(srow + min(d0 + 4, hb - 4));
-                bsc4[G] = (uint32_t)((((uint64_t)hi << 32) | lo) >> (8 * (blk0 & 3)));
-            }
-        };
-        if (!STRICT) load_w(0);
-
-        const int64_t w_off = ((int64_t)s * nblk_mi + jb) * kRecWords + (lane & 31);
-        for (int l = 0; l < L; ++l) {
-            const int b = (c0 + l) % kNBuf;             // this layer's buffer
-            const int bprev = (b + kNBuf - 1) % kNBuf;  // the previous layer's
-            uint4 xq = make_uint4(0, 0, 0, 0);
-            if (l == 0) {
-                if (k0 < H) xq = *reinterpret_cast<const uint4*>(a.x0 + k0);
-            } else {
-                live = wait_x(a, xbuf + bprev * a.xwords, xq, live);
-            }
-            if (STRICT) load_w(l);
-
-            // x_l -> three E4M3 terms in LDS
-            if (k0 < H) {
-                float v[8];
-                const uint32_t w4[4] = {xq.x, xq.y, xq.z, xq.w};
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v[2 * i] = mx::bf16_to_f32((uint16_t)(w4[i] & 0xFFFFu));
-                    v[2 * i + 1] = mx::bf16_to_f32((uint16_t)(w4[i] >> 16));
-                }
-                uint64_t w8[kTerms];
-                uint32_t codes;
-                split8(v, w8, codes);
-#pragma unroll
-                for (int t = 0; t < kTerms; ++t) {
-                    *reinterpret_cast<uint64_t*>(&sm.a.x8[t][k0]) = w8[t];
-                    if ((threadIdx.x & 3) == 0) sm.a.xsc[t][k0 >> 5] = (uint8_t)(codes >> (8 * t));
-                }
-            }
-            lds_barrier();
-
-            mx::v8i av[4];
-            uint32_t asc[4];
+        for (int m = 0; m < NT; ++m) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int base = bpw * wave + min(i, sa - 1);
-                const bool ok = r < kTerms && i < sa;
-                const uint4* plo = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (g >> 1)) * 32 + 16 * (g & 1)])
-                                      : &sm.a.zero[0];
-                const uint4* phi = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (2 + (g >> 1))) * 32 + 16 * (g & 1)])
-                                      : &sm.a.zero[1];
-                av[i] = cat8(*plo, *phi);
-                const uint32_t c = sm.a.xsc[rr][base + sa * g];
-                asc[i] = ok ? c : 127u;
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw[tup[m]], woff[m] + 16 * min(i, sa - 1), 0, 0);
+                bq[m][i] = make_uint4(v.x, v.y, v.z, v.w);
             }
-            mx::v4f acc[4];
-#pragma unroll
-            for (int G = 0; G < 4; ++G) acc[G] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int G = 0; G < 4; ++G)
-                    acc[G] = mx::mfma16_fp8a_fp4b(av[i], bq[G][i], acc[G], asc[i], (bsc4[G] >> (8 * i)) & 0xFFu);
-#pragma unroll
-            for (int G = 0; G < 4; ++G) mx::pin(acc[G]);
-            if (lane < 16) {
-#pragma unroll
-                for (int G = 0; G < 4; ++G) sm.a.red[wave][G][lane] = acc[G][0] + acc[G][1] + acc[G][2];
-            }
-            lds_barrier();
-            if (wave == 0) {
-                const int j = lane & 31;
-                float gsum = 0.f, usum = 0.f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    gsum += sm.a.red[w][j >> 4][j & 15];
-                    usum += sm.a.red[w][2 + (j >> 4)][j & 15];
-                }
-                uint32_t codes;
-                const uint32_t bytes = split32(mx::silu_mul(gsum, usum), codes);
-                const uint32_t word = bytes | (j < kTerms ? ((codes >> (8 * j)) & 0xFFu) << 24 : 0u);
-                wait_stores();   // the previous layer's empty-stores are visible before this publish
-                if (lane < 32) {
-                    __hip_atomic_store(hbuf + b * a.hwords + w_off, word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                    // empty this record in the previous layer's buffer (written
-                    // again two layers on; its readers, the down workgroups of
-                    // the previous layer, are done: x_l is complete)
-                    __hip_atomic_store(hbuf + bprev * a.hwords + w_off, kEmpty, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-                }
-            }
-            // The next layer's weights stream under the down phase.  Issued
-            // after the publish: a burst of loads stalls the issuing wave
-            // once the CU's memory queue is full.
-            if (!STRICT && l + 1 < L) load_w(l + 1);
+            bslo[m] = __builtin_amdgcn_raw_buffer_load_b32(rs[tup[m]], soff[m], 0, 0);
+            bshi[m] = __builtin_amdgcn_raw_buffer_load_b32(rs[tup[m]], soff[m] + shi, 0, 0);
         }
-        if (!live) set_error(a);
-        if (threadIdx.x == 0) *memo = c0 + L;
-        return;
+    };
+    // ---- down weights: column tiles cw and cw + 4 (16 columns each) of the
+    // workgroup's columns
+    const int sb0 = (g * steps) & ~3;
+    const int ilast = min(steps, kb - g * steps) - 1;   // last in-row step of this lane group (may be < 0)
+    bool dok[2];
+    uint32_t woffd[2], soffd[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int ct = cw + 4 * k;
+        dok[k] = ct < nct;
+        const int drow = c0d + 16 * ct + r;
+        woffd[k] = dok[k] ? (uint32_t)(drow * (Mi >> 1) + g * steps * 16) : kNone;
+        soffd[k] = dok[k] ? (uint32_t)(drow * kb) : kNone;
     }
-
-    // ===================================================== down + combine
-    // 32 output columns: column blocks cq = 0, 1 of 16 (one MFMA tile each);
-    // wave w owns slots 2w, 2w+1 of both blocks (the h operand of a slot is
-    // shared by the two blocks)
-    const int cb = bid - nA;
-    const int c0c = cb * 32;
-    const int Mi = a.Mi;
-    const int kb = Mi >> 5;
-    const int steps = (kb + 3) >> 2;
-    if (threadIdx.x < 2) sm.b.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
-    if (threadIdx.x == 2) sm.b.code127[0] = 0x7F7F7F7Fu;
-    // x_l of this workgroup's 32 columns (threads 0..31): layer 0 from the
-    // input, later layers from this workgroup's own previous result
-    float xown = 0.0f;
-    if (threadIdx.x < 32) xown = mx::bf16_to_f32(a.x0[c0c + threadIdx.x]);
-
-    uint4 bq[2][2][MS];      // [slot q][column block cq][K step]
-    uint32_t bsw[2][2][3];
-    int slot[2];
-    float wgt[2];
-    auto load_w = [&](int l) {
-        const StackLayer* ly = a.layers + l;
+    uint4 dq[2][MS];
+    uint32_t dsw[2][3];
+    auto load_dn = [&](int l, bool valid) {
+        const int e = route_id(l);
+        const __amdgpu_buffer_rsrc_t rw = rsrc(route_ptr(l, 2) + (int64_t)e * a.wp_stride_dn, valid ? H * (Mi >> 1) : 0);
+        const __amdgpu_buffer_rsrc_t rs = rsrc(route_ptr(l, 5) + (int64_t)e * a.ws_stride_dn, valid ? H * kb : 0);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            slot[q] = 2 * wave + q;
-            const int sl = slot[q] < E ? slot[q] : 0;
-            int e = __builtin_amdgcn_readfirstlane(a.ids[l * E + sl]);
-            e = e < 0 ? 0 : (e >= a.n_experts ? a.n_experts - 1 : e);
-            wgt[q] = a.w[l * E + sl];
-            const bool lv = slot[q] < E;
+        for (int k = 0; k < 2; ++k) {
 #pragma unroll
-            for (int cq = 0; cq < 2; ++cq) {
-                const int row = c0c + 16 * cq + r;
-                const uint8_t* wrow = ly->wp[2] + (int64_t)e * a.wp_stride_dn + (int64_t)row * (Mi >> 1);
-                const uint8_t* srow = ly->ws[2] + (int64_t)e * a.ws_stride_dn + (int64_t)row * kb;
+            for (int i = 0; i < MS; ++i) {
+                const v4u q = __builtin_amdgcn_raw_buffer_load_b128(rw, woffd[k] + 16 * max(0, min(i, ilast)), 0, 0);
+                dq[k][i] = make_uint4(q.x, q.y, q.z, q.w);
+            }
+            if (KB4) {
 #pragma unroll
-                for (int i = 0; i < MS; ++i) {
-                    const int blk = g * steps + i;
-                    bq[q][cq][i] = ld_sel(reinterpret_cast<const uint4*>(wrow + min(blk, kb - 1) * 16),
-                                          lv && i < steps && blk < kb, make_uint4(0, 0, 0, 0));
-                }
-                const int sb0 = (g * steps) & ~3;
-                if ((kb & 3) == 0) {
+                for (int d = 0; d < 3; ++d)
+                    dsw[k][d] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + min(sb0 + 4 * d, kb - 4), 0, 0);
+            } else {
 #pragma unroll
-                    for (int d = 0; d < 3; ++d)
-                        bsw[q][cq][d] = *reinterpret_cast<const uint32_t*>(srow + min(sb0 + 4 * d, kb - 4));
-                } else {
+                for (int d = 0; d < 3; ++d) {
+                    uint32_t w = 0;
 #pragma unroll
-                    for (int d = 0; d < 3; ++d) {
-                        uint32_t v = 0;
-#pragma unroll
-                        for (int b = 0; b < 4; ++b) {
-                            const int off = sb0 + 4 * d + b;
-                            v |= ((lv && off < kb) ? (uint32_t)srow[off] : 127u) << (8 * b);
-                        }
-                        bsw[q][cq][d] = v;
-                    }
+                    for (int q = 0; q < 4; ++q)
+                        w |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, soffd[k] + min(sb0 + 4 * d + q, kb - 1), 0, 0)
+                             << (8 * q);
+                    dsw[k][d] = w;
                 }
             }
         }
     };
-    if (!STRICT) load_w(0);
 
-    const int nwords = E * nblk_mi * kRecWords;
-    constexpr int kGroups = (kMaxE * 4 * MS * kRecWords) / 2048;
-    for (int l = 0; l < L; ++l) {
-        const int b = (c0 + l) % kNBuf;
-        const int bprev = (b + kNBuf - 1) % kNBuf;
-        if (STRICT) {
-            if (l > 0) {
-                uint4 unused;
-                live = wait_x(a, xbuf + bprev * a.xwords, unused, live);
-            }
-            load_w(l);
-        }
-        // h_l: poll all words, unpack term bytes and codes into LDS
-        const uint32_t* cur = hbuf + b * a.hwords;
+    if (!STRICT) {
+        const int l0 = min(par, L - 1);
+        load_gu(l0, par < L);
+        load_dn(l0, par < L);
+    }
+    bool live = true;
+    for (int l = par; l < L; l += 2) {
+        const uint32_t tag = c0 + (uint32_t)l + 1u;          // this layer's tag (never 0)
+        const int b = (int)((c0 + (uint32_t)l) % kNBuf);
+        // combine weights of every slot (read now, used after the y poll)
+        float wt[kMaxE];
+#pragma unroll
+        for (int t = 0; t < kMaxE; ++t) wt[t] = t < E ? route_w(l, t) : 0.0f;
+        // ---- 1. x_l for the wave's K quarter (columns cw*H/4 ..) into E4M3 term records (LDS)
+        // and, for the combine, bf16 (LDS)
         {
-            const __amdgpu_buffer_rsrc_t rs =
-                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(cur), (short)0, nwords * 4, 0x00020000);
-            int off[2 * kGroups];
+            const int nq = H >> 2;                  // columns per quarter (128..512)
+            const int q0 = cw * nq;
+            if (l == 0) {
+                // the launch's input: split here, lane -> values q0 + 8 lane .. +7 (whole quads)
+                if (8 * lane < nq) {
+                    const int k0 = q0 + 8 * lane;
+                    const uint4 q = *reinterpret_cast<const uint4*>(a.x0 + k0);
+                    *reinterpret_cast<uint4*>(&sm.xb[k0]) = q;
+                    const uint32_t xq[4] = {q.x, q.y, q.z, q.w};
+                    float v[8];
 #pragma unroll
-            for (int k = 0; k < kGroups; ++k)
-#pragma unroll
-                for (int h = 0; h < 2; ++h) off[2 * k + h] = min(2048 * k + 8 * (int)threadIdx.x + 4 * h, nwords - 4) * 4;
-            v4u v[2 * kGroups];
-            live = poll_groups<2 * kGroups>(a, rs, off, v, live);
-#pragma unroll
-            for (int k = 0; k < kGroups; ++k) {
-                const int wi = 2048 * k + 8 * (int)threadIdx.x;
-                if (wi < nwords) {
-                    const uint32_t wv[8] = {v[2 * k].x, v[2 * k].y, v[2 * k].z, v[2 * k].w,
-                                            v[2 * k + 1].x, v[2 * k + 1].y, v[2 * k + 1].z, v[2 * k + 1].w};
-                    const int rec = 64 * k + ((int)threadIdx.x >> 2);
-#pragma unroll
-                    for (int t = 0; t < kTerms; ++t) {
-                        const uint32_t sel = 0x0C0C0000u | ((4u + t) << 8) | (uint32_t)t;
-                        const uint32_t lo = __builtin_amdgcn_perm(wv[1], wv[0], sel) |
-                                            (__builtin_amdgcn_perm(wv[3], wv[2], sel) << 16);
-                        const uint32_t hi = __builtin_amdgcn_perm(wv[5], wv[4], sel) |
-                                            (__builtin_amdgcn_perm(wv[7], wv[6], sel) << 16);
-                        *reinterpret_cast<uint64_t*>(sm.b.h8 + (rec * kTerms + t) * 32 + 8 * (threadIdx.x & 3)) =
-                            (uint64_t)lo | ((uint64_t)hi << 32);
+                    for (int i = 0; i < 4; ++i) {
+                        v[2 * i] = mx::bf16_to_f32((uint16_t)(xq[i] & 0xFFFFu));
+                        v[2 * i + 1] = mx::bf16_to_f32((uint16_t)(xq[i] >> 16));
                     }
-                    if ((threadIdx.x & 3) == 0)
-                        sm.b.hsc[rec] = (wv[0] >> 24) | ((wv[1] >> 24) << 8) | ((wv[2] >> 24) << 16);
+                    split8_to_record(v, sm.xr + (k0 >> 5) * kRecBytes, k0 & 31);
+                }
+            } else {
+                // published (already split) in layer l-1 by the other set: one word per column,
+                // [term bytes 0..2 | code of term (column % 32) for columns 0..2 of a block |
+                //  bf16 | tag16]; lane -> columns q0 + 256 i + 4 lane .. +3
+                const __amdgpu_buffer_rsrc_t rs = region(x_base((b + kNBuf - 1) % kNBuf), H);
+                uint32_t off[8];
+                bool ok[8];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) {
+                        ok[4 * i + c] = 256 * i + 4 * lane < nq;
+                        off[4 * i + c] = (uint32_t)((q0 + min(256 * i + 4 * lane, nq - 4) + c) * 8);
+                    }
+                v2u xw[8];
+                live = poll_words<8, 16>(a, rs, off, ok, tag16(tag - 1u), xw, live);
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    if (256 * i + 4 * lane < nq) {
+                        const int c0 = q0 + 256 * i + 4 * lane;
+                        uint8_t* rec = sm.xr + (c0 >> 5) * kRecBytes;
+#pragma unroll
+                        for (int t = 0; t < kTerms; ++t) {
+                            uint32_t d = 0;
+#pragma unroll
+                            for (int c = 0; c < 4; ++c) d |= ((xw[4 * i + c].x >> (8 * t)) & 0xFFu) << (8 * c);
+                            *reinterpret_cast<uint32_t*>(rec + 32 * t + (c0 & 31)) = d;
+                        }
+                        if ((c0 & 31) == 0)
+                            *reinterpret_cast<uint32_t*>(rec + 96) =
+                                (xw[4 * i].x >> 24) | ((xw[4 * i + 1].x >> 24) << 8) | ((xw[4 * i + 2].x >> 24) << 16);
+                        *reinterpret_cast<uint2*>(&sm.xb[c0]) =
+                            make_uint2((xw[4 * i].y & 0xFFFFu) | (xw[4 * i + 1].y << 16),
+                                       (xw[4 * i + 2].y & 0xFFFFu) | (xw[4 * i + 3].y << 16));
+                    }
                 }
             }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own records, read below
         }
-        lds_barrier();
-
-        const int sb0 = (g * steps) & ~3;
-        bool lv[2];
-        const uint8_t* h8[2];
-        const uint32_t* hsq[2];
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            lv[q] = slot[q] < E;
-            const int sl = lv[q] ? slot[q] : 0;
-            h8[q] = sm.b.h8 + (sl * kb * kTerms + rr) * 32;
-            hsq[q] = sm.b.hsc + sl * kb;
+        if (STRICT) {
+            load_gu(l, true);
+            load_dn(l, true);
         }
-        const float w0 = wgt[0], w1 = wgt[1];
-        mx::v4f acc[2][2] = {{{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}, {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}}};
+        // ---- 2. gate/up MFMAs: A = x_l terms (rows 0..2), B = the tile's weight rows
+        {
+            mx::v8i av[4];
+            uint32_t asc[4];
 #pragma unroll
-        for (int i = 0; i < MS; ++i) {
-            const int blo = (g >> 1) * steps + i;
-            const int bhi = (2 + (g >> 1)) * steps + i;
-            const int bown = g * steps + i;
-            const bool rok = r < kTerms && i < steps;
-            const int bi = g * steps + i - sb0;
+            for (int i = 0; i < 4; ++i) {
+                const int base = bpw * cw + min(i, sa - 1);
+                const bool ok = r < kTerms && i < sa;
+                const uint4* plo = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + sa * (g >> 1)) * kRecBytes + 32 * rr + 16 * (g & 1))
+                                      : &sm.zero[0];
+                const uint4* phi = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + sa * (2 + (g >> 1))) * kRecBytes + 32 * rr + 16 * (g & 1))
+                                      : &sm.zero[1];
+                av[i] = cat8(*plo, *phi);
+                const uint32_t c = sm.xr[(base + sa * g) * kRecBytes + 96 + rr];
+                asc[i] = ok ? c : 127u;
+            }
+            mx::v4f acc[NT];
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                const bool ok = rok && lv[q];
-                const uint4* plo = (ok && blo < kb) ? reinterpret_cast<const uint4*>(h8[q] + blo * (kTerms * 32) + 16 * (g & 1))
-                                                    : &sm.b.zero[0];
-                const uint4* phi = (ok && bhi < kb) ? reinterpret_cast<const uint4*>(h8[q] + bhi * (kTerms * 32) + 16 * (g & 1))
-                                                    : &sm.b.zero[1];
-                const uint32_t* pc = (ok && bown < kb) ? &hsq[q][bown] : &sm.b.code127[0];
+            for (int m = 0; m < NT; ++m) {
+                acc[m] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
+                const uint64_t sc8 = (((uint64_t)bshi[m] << 32) | bslo[m]) >> (8 * (blk0 & 3));
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    acc[m] = mx::mfma16_fp8a_fp4b(av[i], bq[m][i], acc[m], asc[i], (uint32_t)(sc8 >> (8 * i)) & 0xFFu);
+            }
+#pragma unroll
+            for (int m = 0; m < NT; ++m) mx::pin(acc[m]);
+            if (lane < 16) {
+#pragma unroll
+                for (int m = 0; m < NT; ++m) sm.red[cw][m][lane] = acc[m][0] + acc[m][1] + acc[m][2];
+            }
+        }
+        lds_barrier();                                                   // B2: gate/up partial sums
+        // publish the g/u values of tile m (wave m % 4): lane r = row r
+        for (int m = cw; m < NT; m += kWaves) {
+            const int t = jj + kPerSet * m;
+            if (lane < 16 && t < ntile) {
+                float v = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) v += sm.red[w][m][lane];
+                put_local(gu_base(b) + t * 16 + lane, __float_as_uint(v), tag);
+            }
+        }
+        // ---- 3. the slot's g/u for this wave's 32-blocks of h (rows r0 .. r0 + nr), row 64k + lane
+        // of them per load (coalesced); h = silu(g) * u per row into LDS; then lane 8i + q -> rows
+        // 4q .. 4q+3 of block i into E4M3 term records (8 lanes per block)
+        {
+            const int bph = (kb + 3) >> 2;                // blocks per wave (<= 8)
+            const int blo = min(cw * bph, kb), bhi = min(blo + bph, kb);
+            const int r0 = 32 * blo, nr = 32 * (bhi - blo);
+            const __amdgpu_buffer_rsrc_t rs = region(gu_base(b), 2 * Mi);
+            uint32_t off[8];
+            bool ok[8];
+            uint32_t gv[8];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int row = r0 + min(64 * k + lane, max(nr - 1, 0));
+                ok[k] = ok[4 + k] = 64 * k + lane < nr;
+                off[k] = (uint32_t)(min(row, Mi - 1) * 8);
+                off[4 + k] = (uint32_t)((Mi + min(row, Mi - 1)) * 8);
+            }
+            live = poll_tagged<8>(a, rs, off, ok, tag, gv, live);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (ok[k]) sm.hs[r0 + 64 * k + lane] = mx::silu_mul(__uint_as_float(gv[k]), __uint_as_float(gv[4 + k]));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own h values, read below
+            const int hblk = blo + (lane >> 3);
+            if (hblk < bhi) {
+                const int pos = 4 * (lane & 7);
+                const uint4 q = *reinterpret_cast<const uint4*>(&sm.hs[32 * hblk + pos]);
+                float v[4] = {__uint_as_float(q.x), __uint_as_float(q.y), __uint_as_float(q.z), __uint_as_float(q.w)};
+                uint32_t w4[kTerms], codes;
+                split4(v, w4, codes);
+                uint8_t* rec = sm.hr + hblk * kRecBytes;
+#pragma unroll
+                for (int t = 0; t < kTerms; ++t) *reinterpret_cast<uint32_t*>(rec + 32 * t + pos) = w4[t];
+                if (pos == 0) *reinterpret_cast<uint32_t*>(rec + 96) = codes;
+            }
+        }
+        lds_barrier();                                                   // B3: h_l staged
+        // ---- 4. down MFMAs: A = h_l terms, B = 16 columns' down rows (two column tiles, their
+        // accumulations interleaved); publish y_s
+        {
+            const uint8_t* h8 = sm.hr + 32 * rr;   // term rr of block 0
+            mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int i = 0; i < MS; ++i) {
+                const int blo = (g >> 1) * steps + i;
+                const int bhi = (2 + (g >> 1)) * steps + i;
+                const int bown = g * steps + i;
+                const bool rok = r < kTerms && i < steps;
+                const uint4* plo = (rok && blo < kb) ? reinterpret_cast<const uint4*>(h8 + blo * kRecBytes + 16 * (g & 1))
+                                                     : &sm.zero[0];
+                const uint4* phi = (rok && bhi < kb) ? reinterpret_cast<const uint4*>(h8 + bhi * kRecBytes + 16 * (g & 1))
+                                                     : &sm.zero[1];
+                const uint8_t* pc = (rok && bown < kb) ? sm.hr + bown * kRecBytes + 96 + rr
+                                                       : reinterpret_cast<const uint8_t*>(&sm.code127[0]);
                 const mx::v8i av = cat8(*plo, *phi);
-                const uint32_t asc = (*pc >> (8 * rr)) & 0xFFu;
+                const uint32_t asc = *pc;
+                const int bi = g * steps + i - sb0;
 #pragma unroll
-                for (int cq = 0; cq < 2; ++cq) {
-                    const uint32_t wd = bi < 4 ? bsw[q][cq][0] : (bi < 8 ? bsw[q][cq][1] : bsw[q][cq][2]);
-                    acc[q][cq] = mx::mfma16_fp8a_fp4b(av, bq[q][cq][i], acc[q][cq], asc, (wd >> (8 * (bi & 3))) & 0xFFu);
+                for (int k = 0; k < 2; ++k) {
+                    const uint32_t wd = bi < 4 ? dsw[k][0] : (bi < 8 ? dsw[k][1] : dsw[k][2]);
+                    acc[k] = mx::mfma16_fp8a_fp4b(av, dq[k][i], acc[k], asc, (wd >> (8 * (bi & 3))) & 0xFFu);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+                mx::pin(acc[k]);
+                if (dok[k] && lane < 16)
+                    put_device(part_base(b, s) + c0d + 16 * (cw + 4 * k) + lane,
+                               __float_as_uint(acc[k][0] + acc[k][1] + acc[k][2]), tag);
+            }
+        }
+        // ---- 5. y of every slot for block cb = 4 jj + cw (lanes 0..31 = its columns); x_{l+1};
+        // its E4M3 terms, published with the bf16 value for the other set's next layer
+        {
+            const int cb = 4 * jj + cw;
+            if (cb < hb) {
+                const bool ccol = lane < 32;
+                const int col = 32 * cb + (lane & 31);
+                // slot t's y at word t*part_q + col of the y region
+                const __amdgpu_buffer_rsrc_t rs = region(part_base(b, 0), E * a.part_q);
+                uint32_t off[kMaxE];
+                bool ok[kMaxE];
+                uint32_t yv[kMaxE];
+#pragma unroll
+                for (int t = 0; t < kMaxE; ++t) {
+                    ok[t] = ccol && t < E;
+                    off[t] = (uint32_t)((min(t, E - 1) * a.part_q + col) * 8);
+                }
+                live = poll_tagged<kMaxE>(a, rs, off, ok, tag, yv, live);
+                // the one-layer kernel's order: per slot pair (2w, 2w+1) a fused
+                // multiply-add chain from 0, then the four pair sums left to right
+                float y = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kMaxE / 2; ++w) {
+                    float part = 0.0f;
+                    if (2 * w < E) part = fmaf(wt[2 * w], __uint_as_float(yv[2 * w]), part);
+                    if (2 * w + 1 < E) part = fmaf(wt[2 * w + 1], __uint_as_float(yv[2 * w + 1]), part);
+                    y = w == 0 ? part : y + part;
+                }
+                // runtime/model_runner_v2.py:208: x = x + moe.bfloat16() in bf16
+                const float yb = mx::bf16_to_f32(mx::f32_to_bf16_rne(y));
+                const uint16_t xn = mx::f32_to_bf16_rne(mx::bf16_to_f32(sm.xb[col]) + yb);
+                if (l + 1 < L) {
+                    uint32_t codes;
+                    const uint32_t bytes = split32(mx::bf16_to_f32(xn), codes);   // over lanes 0..31
+                    const uint32_t code = (lane & 31) < kTerms ? (codes >> (8 * (lane & 31))) & 0xFFu : 0u;
+                    if (ccol) put_word(x_base(b) + col, bytes | (code << 24), (uint32_t)xn | (tag16(tag) << 16));
+                } else if (s == 0 && ccol) {
+                    a.x_out[col] = xn;
+                }
+                if (s == 0 && ccol) {
+                    if (a.x_all) a.x_all[(int64_t)l * H + col] = xn;
+                    if (a.y_all) a.y_all[(int64_t)l * H + col] = y;
                 }
             }
         }
-        float part[2] = {0.0f, 0.0f};
-#pragma unroll
-        for (int cq = 0; cq < 2; ++cq) {
-#pragma unroll
-            for (int q = 0; q < 2; ++q) mx::pin(acc[q][cq]);
-            if (lv[0]) part[cq] = fmaf(w0, acc[0][cq][0] + acc[0][cq][1] + acc[0][cq][2], part[cq]);
-            if (lv[1]) part[cq] = fmaf(w1, acc[1][cq][0] + acc[1][cq][1] + acc[1][cq][2], part[cq]);
+        lds_barrier();                                                   // B5: every poll of the layer done
+        if (!STRICT) {
+            // layer l+2 streams while the other set computes layer l+1
+            const int ln = l + 2 < L ? l + 2 : l;
+            load_gu(ln, l + 2 < L);
+            load_dn(ln, l + 2 < L);
         }
-        if (lane < 16) {
-            sm.b.red[wave][lane] = part[0];
-            sm.b.red[wave][16 + lane] = part[1];
-        }
-        lds_barrier();
-        if (threadIdx.x < 32) {
-            const int c = c0c + threadIdx.x;
-            const float y = sm.b.red[0][threadIdx.x] + sm.b.red[1][threadIdx.x] + sm.b.red[2][threadIdx.x] +
-                            sm.b.red[3][threadIdx.x];
-            // runtime/model_runner_v2.py:208: x = x + moe.bfloat16() in bf16
-            const float yb = mx::bf16_to_f32(mx::f32_to_bf16_rne(y));
-            const uint16_t xn = mx::f32_to_bf16_rne(xown + yb);
-            xown = mx::bf16_to_f32(xn);
-            wait_stores();   // the previous layer's empty-stores are visible before this publish
-            if (l + 1 < L)
-                __hip_atomic_store(xbuf + b * a.xwords + c, (uint32_t)xn, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            else
-                a.x_out[c] = xn;
-            // empty these columns in the previous layer's buffer (written again
-            // two layers on; its readers, the gate/up workgroups of this layer,
-            // are done: h_l is complete)
-            __hip_atomic_store(xbuf + bprev * a.xwords + c, kEmpty, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (a.x_all) a.x_all[(int64_t)l * H + c] = xn;
-            if (a.y_all) a.y_all[(int64_t)l * H + c] = y;
-        }
-        if (!STRICT && l + 1 < L) load_w(l + 1);   // streams under the next gate/up phase, after the publish
     }
     if (!live) set_error(a);
-    if (threadIdx.x == 0) *memo = c0 + L;
+    if (threadIdx.x == 0) *memo = (int)(c0 + (uint32_t)L);
 }
 
-__global__ void reset_stack_kernel(uint32_t* ws, int cfg, int words) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+__global__ void reset_stack_kernel(uint32_t* ws, int cfg, int64_t words) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < kBufOff / 4) ws[i] = (i == kCfgOff / 4) ? (uint32_t)cfg : 0u;
-    if (i < words) ws[kBufOff / 4 + i] = kEmpty;
+    if (i < words) ws[kBufOff / 4 + i] = 0u;   // tag 0: no layer
 }
-
-size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-int h_words(int E, int Mi) { return (int)(align256((size_t)E * (Mi / 32) * kRecWords * 4) / 4); }
-int x_words(int H) { return (int)(align256((size_t)H * 4) / 4); }
 
 }  // namespace
 
 extern "C" size_t mxfp4_decode_stack_workspace_size(int E, int H, int Mi) {
     if (E <= 0 || H <= 0 || Mi <= 0) return 0;
-    return kBufOff + (size_t)kNBuf * (h_words(E, Mi) + x_words(H)) * 4;
+    return kBufOff + (size_t)kNBuf * (size_t)buf_words(H, Mi) * 8;
 }
 
 extern "C" int mxfp4_decode_stack_reset(void* workspace, int E, int H, int Mi, void* stream) {
     MXH_REQUIRE(workspace, "decode_stack_reset: null workspace");
     MXH_REQUIRE(E >= 1 && E <= kMaxE && Mi >= 32 && Mi <= 1024 && Mi % 32 == 0 && H >= 512 && H <= 2048 && H % 512 == 0,
                 "decode_stack_reset: E=%d H=%d Mi=%d out of range", E, H, Mi);
-    const int words = kNBuf * (h_words(E, Mi) + x_words(H));
-    const int n = words > kBufOff / 4 ? words : kBufOff / 4;
-    hipLaunchKernelGGL(reset_stack_kernel, dim3((n + 255) / 256), dim3(256), 0, mxh::as_stream(stream),
+    const int64_t words = (int64_t)kNBuf * buf_words(H, Mi) * 2;   // uint32 words of the buffers
+    const int64_t n = words > kBufOff / 4 ? words : kBufOff / 4;
+    hipLaunchKernelGGL(reset_stack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, mxh::as_stream(stream),
                        static_cast<uint32_t*>(workspace), stack_cfg(E, H, Mi), words);
     return mxh::launch_status("decode_stack_reset");
 }
@@ -557,6 +705,23 @@ extern "C" int mxfp4_decode_stack_status(const void* workspace, int* error_flag)
     return MXFP4_OK;
 }
 
+namespace {
+template <bool ST, int MS, bool K4>
+const void* stack_kernel_nt(int nt) {
+    switch (nt) {
+        case 2: return reinterpret_cast<const void*>(&decode_stack_kernel<ST, MS, K4, 2>);
+        case 4: return reinterpret_cast<const void*>(&decode_stack_kernel<ST, MS, K4, 4>);
+        case 6: return reinterpret_cast<const void*>(&decode_stack_kernel<ST, MS, K4, 6>);
+        default: return reinterpret_cast<const void*>(&decode_stack_kernel<ST, MS, K4, 8>);
+    }
+}
+template <bool ST>
+const void* stack_kernel(int ms, bool k4, int nt) {
+    if (ms <= 6) return k4 ? stack_kernel_nt<ST, 6, true>(nt) : stack_kernel_nt<ST, 6, false>(nt);
+    return k4 ? stack_kernel_nt<ST, 8, true>(nt) : stack_kernel_nt<ST, 8, false>(nt);
+}
+}  // namespace
+
 extern "C" int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const float* w, const void* layer_table,
                                       int n_layers, int n_experts, int E, int H, int Mi, void* x_out, void* x_all,
                                       float* y_all, int strict, void* workspace, size_t workspace_bytes,
@@ -570,25 +735,22 @@ extern "C" int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const f
     MXH_REQUIRE(workspace_bytes >= mxfp4_decode_stack_workspace_size(E, H, Mi), "moe_decode_stack: workspace too small");
     MXH_REQUIRE(((uintptr_t)workspace & 255) == 0, "moe_decode_stack: workspace must be 256-byte aligned");
     MXH_REQUIRE(((uintptr_t)x & 15) == 0, "moe_decode_stack: x must be 16-byte aligned");
-    const int nA = E * (Mi / 32), nB = H / 32;
     int dev = 0, n_cu = 0;
     MXH_REQUIRE(hipGetDevice(&dev) == hipSuccess &&
                     hipDeviceGetAttribute(&n_cu, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess,
                 "moe_decode_stack: cannot query the CU count");
-    MXH_REQUIRE(nA + nB <= n_cu && nA + nB <= kMaxWg,
-                "moe_decode_stack: E*Mi/32 + H/32 = %d workgroups, more than the %d CUs (one resident workgroup per CU)",
-                nA + nB, n_cu);
+    MXH_REQUIRE(n_cu == kGrid, "moe_decode_stack: needs a GPU of %d CUs in %d XCDs (this one has %d CUs)", kGrid, kXcds,
+                n_cu);
     const int steps = (Mi / 32 + 3) / 4;
-    const void* kern = steps <= 6 ? (strict ? reinterpret_cast<const void*>(&decode_stack_kernel<true, 6>)
-                                            : reinterpret_cast<const void*>(&decode_stack_kernel<false, 6>))
-                                  : (strict ? reinterpret_cast<const void*>(&decode_stack_kernel<true, 8>)
-                                            : reinterpret_cast<const void*>(&decode_stack_kernel<false, 8>));
+    const bool kb4 = (Mi / 32) % 4 == 0;
+    const int nt = (((Mi / 8 + kPerSet - 1) / kPerSet) + 1) & ~1;   // gate/up tiles per workgroup, even
+    const void* kern = strict ? stack_kernel<true>(steps, kb4, nt) : stack_kernel<false>(steps, kb4, nt);
     int per_cu = 0;
-    MXH_REQUIRE(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, 256, 0) == hipSuccess,
+    MXH_REQUIRE(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kThreads, 0) == hipSuccess,
                 "moe_decode_stack: occupancy query failed");
     // every workgroup waits on others, so the whole grid must be resident at once
-    MXH_REQUIRE((int64_t)per_cu * n_cu >= nA + nB,
-                "moe_decode_stack: %d workgroups but only %d x %d can be resident at once", nA + nB, per_cu, n_cu);
+    MXH_REQUIRE((int64_t)per_cu * n_cu >= kGrid,
+                "moe_decode_stack: %d workgroups but only %d x %d can be resident at once", kGrid, per_cu, n_cu);
     StackArgs a{};
     a.layers = static_cast<const StackLayer*>(layer_table);
     a.ids = ids;
@@ -607,17 +769,17 @@ extern "C" int mxfp4_moe_decode_stack(const void* x, const int32_t* ids, const f
     a.H = H;
     a.Mi = Mi;
     a.cfg = stack_cfg(E, H, Mi);
-    a.hwords = h_words(E, Mi);
-    a.xwords = x_words(H);
+    a.gu_q = gu_words(Mi);
+    a.part_q = part_words(H);
+    a.x_q = x_words(H);
+    a.buf_q = buf_words(H, Mi);
     a.ws = static_cast<uint8_t*>(workspace);
-    hipStream_t st = mxh::as_stream(stream);
-    const dim3 grid(nA + nB), block(256);
-    if (steps <= 6) {
-        if (strict) hipLaunchKernelGGL((decode_stack_kernel<true, 6>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((decode_stack_kernel<false, 6>), grid, block, 0, st, a);
-    } else {
-        if (strict) hipLaunchKernelGGL((decode_stack_kernel<true, 8>), grid, block, 0, st, a);
-        else hipLaunchKernelGGL((decode_stack_kernel<false, 8>), grid, block, 0, st, a);
+    void* args[] = {&a};
+    const hipError_t le = hipLaunchKernel(kern, dim3(kGrid), dim3(kThreads), args, 0, mxh::as_stream(stream));
+    if (le != hipSuccess) {
+        mxh::set_error("moe_decode_stack: kernel launch failed: %s", hipGetErrorString(le));
+        (void)hipGetLastError();
+        return (int)le;
     }
     return mxh::launch_status("moe_decode_stack");
 }

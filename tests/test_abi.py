@@ -43,8 +43,9 @@ def test_every_declared_symbol_is_exported(lib):
 def test_workspace_size(lib):
     assert lib.mxfp4_linear_workspace_size(4, 2048) == 4096 + 256
     assert lib.mxfp4_linear_workspace_size(0, 2048) == 0
-    # header + memos (4096 B), three h buffers of 8*24*32 words, three x buffers of 2048 words
-    assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 4096 + 3 * (6144 + 2048) * 4
+    # header + memos (2048 B), then two buffers of 8-byte tagged words: per XCD 2*Mi g/u words
+    # and H x words, per slot H y words
+    assert lib.mxfp4_decode_stack_workspace_size(8, 2048, 768) == 2048 + 2 * 8 * (2 * 768 + 2048 + 2048) * 8
     assert lib.mxfp4_decode_stack_workspace_size(0, 2048, 768) == 0
     # argmax: 256-byte counter head, then (M, P) maxima and indices, P = ceil(V / 4096) slices
     assert lib.mxfp4_argmax_workspace_size(8, 151936) == 256 + 2 * 8 * 38 * 4
