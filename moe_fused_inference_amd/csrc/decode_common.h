@@ -23,22 +23,19 @@ constexpr uint32_t kEmpty = 0xBADBAD7Fu;  // "no value yet": byte 0 is the E4M3 
 
 // E8M0 code of the smallest 2^e with amax <= 448*2^e (E4M3 range), e in
 // [-127, 127]; zero blocks get 127.
+// Branch-free: both the normal and the subnormal exponent are computed and
+// selected (amax is never negative).
 __device__ __forceinline__ uint32_t e4m3_block_code(float amax) {
-    if (!(amax > 0.0f)) return 127u;
-    uint32_t bits = __float_as_uint(amax);
-    int ex = (int)(bits >> 23);
-    uint32_t frac = bits & 0x7FFFFFu;
-    int x;
-    if (ex == 0) {
-        int p = 31 - __clz((int)frac);
-        x = p - 149;
-        frac = (frac << (23 - p)) & 0x7FFFFFu;
-    } else {
-        x = ex - 127;
-    }
-    int e = (frac <= 0x600000u) ? x - 8 : x - 7;  // (1+f) <= 1.75 -> 448 fits
+    const uint32_t bits = __float_as_uint(amax);
+    const int ex = (int)(bits >> 23);
+    const uint32_t frac = bits & 0x7FFFFFu;
+    const int p = 31 - __clz((int)(frac | 1u));             // subnormal: leading bit of frac
+    const uint32_t fn = (frac << (23 - p)) & 0x7FFFFFu;     // and frac normalised
+    const int x = ex == 0 ? p - 149 : ex - 127;
+    const uint32_t f = ex == 0 ? fn : frac;
+    int e = (f <= 0x600000u) ? x - 8 : x - 7;               // (1+f) <= 1.75 -> 448 fits
     e = e < -127 ? -127 : (e > 127 ? 127 : e);
-    return (uint32_t)(e + 127);
+    return amax > 0.0f ? (uint32_t)(e + 127) : 127u;        // zero (and NaN) blocks: 127
 }
 
 __device__ __forceinline__ float e8m0_value(uint32_t code) {

@@ -290,7 +290,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 usum += sm.a.red[w][2 + (j >> 4)][j & 15];
             }
             uint32_t codes;
-            const uint32_t bytes = split32(mx::silu_mul(gsum, usum), codes);
+            const uint32_t bytes = split32(mx::silu_mul_fast(gsum, usum), codes);
             const uint32_t word = bytes | (j < kTerms ? ((codes >> (8 * j)) & 0xFFu) << 24 : 0u);
             const bool cfg_ok = cfg == a.cfg;
             const int64_t w_off = ((int64_t)s * nblk_mi + jb) * kRecWords + j;

@@ -563,8 +563,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             }
             live = poll_tagged<8>(a, rs, off, ok, tag, gv, live);
 #pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (ok[k]) sm.hs[r0 + 64 * k + lane] = mx::silu_mul(__uint_as_float(gv[k]), __uint_as_float(gv[4 + k]));
+            for (int k = 0; k < 4; ++k) {
+                const float h = mx::silu_mul_fast(__uint_as_float(gv[k]), __uint_as_float(gv[4 + k]));
+                if (64 * k < nr && ok[k]) sm.hs[r0 + 64 * k + lane] = h;   // 64k < nr: wave-uniform
+            }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own h values, read below
             const int hblk = blo + (lane >> 3);
             if (hblk < bhi) {

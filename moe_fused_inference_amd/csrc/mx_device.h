@@ -173,9 +173,22 @@ __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     return (uint16_t)(u >> 16);
 }
 
+// h is a rounded fp32 value, as in the reference: no contraction of its last
+// product into whatever the caller computes from it next (an FMA there would
+// make the result depend on the surrounding code).
 __device__ __forceinline__ float silu_mul(float g, float u) {
+#pragma clang fp contract(off)
     // h = g / (1 + exp(-g)) * u, fp32 (src/ext/mxfp4_decode.cu:258)
     return (g / (1.0f + expf(-g))) * u;
+}
+
+// silu_mul on the hardware exp2 and reciprocal (a few ulp from silu_mul):
+// for the fused decode kernels, whose h is split into three E4M3 terms (a
+// relative resolution of 2^-12) rather than rounded to a 4-bit code.
+__device__ __forceinline__ float silu_mul_fast(float g, float u) {
+#pragma clang fp contract(off)
+    const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);   // exp(-g); +inf for g < -88
+    return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
 // Reduction over the wave, result in every lane: DPP within rows of 16 lanes
