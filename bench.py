@@ -596,18 +596,36 @@ def copy_reference(torch, nbytes=1 << 30, reps=4):
     log(f"copy reference: {reps} x {nbytes} B device-to-device")
 
 
+STACK_SRC = os.path.join(ROOT, "moe_fused_inference_amd", "csrc", "decode_stack.hip")
+
+
+def source_sha256(path):
+    import hashlib
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()
+
+
 def read_traffic():
     """HBM bytes per launch of the headline kernel (decode_stack_kernel, one
     launch = 48 layers) from the committed counter summary (key: value
-    lines), or None."""
+    lines), and a note.  The summary records the SHA-256 of the kernel source
+    it measured; if that is not the current source, the figure is stale and
+    (None, note) is returned."""
     path = os.path.join(ROOT, "profiles", "decode_stack_traffic.txt")
     if not os.path.exists(path):
-        return None
+        return None, "no counter summary in profiles/"
+    kv = {}
     with open(path) as f:
         for line in f:
-            if line.startswith("hbm_bytes_per_launch:"):
-                return int(float(line.split(":", 1)[1]))
-    return None
+            if ":" in line and not line.startswith((" ", "#", "-")):
+                k, v = line.split(":", 1)
+                kv[k.strip()] = v.strip()
+    if kv.get("source_sha256") != source_sha256(STACK_SRC):
+        return None, "counter summary measured another version of decode_stack.hip (stale): not reported"
+    if "hbm_bytes_per_launch" not in kv:
+        return None, "counter summary has no hbm_bytes_per_launch"
+    return int(float(kv["hbm_bytes_per_launch"])), ("FETCH_SIZE + WRITE_SIZE per launch of this decode_stack.hip "
+                                                   "(" + kv.get("measured", "date not recorded") + ")")
 
 
 def only_extra(args, torch, dext, lext, layers, routes, x0):
@@ -691,7 +709,7 @@ def main():
     log(f"one launch per layer: {us_one:.3f} us/layer, {LAYER_BYTES / (us_one * 1e-6) / 1e9:.1f} GB/s")
     if args.only == "decode1":
         return
-    traffic = read_traffic()
+    traffic, traffic_note = read_traffic()
 
     extra = {"one_launch_per_layer": {
         "us_per_layer": round(us_one, 3), "gbs": round(LAYER_BYTES / (us_one * 1e-6) / 1e9, 1),
@@ -787,9 +805,9 @@ def main():
         "us_per_layer": round(us_layer, 3), "tok_per_s": round(1e3 / ms_step, 1),
         "layer_bytes": LAYER_BYTES, "layer_flops": LAYER_FLOPS,
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_note": traffic_note,
                      "algorithmic_bytes_per_launch": LAYERS * LAYER_BYTES,
-                     "kernel": "decode_stack_kernel<false, 6> (one launch = 48 layers; achieved and traffic "
+                     "kernel": "decode_stack_kernel<false, 6, true, 6> (one launch = 48 layers; achieved and traffic "
                                "per layer = per launch / 48)",
                      "timing": "HIP events on the launching stream around the timed graph replays; rocprofv3 "
                                "kernel-trace average of the same kernel agrees (profiles/)"},
