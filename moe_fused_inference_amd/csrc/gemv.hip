@@ -136,8 +136,9 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
                 aq = sb.a[j];
                 asc = sb.as[j];
             } else {
+                // rows past the group (arow_ok false) are zero: their LDS rows are not built
                 const int c = 4 * s + cx.g;
-                const bool ok = c < cx.nch;
+                const bool ok = c < cx.nch && cx.arow_ok;
                 aq = ok ? *reinterpret_cast<const uint4*>(cx.lq + c * 16) : make_uint4(0, 0, 0, 0);
                 asc = ok ? (uint32_t)cx.lsc[c] : 127u;
             }
@@ -147,24 +148,27 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
     return acc;
 }
 
-// NW waves per workgroup, 16 weight rows each.  NW = 1 spreads a small-N
-// launch (the dense lin_pq projections of a decode step) over 4x more
-// workgroups, so more CUs stream at once.
-template <class Tab, int AMODE, int NW>
-__global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
+// NW row tiles of 16 weight rows per workgroup, each split over S K-parts
+// (one wave per tile and part; the S partial sums meet in LDS in part order).
+// NW = 1 spreads a small-N launch over more workgroups and S > 1 puts a
+// row tile's bytes in flight at once (A_FP4 only), so more CUs stream at once.
+template <class Tab, int AMODE, int NW, int S>
+__global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];  // A_SILU: 16 rows of quantized h
     __shared__ int s_rows[kMaxT];
     __shared__ int s_cnt, s_first;
+    __shared__ mx::v4f s_red[S > 1 ? S - 1 : 1][NW][64];
 
     const int t = blockIdx.y;
     if (t >= a.T) return;
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    const int wave = (threadIdx.x >> 6) % NW;     // row tile
+    const int part = (threadIdx.x >> 6) / NW;     // K part
     const uint8_t* wp = tab.w(t);
     const uint8_t* ws = tab.s(t);
 
     // ---- grouping: the first entry with this weight owns all of its rows
-    if (wave == 0) {
+    if (threadIdx.x < 64) {
         bool dup = false;
         for (int j = lane; j < t; j += 64) dup |= (tab.w(j) == wp) && (tab.s(j) == ws);
         const bool any = __ballot(dup) != 0ull;
@@ -199,17 +203,34 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
     uint8_t* sq = s_dyn;                              // [16][Kp/2]
     uint8_t* ssc = s_dyn + 16 * (a.Kp >> 1);          // [16][nch]
 
+    // this wave's K part: MFMA K-steps [sb, se), blocks from 4*sb on
+    const int spw = (steps + S - 1) / S;
+    const int sb = min(steps, part * spw), se = min(steps, sb + spw);
+    const int64_t boff = 4 * (int64_t)sb;
     for (int rt = 0; rt < cnt; rt += 16) {
+        // A-operand source row of this lane (row r of the tile)
+        const bool arow_ok = (rt + r) < cnt;
+        int asrc = 0;
+        if (AMODE == A_FP4 && arow_ok) asrc = map_entry(a, a.t0 + s_rows[rt + r]).src;
+        const uint8_t* arow = a.aq + (int64_t)asrc * (a.Kp >> 1);
+        const uint8_t* asrow = a.as + (int64_t)asrc * nch;
+        const SegCtx cx{wrow + boff * 16, srow + boff, arow + boff * 16, asrow + boff,
+                        sq + r * (a.Kp >> 1) + boff * 16, ssc + r * nch + boff,
+                        g, se - sb, nch - (int)boff, arow_ok};
+        SegBuf s0buf, s1buf;
+        if (sb < se) load_seg<AMODE>(s0buf, cx, 0);   // the weights stream while h is built
         if (AMODE == A_SILU) {
-            // Build the 16-row A tile: h = silu(g)*u (fp32) quantized per
-            // 32-block with the bit-exact rule; rows past the group are zero.
+            // Build the group's rows of the 16-row A tile: h = silu(g)*u (fp32)
+            // quantized per 32-block with the bit-exact rule (rows past the
+            // group are read as zeros by compute_seg, so they are not built).
             const int upr = a.Kp >> 3;
-            for (int u = threadIdx.x; u < 16 * upr; u += 64 * NW) {
+            const int nb = min(16, cnt - rt);
+            for (int u = threadIdx.x; u < nb * upr; u += 64 * NW * S) {   // quads stay together
                 const int rr = u / upr;
                 const int uu = u - rr * upr;
                 const int k0 = uu * 8;
                 float h[8];
-                if (rt + rr < cnt) {
+                {
                     const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
                     const float* grow = a.gu + (int64_t)em.src * 2 * a.K;
 #pragma unroll
@@ -217,9 +238,6 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
                         const int k = k0 + i;
                         h[i] = (k < a.K) ? mx::silu_mul(grow[k], grow[a.K + k]) : 0.0f;
                     }
-                } else {
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) h[i] = 0.0f;
                 }
                 float am = 0.0f;
 #pragma unroll
@@ -234,38 +252,43 @@ __global__ __launch_bounds__(64 * NW) void grouped_gemv_kernel(Tab tab, GemvArgs
             __syncthreads();
         }
 
-        // A-operand source row of this lane (row r of the tile)
-        const bool arow_ok = (rt + r) < cnt;
-        int asrc = 0;
-        if (AMODE == A_FP4 && arow_ok) asrc = map_entry(a, a.t0 + s_rows[rt + r]).src;
-        const uint8_t* arow = a.aq + (int64_t)asrc * (a.Kp >> 1);
-        const uint8_t* asrow = a.as + (int64_t)asrc * nch;
-
         mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
-        SegBuf s0buf, s1buf;
-        const SegCtx cx{wrow, srow, arow, asrow, sq + r * (a.Kp >> 1), ssc + r * nch,
-                        g, steps, nch, arow_ok};
-        load_seg<AMODE>(s0buf, cx, 0);
-        for (int s0 = 0; s0 < steps; s0 += 2 * kSeg) {
-            if (s0 + kSeg < steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
-            acc = compute_seg<AMODE>(s0buf, cx, s0, acc);
-            if (s0 + kSeg >= steps) break;
-            if (s0 + 2 * kSeg < steps) load_seg<AMODE>(s0buf, cx, s0 + 2 * kSeg);
-            acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
-        }
-
-        mx::pin(acc);
-        // D[4*(l/16)+i][l%16]: token row, weight row
-        const int col = n0 + r;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int rr = 4 * g + i;
-            if (rt + rr < cnt && col < a.N) {
-                const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
-                a.out[(int64_t)em.dst * a.ld_out + em.col + col] = acc[i];
+        if (sb < se) {
+            for (int s0 = 0; s0 < cx.steps; s0 += 2 * kSeg) {
+                if (s0 + kSeg < cx.steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
+                acc = compute_seg<AMODE>(s0buf, cx, s0, acc);
+                if (s0 + kSeg >= cx.steps) break;
+                if (s0 + 2 * kSeg < cx.steps) load_seg<AMODE>(s0buf, cx, s0 + 2 * kSeg);
+                acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
             }
         }
-        if (AMODE == A_SILU) __syncthreads();  // LDS tile reused by the next row tile
+        mx::pin(acc);
+        if constexpr (S > 1) {
+            // partial sums in part order (parts 1.. hand theirs to part 0)
+            if (part > 0) s_red[part - 1][wave][lane] = acc;
+            __syncthreads();
+            if (part == 0) {
+#pragma unroll
+                for (int p = 1; p < S; ++p) {
+                    const mx::v4f o = s_red[p - 1][wave][lane];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[i] += o[i];
+                }
+            }
+        }
+        // D[4*(l/16)+i][l%16]: token row, weight row
+        const int col = n0 + r;
+        if (part == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rr = 4 * g + i;
+                if (rt + rr < cnt && col < a.N) {
+                    const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
+                    a.out[(int64_t)em.dst * a.ld_out + em.col + col] = acc[i];
+                }
+            }
+        }
+        if (AMODE == A_SILU || S > 1) __syncthreads();  // LDS reused by the next row tile
     }
 }
 
@@ -535,17 +558,26 @@ int launch_gemv(const Tab& tab, const GemvArgs& a, int amode, hipStream_t st) {
     // one wave per workgroup when the 4-wave grid would not reach 4
     // workgroups per CU (the A_SILU tile build is shared by the waves of a
     // workgroup, so that path keeps 4)
+    // (a 16-row tile with >= 4 MFMA K-steps is split over 4 waves by K, so a
+    // tile's weight bytes are all in flight at once)
     const bool one = amode == A_FP4 && (int64_t)((a.N + 63) / 64) * a.T < 1024;
+    const int steps = ((a.Kp >> 5) + 3) >> 2;
     if (one) {
         dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)a.T);
-        hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 1>), grid, dim3(64), 0, st, tab, a);
+        if (steps >= 4)
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 1, 4>), grid, dim3(256), 0, st, tab, a);
+        else
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 1, 1>), grid, dim3(64), 0, st, tab, a);
     } else {
         dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.T);
         if (amode == A_FP4)
-            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 4>), grid, dim3(256), 0, st, tab, a);
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 4, 1>), grid, dim3(256), 0, st, tab, a);
+        else if (steps >= 2)
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 2>), grid, dim3(512), silu_lds_bytes(a.Kp),
+                               st, tab, a);
         else
-            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4>), grid, dim3(256), silu_lds_bytes(a.Kp), st,
-                               tab, a);
+            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 1>), grid, dim3(256), silu_lds_bytes(a.Kp),
+                               st, tab, a);
     }
     return mxh::launch_status("grouped_gemv");
 }
