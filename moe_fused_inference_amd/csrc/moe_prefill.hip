@@ -65,10 +65,13 @@ enum { MODE_GATEUP = 0, MODE_DOWN = 1 };
 // contiguous quarter of the row-major (token, slot) pairs: a first coalesced
 // pass counts its matches (ballot) and its valid ids below E; the waves
 // exchange the counts once through LDS; a second pass writes the matches in
-// order (ballot rank), so the result is a stable sort by expert id.
+// order (ballot rank), so the result is a stable sort by expert id.  With
+// `sscore`, the pair's routing weight is written beside it in sorted order
+// (fp32 of the bf16 score), so the down epilogue needs no dependent load.
 __global__ __launch_bounds__(256) void route_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
                                                     int* __restrict__ counts, int* __restrict__ offs,
-                                                    int* __restrict__ pairs) {
+                                                    int* __restrict__ pairs, const uint16_t* __restrict__ scores,
+                                                    float* __restrict__ sscore) {
     __shared__ int s_eq[4], s_lt[4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int E = blockIdx.x;
@@ -111,7 +114,11 @@ __global__ __launch_bounds__(256) void route_kernel(const int64_t* __restrict__ 
         for (int u = 0; u < U; ++u) {
             const bool m = id[u] == (int64_t)E;
             const unsigned long long bal = __ballot(m);
-            if (m) pairs[pos + __popcll(bal & ((1ull << lane) - 1ull))] = b + 64 * u + lane;
+            if (m) {
+                const int at = pos + __popcll(bal & ((1ull << lane) - 1ull));
+                pairs[at] = b + 64 * u + lane;
+                if (sscore) sscore[at] = mx::bf16_to_f32(scores[b + 64 * u + lane]);
+            }
             pos += __popcll(bal);
         }
     }
@@ -147,7 +154,7 @@ struct GArgs {
     uint8_t* hq;             // GATEUP out: (P, Mi/2) MXFP4 h in sorted order
     uint8_t* hs;             //             (P, Mi/32)
     uint16_t* yd;            // DOWN out: (P, H) bf16 at the pair's own index
-    const uint16_t* scores;  // DOWN: (P) bf16 routing weights
+    const float* sscore;     // DOWN: (P) routing weights in sorted pair order
     int a_rows;              // rows of aq / as (T for gate/up, P for down)
 };
 
@@ -231,12 +238,26 @@ __device__ __forceinline__ int weight_row(int rho, int n0, int& proj) {
     return n0 + rho;
 }
 
+// Down epilogue inputs of the lane's two token rows rbase + 32i + lr: the
+// pair index and its routing weight (loaded ahead of the K loop by the
+// kernels that can, so the epilogue waits on no load).
+__device__ __forceinline__ void down_rows(const GArgs& g, int off, int mt, int mrows, int rbase, int lr, int (&pp)[2],
+                                          float (&ss)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int rloc = rbase + 32 * i + lr;
+        pp[i] = rloc < mrows ? g.pairs[off + mt + rloc] : 0;
+        ss[i] = rloc < mrows ? g.sscore[off + mt + rloc] : 0.0f;
+    }
+}
+
 // Epilogue of a 128 x 128 tile (acc[i][j] of the 2 x 2 wave layout):
 // gate/up -> h = silu(g)*u, fp16, MXFP4 rows in sorted pair order; down ->
-// bf16(bf16(y) * score) at the pair's own index.
+// bf16(bf16(y) * score) at the pair's own index (pp / ss from down_rows).
 template <int MODE>
 __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs& g, int n0, int off, int mt,
-                                              int mrows, int rbase, int wn, int lr, int h) {
+                                              int mrows, int rbase, int wn, int lr, int h, const int (&pp)[2],
+                                              const float (&ss)[2]) {
     // acc[i][j] element q of lane l: token wm*64 + 32i + l%32, weight row
     // wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
     if (MODE == MODE_GATEUP) {
@@ -249,7 +270,7 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
             float amax = 0.0f;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                v[q] = mx::round_to_f16(mx::silu_mul(acc[i][0][q], acc[i][1][q]));
+                v[q] = mx::round_to_f16(mx::silu_mul_fast(acc[i][0][q], acc[i][1][q]));
                 amax = fmaxf(amax, fabsf(v[q]));
             }
             amax = fmaxf(amax, __shfl_xor(amax, 32));
@@ -285,22 +306,23 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
         for (int i = 0; i < 2; ++i) {
             const int rloc = rbase + 32 * i + lr;
             if (rloc < mrows) {
-                const int p = g.pairs[off + mt + rloc];
-                const float sc = mx::bf16_to_f32(g.scores[p]);
+                const int p = pp[i];
+                const float sc = ss[i];
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     const int cb = n0 + wn * 64 + 32 * j;   // 32-column block
                     if (cb < H) {
 #pragma unroll
                         for (int q4 = 0; q4 < 4; ++q4) {
-                            uint32_t b[4];
+                            uint32_t b[2];
 #pragma unroll
-                            for (int r = 0; r < 4; ++r) {
-                                const float y = mx::bf16_to_f32(mx::f32_to_bf16_rne(acc[i][j][4 * q4 + r]));
-                                b[r] = mx::f32_to_bf16_rne(y * sc);
+                            for (int r = 0; r < 2; ++r) {
+                                // bf16(bf16(y) * score), two at a time
+                                const uint32_t y2 = mx::f32x2_to_bf16x2(acc[i][j][4 * q4 + 2 * r], acc[i][j][4 * q4 + 2 * r + 1]);
+                                b[r] = mx::f32x2_to_bf16x2(__uint_as_float(y2 << 16) * sc,
+                                                           __uint_as_float(y2 & 0xFFFF0000u) * sc);
                             }
-                            const uint2 d = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
-                            *reinterpret_cast<uint2*>(g.yd + (int64_t)p * H + cb + 8 * q4 + 4 * h) = d;
+                            *reinterpret_cast<uint2*>(g.yd + (int64_t)p * H + cb + 8 * q4 + 4 * h) = make_uint2(b[0], b[1]);
                         }
                     }
                 }
@@ -413,7 +435,10 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_kernel(GArgs g, W w) {
 #pragma unroll
             for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
 
-        tile_epilogue<MODE>(acc, g, n0, off, mt, mrows, wm * 64, wn, lr, h);
+        int pp[2] = {0, 0};
+        float ss[2] = {0.0f, 0.0f};
+        if (MODE == MODE_DOWN) down_rows(g, off, mt, mrows, wm * 64, lr, pp, ss);
+        tile_epilogue<MODE>(acc, g, n0, off, mt, mrows, wm * 64, wn, lr, h, pp, ss);
         __syncthreads();   // LDS buffers are refilled by the next token tile
     }
 }
@@ -577,9 +602,285 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_dma_kernel(GArgs g, W w) 
 #pragma unroll
         for (int half = 0; half < 2; ++half) {
             mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]}, {acc[2 * half + 1][0], acc[2 * half + 1][1]}};
-            tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, wm * 128 + 64 * half, wn, lr, h);
+            int pp[2] = {0, 0};
+            float ss[2] = {0.0f, 0.0f};
+            if (MODE == MODE_DOWN) down_rows(g, off, mt, mrows, wm * 128 + 64 * half, lr, pp, ss);
+            tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, wm * 128 + 64 * half, wn, lr, h, pp, ss);
         }
         __syncthreads();   // the ring is refilled by the next token tile
+    }
+}
+
+// ------------------------------------------------------------------ 256 x 256 tiles, 8 waves
+// Tiles of up to 256 tokens x 256 weight rows (gate/up: the gate and up rows
+// of 128 features; down: 256 output columns), 8 waves in 2 (tokens) x 4
+// (weight rows), a wave owning 128 tokens x 64 weight rows as 4 x 2 MFMA
+// accumulators.  K step 256, so every copied row piece is a whole 128-byte
+// line (global -> LDS by buffer_load ... lds, XOR swizzle of the 16-byte
+// chunks), in a 2-stage ring of 68 KB stages (one workgroup per CU).  The
+// token tile is sized to the expert's count in 64-row steps: only
+// ceil(rows / 64) * 64 token rows are copied, and a wave issues the MFMAs of
+// those of its 32-token blocks that hold routed tokens, so an expert with
+// ~130 tokens costs what ~130 tokens need rather than a full 256-row tile.
+// All tiles of one expert take workgroup numbers of one residue mod 8, i.e.
+// run on one XCD (workgroups are dealt to the 8 XCDs round-robin), so the
+// expert's gathered token rows are fetched into one L2.  Requires
+// Kp % 256 == 0.
+constexpr int X_BM = 256, X_BN = 256;
+constexpr int X_ROWB = 128;                        // bytes per row per K step
+constexpr int X_A = X_BM * X_ROWB;                 // 32 KB of token rows
+constexpr int X_W = X_BN * X_ROWB;                 // 32 KB of weight rows
+constexpr int X_SA = X_BM * 8, X_SW = X_BN * 8;    // 8 scale bytes per row
+constexpr int X_STAGE = X_A + X_W + X_SA + X_SW;   // 68 KB
+constexpr int X_THREADS = 512;
+constexpr int X_TROW = 144;                           // down transpose: bytes per row (128 + 16 of pad)
+constexpr int X_PP = 8 * 128 * X_TROW;                // after the ring / the 8 waves' transpose buffers
+constexpr int X_LDS = X_PP + 8 * X_BM;                // + the down tile's pair indices and weights
+static_assert(X_PP >= 2 * X_STAGE && X_LDS <= 160 * 1024, "x8 LDS layout");
+
+// Per-tile copy plan of one wave: NA token-row blocks (8 rows of 128 bytes
+// each), 4 weight-row blocks and 2 scale copies (32 rows x 8 bytes each).
+struct XCopies {
+    mx::v4u ars, wrs, srs[2];
+    uint32_t avo[4], wvo[4], svo[2], sdst[2];
+    int na;
+};
+
+template <int MODE, class W>
+__device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, int e, int n0, int off, int mt,
+                                        int mrows, int wave, int lane) {
+    const uint32_t cbytes = (uint32_t)g.Kp >> 1, nch = (uint32_t)g.Kp >> 5;
+    const int slot = lane & 7, lrow = lane >> 3;
+    c.na = (mrows + 63) >> 6;
+    auto src_row = [&](int r) {   // token (gate/up) or sorted h row (down) of tile row r
+        const int rc = min(r, mrows - 1);
+        return MODE == MODE_GATEUP ? g.pairs[off + mt + rc] / g.topk : off + mt + rc;
+    };
+    c.ars = mx::buf_rsrc(g.aq, (int64_t)g.a_rows * cbytes);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int r = 64 * j + 8 * wave + lrow;   // block 8j + wave
+        c.avo[j] = (uint32_t)src_row(r) * cbytes + ((slot ^ mx::swz_key128(r)) << 4);
+    }
+    // weight blocks 4*wave + j: rows 32*wave .. +31, one projection
+    int proj;
+    weight_row<MODE>(32 * wave, n0, proj);
+    c.wrs = mx::buf_rsrc(w.p(e, proj), (int64_t)g.Nw * cbytes);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int rho = 32 * wave + 8 * j + lrow;
+        int pj;
+        const int rr = min(weight_row<MODE>(rho, n0, pj), g.Nw - 1);
+        c.wvo[j] = (uint32_t)rr * cbytes + ((slot ^ mx::swz_key128(rho)) << 4);
+    }
+    // scale copies q = 2*wave + j of 2*na (token rows) + 8 (weight rows);
+    // the surplus ones repeat an earlier copy (same bytes, same place)
+    const int nq = 2 * c.na + 8;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int q = (2 * wave + j) % nq;
+        const int row = 32 * (q < 2 * c.na ? q : q - 2 * c.na) + (lane >> 1);
+        if (q < 2 * c.na) {
+            c.srs[j] = mx::buf_rsrc(g.as, (int64_t)g.a_rows * nch);
+            c.svo[j] = (uint32_t)src_row(row) * nch + 4 * (lane & 1);
+            c.sdst[j] = X_A + X_W + 256 * q;
+        } else {
+            int pj;   // one projection per 32-row block: wave-uniform
+            const int rr = min(weight_row<MODE>(row, n0, pj), g.Nw - 1);
+            c.srs[j] = mx::buf_rsrc(w.s(e, pj), (int64_t)g.Nw * nch);
+            c.svo[j] = (uint32_t)rr * nch + 4 * (lane & 1);
+            c.sdst[j] = X_A + X_W + X_SA + 256 * (q - 2 * c.na);
+        }
+    }
+}
+
+// Copies of K step `s` into the stage at LDS address `buf`, part `part` of 4
+// (one token block, one weight block and, in parts 0-1, one scale copy), so a
+// step's copies are spread over the MFMA substeps of the previous one.
+__device__ __forceinline__ void x8_issue(const XCopies& c, uint32_t buf, int s, int part, int wave) {
+    const uint32_t kofs = (uint32_t)s * X_ROWB;
+    if (part < c.na) mx::dma16(c.avo[part], c.ars, kofs, buf + (8 * part + wave) * 1024);
+    mx::dma16(c.wvo[part], c.wrs, kofs, buf + X_A + (4 * wave + part) * 1024);
+    if (part < 2) mx::dma4(c.svo[part], c.srs[part], (uint32_t)s * 8, buf + c.sdst[part]);
+}
+
+// K loop and epilogue of one wave on one token tile; NB = the wave's 32-token
+// blocks holding routed tokens (0..4).
+template <int MODE, int NB>
+__device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_t* smem, uint32_t ring, int n0,
+                                        int off, int mt, int mrows, int wave, int lane) {
+    const int wm = wave >> 2, wn = wave & 3;
+    const int lr = lane & 31, h = lane >> 5;
+    const int key = mx::swz_key128(lr);
+    const int nsteps = g.Kp / 256;
+    mx::v16f acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
+
+    // down: the tile's pair indices and routing weights go to LDS beside the
+    // ring (loaded before the first copies; waiting for them costs nothing
+    // extra, since the first K step waits for those copies anyway)
+    int rp = 0;
+    float rs = 0.0f;
+    const int trow = wave * 64 + lane;
+    if (MODE == MODE_DOWN && trow < mrows) {
+        rp = g.pairs[off + mt + trow];
+        rs = g.sscore[off + mt + trow];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) x8_issue(c, ring, 0, q, wave);
+    if (MODE == MODE_DOWN && trow < X_BM) {
+        reinterpret_cast<int*>(smem + X_PP)[trow] = rp;
+        reinterpret_cast<float*>(smem + X_PP + 4 * X_BM)[trow] = rs;
+    }
+    for (int it = 0; it < nsteps; ++it) {
+        // this wave's copies of step it have landed and its reads of step
+        // it-1 are done; after the barrier every wave's
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const bool more = it + 1 < nsteps;
+        const uint8_t* cur = smem + (it & 1) * X_STAGE;
+        const uint32_t nxt = ring + ((it + 1) & 1) * X_STAGE;
+        const uint8_t* la = cur + (wm * 128 + lr) * X_ROWB;
+        const uint8_t* lw = cur + X_A + (wn * 64 + lr) * X_ROWB;
+        const uint8_t* lsa = cur + X_A + X_W + (wm * 128 + lr) * 8;
+        const uint8_t* lsw = cur + X_A + X_W + X_SA + (wn * 64 + lr) * 8;
+        uint32_t sa[4], sb[2];
+#pragma unroll
+        for (int i = 0; i < NB; ++i) sa[i] = scale_word(lsa + i * 32 * 8, h);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) sb[j] = scale_word(lsw + j * 32 * 8, h);
+        // (reading substep ks+1's operands ahead of substep ks's MFMAs needs a
+        // second operand set, which does not fit beside the accumulators at
+        // two waves per SIMD)
+        uint4 af[1][4], bf[1][2];
+        auto load = [&](int ks, int r) {
+            const int koff = ((2 * ks + h) ^ key) << 4;
+#pragma unroll
+            for (int i = 0; i < NB; ++i) af[r][i] = *reinterpret_cast<const uint4*>(la + koff + i * 32 * X_ROWB);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) bf[r][j] = *reinterpret_cast<const uint4*>(lw + koff + j * 32 * X_ROWB);
+        };
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (more) x8_issue(c, nxt, it + 1, ks, wave);
+            if (NB > 0) {
+                load(ks, 0);
+                const int r = 0;
+                // D[weight row][token]: the weight tile is the MFMA A operand
+#pragma unroll
+                for (int i = 0; i < NB; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        if (ks == 0) acc[i][j] = mfma32<0>(bf[r][j], af[r][i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 1) acc[i][j] = mfma32<1>(bf[r][j], af[r][i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 2) acc[i][j] = mfma32<2>(bf[r][j], af[r][i], acc[i][j], sb[j], sa[i]);
+                        if (ks == 3) acc[i][j] = mfma32<3>(bf[r][j], af[r][i], acc[i][j], sb[j], sa[i]);
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
+    if (MODE == MODE_DOWN) {
+        // bf16(bf16(y) * score) goes through LDS, so that each store
+        // instruction writes 8 whole 128-byte row segments instead of 16
+        // bytes of 32 rows: wave w transposes its 128 x 64 block in its own
+        // X_TROW-pitched buffer, over the ring (free once every wave is past
+        // its last MFMA)
+        __syncthreads();
+        if (NB == 0) return;
+        uint8_t* tb = smem + wave * 128 * X_TROW;
+        const int* lp = reinterpret_cast<const int*>(smem + X_PP);
+        const float* ls = reinterpret_cast<const float*>(smem + X_PP + 4 * X_BM);
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+            const float sc = ls[wm * 128 + 32 * i + lr];
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int q4 = 0; q4 < 4; ++q4) {
+                    uint32_t b[2];
+#pragma unroll
+                    for (int r = 0; r < 2; ++r) {
+                        const uint32_t y2 = mx::f32x2_to_bf16x2(acc[i][j][4 * q4 + 2 * r], acc[i][j][4 * q4 + 2 * r + 1]);
+                        b[r] = mx::f32x2_to_bf16x2(__uint_as_float(y2 << 16) * sc, __uint_as_float(y2 & 0xFFFF0000u) * sc);
+                    }
+                    // element q of block j: column 32j + 8(q/4) + 4h + q%4
+                    *reinterpret_cast<uint2*>(tb + (32 * i + lr) * X_TROW + (32 * j + 8 * q4 + 4 * h) * 2) =
+                        make_uint2(b[0], b[1]);
+                }
+        }
+        // lane: row 8*st + lane/8 of the wave's block, 16 bytes at column
+        // chunk lane%8; per-lane bases, so each step's LDS reads take
+        // immediate offsets
+        const int ch = lane & 7;
+        const int col = n0 + wn * 64 + 8 * ch;
+        const int lim = col < g.Nw ? mrows - wm * 128 - (lane >> 3) : 0;   // rows 8*st < lim are routed
+        const uint8_t* tr = tb + (lane >> 3) * X_TROW + 16 * ch;
+        const int* pr = lp + wm * 128 + (lane >> 3);
+        uint16_t* yc = g.yd + col;
+#pragma unroll
+        for (int st = 0; st < 4 * NB; ++st) {
+            if (8 * st < lim) {
+                const uint4 v = *reinterpret_cast<const uint4*>(tr + 8 * st * X_TROW);
+                *reinterpret_cast<uint4*>(yc + (int64_t)pr[8 * st] * g.Nw) = v;
+            }
+        }
+        return;
+    }
+    if (NB == 0) return;
+    // gate/up: the wave's 128 token rows as two 64-row halves of the 128 x 128 epilogue
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+        if (2 * half >= NB) continue;
+        mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]}, {acc[2 * half + 1][0], acc[2 * half + 1][1]}};
+        const int pp[2] = {0, 0};
+        const float ss[2] = {0.0f, 0.0f};
+        tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, wm * 128 + 64 * half, wn, lr, h, pp, ss);
+    }
+}
+
+template <int MODE, class W>
+__global__ __launch_bounds__(X_THREADS, 1) void grouped_gemm_x8_kernel(GArgs g, W w, int ntiles, int n_exp) {
+    extern __shared__ __align__(16) uint8_t smem[];
+    const int bid = blockIdx.x;
+    const int e = (bid & 7) + 8 * ((bid >> 3) / ntiles);
+    const int nt = (bid >> 3) % ntiles;
+    if (e >= n_exp) return;
+    const int cnt = g.counts[e];
+    if (cnt == 0) return;
+    const int off = g.offs[e];
+    const int n0 = nt * (MODE == MODE_GATEUP ? X_BN / 2 : X_BN);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(mx::lds_addr(smem));
+    for (int mt = 0; mt < cnt; mt += X_BM) {
+        const int mrows = min(X_BM, cnt - mt);
+        XCopies c;
+        x8_plan<MODE>(c, g, w, e, n0, off, mt, mrows, wave, lane);
+        const int nb = min(max((mrows - (wave >> 2) * 128 + 31) >> 5, 0), 4);
+        switch (nb) {
+            case 4: x8_tile<MODE, 4>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+            case 3: x8_tile<MODE, 3>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+            case 2: x8_tile<MODE, 2>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+            case 1: x8_tile<MODE, 1>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+            default: x8_tile<MODE, 0>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+        }
+        // every wave is done with the ring before the next token tile
+        // refills it (and its vmcnt counts only the new copies)
+        if (mt + X_BM < cnt) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
     }
 }
 
@@ -615,7 +916,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* __
 
 // ------------------------------------------------------------------ host
 struct WsLayout {
-    size_t counts, offs, pairs, xq, xs, hq, hs, yd, total;
+    size_t counts, offs, pairs, sscore, xq, xs, hq, hs, yd, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -627,6 +928,7 @@ WsLayout ws_layout(int T, int topk, int n_exp, int H, int Mi) {
     L.counts = o; o = align256(o + sizeof(int) * n_exp);
     L.offs = o;   o = align256(o + sizeof(int) * n_exp);
     L.pairs = o;  o = align256(o + sizeof(int) * P);
+    L.sscore = o; o = align256(o + sizeof(float) * P);
     L.xq = o;     o = align256(o + (size_t)T * (H / 2));
     L.xs = o;     o = align256(o + (size_t)T * (H / 32));
     L.hq = o;     o = align256(o + P * (Mi / 2));
@@ -650,15 +952,17 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
                 "moe_prefill: x/out must be 16-byte and workspace 256-byte aligned");
     const WsLayout L = ws_layout(T, topk, n_exp, H, Mi);
     MXH_REQUIRE(ws_bytes >= L.total, "moe_prefill: workspace of %zu bytes < required %zu", ws_bytes, L.total);
-    static bool attr_set[2][4] = {{false, false, false, false}, {false, false, false, false}};
+    static bool attr_set[2][6] = {};
     constexpr int tw = std::is_same<W, TableW>::value ? 1 : 0;
-    for (int m = 0; m < 4; ++m) {
+    for (int m = 0; m < 6; ++m) {
         if (attr_set[tw][m]) continue;
-        const void* fns[4] = {reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_GATEUP, W>),
+        const void* fns[6] = {reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_GATEUP, W>),
                               reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_DOWN, W>),
                               reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_GATEUP, W>),
-                              reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_DOWN, W>)};
-        const int bytes = m < 2 ? 2 * BUF_BYTES : D_NST * D_STAGE;
+                              reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_DOWN, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_x8_kernel<MODE_GATEUP, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_x8_kernel<MODE_DOWN, W>)};
+        const int bytes = m < 2 ? 2 * BUF_BYTES : m < 4 ? D_NST * D_STAGE : X_LDS;
         hipError_t e = hipFuncSetAttribute(fns[m], hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         MXH_REQUIRE(e == hipSuccess, "moe_prefill: cannot reserve %d B of LDS: %s", bytes, hipGetErrorString(e));
         attr_set[tw][m] = true;
@@ -669,7 +973,9 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     int* pairs = reinterpret_cast<int*>(ws + L.pairs);
     const int P = T * topk;
 
-    hipLaunchKernelGGL(route_kernel, dim3(n_exp), dim3(256), 0, st, topi, P, n_exp, counts, offs, pairs);
+    float* sscore = reinterpret_cast<float*>(ws + L.sscore);
+    hipLaunchKernelGGL(route_kernel, dim3(n_exp), dim3(256), 0, st, topi, P, n_exp, counts, offs, pairs, scores,
+                       sscore);
     int rc = mxh::launch_status("moe_prefill route");
     if (rc != MXFP4_OK) return rc;
     rc = mxh::quantize_rows_impl(x, MXFP4_DT_BF16, 1, H, T, H, H, ws + L.xq, ws + L.xs, st);
@@ -683,14 +989,22 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     g.hq = ws + L.hq;
     g.hs = ws + L.hs;
     g.yd = reinterpret_cast<uint16_t*>(ws + L.yd);
-    g.scores = scores;
+    g.sscore = sscore;
 
     g.aq = ws + L.xq;
     g.as = ws + L.xs;
     g.Kp = H;
     g.Nw = Mi;
     g.a_rows = T;
-    if (H % DK == 0)
+    // the copy kernels address operands with 32-bit byte offsets
+    const bool fit_gu = (int64_t)T * (H / 2) < (1ll << 32) && (int64_t)Mi * (H / 2) < (1ll << 32);
+    const bool fit_dn = (int64_t)P * (Mi / 2) < (1ll << 32) && (int64_t)H * (Mi / 2) < (1ll << 32);
+    const int xgroups = (n_exp + 7) / 8;
+    if (H % 256 == 0 && fit_gu) {
+        const int ntiles = (Mi + X_BN / 2 - 1) / (X_BN / 2);
+        hipLaunchKernelGGL((grouped_gemm_x8_kernel<MODE_GATEUP, W>), dim3(8 * xgroups * ntiles), dim3(X_THREADS),
+                           X_LDS, st, g, w, ntiles, n_exp);
+    } else if (H % DK == 0 && fit_gu)
         hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256),
                            D_NST * D_STAGE, st, g, w);
     else
@@ -704,7 +1018,11 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     g.Kp = Mi;
     g.Nw = H;
     g.a_rows = P;
-    if (Mi % DK == 0)
+    if (Mi % 256 == 0 && fit_dn) {
+        const int ntiles = (H + X_BN - 1) / X_BN;
+        hipLaunchKernelGGL((grouped_gemm_x8_kernel<MODE_DOWN, W>), dim3(8 * xgroups * ntiles), dim3(X_THREADS),
+                           X_LDS, st, g, w, ntiles, n_exp);
+    } else if (Mi % DK == 0 && fit_dn)
         hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256),
                            D_NST * D_STAGE, st, g, w);
     else
@@ -728,7 +1046,7 @@ extern "C" int mxfp4_moe_group(const int64_t* topi, int T, int topk, int n_exper
     MXH_REQUIRE(T > 0 && topk > 0 && (int64_t)T * topk < (1ll << 30), "moe_group: T=%d topk=%d", T, topk);
     MXH_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts, "moe_group: n_experts=%d (1..%d)", n_experts, kMaxExperts);
     hipLaunchKernelGGL(route_kernel, dim3(n_experts), dim3(256), 0, mxh::as_stream(stream), topi, T * topk, n_experts,
-                       counts, offsets, pairs);
+                       counts, offsets, pairs, nullptr, nullptr);
     return mxh::launch_status("moe_group");
 }
 

@@ -67,12 +67,19 @@ __device__ __forceinline__ float e8m0_inv_scale(uint32_t code) {
 }
 
 // E2M1 code of x = v / scale: nearest magnitude, ties up, clamp at 6,
-// sign bit from (x < 0) (quant/fp4_format.py:24-46).
+// sign bit from (x < 0) (quant/fp4_format.py:24-46).  The magnitude code is
+// the count of the thresholds 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5 that |x|
+// reaches.  From 1 up the E2M1 grid is a float with one mantissa bit, so
+// there the count is |x| rounded half-up to one mantissa bit (add half an
+// ulp of that grid, 2^21, to the fp32 bits and keep exponent + top mantissa
+// bit) minus the code offset, clamped to [2, 7]; below 1 it is the first two
+// comparisons.  Equal to the plain threshold count on all 2^32 inputs (NaN
+// -> 0, -0 -> 0), in about half the instructions.
 __device__ __forceinline__ uint32_t e2m1_code(float x) {
-    float a = __builtin_fabsf(x);
-    uint32_t m = (uint32_t)(a >= 0.25f) + (uint32_t)(a >= 0.75f) + (uint32_t)(a >= 1.25f) +
-                 (uint32_t)(a >= 1.75f) + (uint32_t)(a >= 2.5f) + (uint32_t)(a >= 3.5f) +
-                 (uint32_t)(a >= 5.0f);
+    const float a = __builtin_fabsf(x);
+    const int hi = min(max((int)((__float_as_uint(a) + 0x200000u) >> 22) - 252, 2), 7);
+    const uint32_t lo = (uint32_t)(a >= 0.25f) + (uint32_t)(a >= 0.75f);
+    const uint32_t m = a >= 1.0f ? (uint32_t)hi : lo;
     return m | (x < 0.0f ? 8u : 0u);
 }
 
@@ -167,6 +174,15 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builti
 __device__ __forceinline__ float round_to_f16(float f) { return (float)(_Float16)f; }
 
 // fp32 -> bf16 bits, round to nearest even (finite inputs).
+// Two fp32 -> bf16 (RNE, as f32_to_bf16_rne for every non-NaN input) in one
+// v_cvt_pk_bf16_f32: a in the low half, b in the high half.
+__device__ __forceinline__ uint32_t f32x2_to_bf16x2(float a, float b) {
+    typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    const f2 v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf2));
+}
+
 __device__ __forceinline__ uint16_t f32_to_bf16_rne(float f) {
     uint32_t u = __float_as_uint(f);
     u += 0x7FFFu + ((u >> 16) & 1u);
@@ -184,7 +200,9 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 // silu_mul on the hardware exp2 and reciprocal (a few ulp from silu_mul):
 // for the fused decode kernels, whose h is split into three E4M3 terms (a
-// relative resolution of 2^-12) rather than rounded to a 4-bit code.
+// relative resolution of 2^-12), and the prefill MoE, whose h is rounded to
+// fp16 and then to 4-bit codes, which a few-ulp change moves only for an h
+// within ~1e-6 (relative) of a rounding threshold.
 __device__ __forceinline__ float silu_mul_fast(float g, float u) {
 #pragma clang fp contract(off)
     const float e = __builtin_amdgcn_exp2f(-g * 1.44269504088896341f);   // exp(-g); +inf for g < -88

@@ -99,6 +99,8 @@ def test_moe_group_matches_stable_sort():
     (300, 8, 16, 1024, 256, False),
     (260, 2, 4, 512, 160, True),
     (513, 4, 8, 256, 64, True),
+    (700, 4, 8, 512, 512, True),
+    (64, 4, 8, 640, 256, False),
 ])
 def test_moe_compute_vs_oracle(dext, T, k, n_exp, H, Mi, skew):
     stack = make_stack(dext, n_exp, H, Mi, seed=70 + H + Mi)
