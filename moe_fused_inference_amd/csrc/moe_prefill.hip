@@ -10,8 +10,8 @@
 // which issues 3 launches per active expert and syncs on torch.where, with
 // five stream-ordered launches and no host synchronisation:
 //
-//   1. route_kernel       one workgroup per expert: counts of the ids equal
-//                         to / below the expert, then a stable ballot
+//   1. route_kernel       one workgroup per two experts: counts of the ids
+//                         equal to / below each expert, then a stable ballot
 //                         compaction of the (token, slot) pairs routed to it
 //                         in row-major order -- exactly torch.where's order.
 //   2. quantize_rows      h (T, H) bf16 -> fp16-rounded -> MXFP4, once per
@@ -61,70 +61,125 @@ constexpr int kMaxTopk = 32;
 enum { MODE_GATEUP = 0, MODE_DOWN = 1 };
 
 // ------------------------------------------------------------------ routing
-// Workgroup E lists the pairs routed to expert E.  Each wave owns a
-// contiguous quarter of the row-major (token, slot) pairs: a first coalesced
-// pass counts its matches (ballot) and its valid ids below E; the waves
-// exchange the counts once through LDS; a second pass writes the matches in
-// order (ballot rank), so the result is a stable sort by expert id.  With
-// `sscore`, the pair's routing weight is written beside it in sorted order
-// (fp32 of the bf16 score), so the down epilogue needs no dependent load.
-__global__ __launch_bounds__(256) void route_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
-                                                    int* __restrict__ counts, int* __restrict__ offs,
-                                                    int* __restrict__ pairs, const uint16_t* __restrict__ scores,
-                                                    float* __restrict__ sscore) {
-    __shared__ int s_eq[4], s_lt[4];
+// Workgroup b lists the pairs routed to experts 2b and 2b+1 (each id is
+// read once per pass for two experts: half the traffic of one expert per
+// workgroup, at twice the compare-and-ballot work per id, which is what
+// bounds a workgroup here).  Each of the 8 waves owns a contiguous eighth of
+// the row-major (token, slot) pairs: a first coalesced pass counts, per expert,
+// its matches (ballot) and its valid ids below the first expert; the waves
+// exchange the counts once through LDS; a second pass writes each expert's
+// matches in order (ballot rank), so the result is a stable sort by expert
+// id.  With `sscore`, the pair's routing weight is written beside it in
+// sorted order (fp32 of the bf16 score), so the down epilogue needs no
+// dependent load.
+constexpr int kRouteEpw = 2;        // experts per workgroup
+constexpr int kRouteWaves = 8;
+__global__ __launch_bounds__(64 * kRouteWaves) void route_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
+                                                                 int* __restrict__ counts, int* __restrict__ offs,
+                                                                 int* __restrict__ pairs,
+                                                                 const uint16_t* __restrict__ scores,
+                                                                 float* __restrict__ sscore) {
+    __shared__ int s_eq[kRouteWaves][kRouteEpw], s_lt[kRouteWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int E = blockIdx.x;
-    const int per_wave = ((P + 255) / 256) * 64;
+    const int E0 = blockIdx.x * kRouteEpw;
+    const int per_wave = ((P + 64 * kRouteWaves - 1) / (64 * kRouteWaves)) * 64;
     const int w0 = min(wave * per_wave, P);
     const int w1 = min(w0 + per_wave, P);
-    constexpr int U = 8;   // chunks of 64 ids in flight per pass step
-    int n_eq = 0, n_lt = 0;
+    constexpr int U = 16;  // chunks of 64 ids in flight per pass step (all of a wave's at P = 16384)
+    int n_eq[kRouteEpw];
+#pragma unroll
+    for (int k = 0; k < kRouteEpw; ++k) n_eq[k] = 0;
+    int n_lt = 0;
     for (int b = w0; b < w1; b += 64 * U) {
         int64_t id[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int u = 0; u < U; ++u) {   // clamped, unconditional loads: all U in flight at once
             const int p = b + 64 * u + lane;
-            id[u] = p < w1 ? topi[p] : -1;
+            const int64_t v = topi[min(p, P - 1)];
+            id[u] = p < w1 ? v : -1;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            n_eq += __popcll(__ballot(id[u] == (int64_t)E));
-            n_lt += (id[u] >= 0 && id[u] < (int64_t)E) ? 1 : 0;
+#pragma unroll
+            for (int k = 0; k < kRouteEpw; ++k)   // (ids >= n_exp match no expert)
+                n_eq[k] += E0 + k < n_exp ? __popcll(__ballot(id[u] == (int64_t)(E0 + k))) : 0;
+            n_lt += (id[u] >= 0 && id[u] < (int64_t)E0) ? 1 : 0;
         }
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) n_lt += __shfl_xor(n_lt, o);
     if (lane == 0) {
-        s_eq[wave] = n_eq;
+#pragma unroll
+        for (int k = 0; k < kRouteEpw; ++k) s_eq[wave][k] = n_eq[k];
         s_lt[wave] = n_lt;
     }
     __syncthreads();
-    const int off = s_lt[0] + s_lt[1] + s_lt[2] + s_lt[3];
-    int pos = off;
-    for (int w = 0; w < wave; ++w) pos += s_eq[w];
+    // expert E0+k starts after the valid ids below E0 and the matches of
+    // E0 .. E0+k-1; this wave's matches of it after those of earlier waves
+    int base = 0;
+    for (int w = 0; w < kRouteWaves; ++w) base += s_lt[w];
+    int pos[kRouteEpw];
+#pragma unroll
+    for (int k = 0; k < kRouteEpw; ++k) {
+        int tot = 0, before = 0;
+        for (int w = 0; w < kRouteWaves; ++w) {
+            tot += s_eq[w][k];
+            before += w < wave ? s_eq[w][k] : 0;
+        }
+        pos[k] = base + before;
+        if (threadIdx.x == 0 && E0 + k < n_exp) {
+            counts[E0 + k] = tot;
+            offs[E0 + k] = base;
+        }
+        base += tot;
+    }
+    // second pass, in segments of 64*U ids: the wave's matches of the
+    // segment, in order and grouped by expert, into its own LDS list, then
+    // out with coalesced stores (one store per match would cost a memory
+    // instruction per ballot)
+    __shared__ int2 s_list[kRouteWaves][64 * U];
+    int2* list = s_list[wave];
     for (int b = w0; b < w1; b += 64 * U) {
         int64_t id[U];
+        uint16_t sc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int p = b + 64 * u + lane;
-            id[u] = p < w1 ? topi[p] : -1;
+            const int64_t v = topi[min(p, P - 1)];
+            id[u] = p < w1 ? v : -1;
+            sc[u] = sscore ? scores[min(p, P - 1)] : (uint16_t)0;
+        }
+        int cnt[kRouteEpw], kb[kRouteEpw], rank[kRouteEpw];
+        int kacc = 0;
+#pragma unroll
+        for (int k = 0; k < kRouteEpw; ++k) {
+            cnt[k] = 0;
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                cnt[k] += E0 + k < n_exp ? __popcll(__ballot(id[u] == (int64_t)(E0 + k))) : 0;
+            kb[k] = kacc;
+            kacc += cnt[k];
+            rank[k] = 0;
         }
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const bool m = id[u] == (int64_t)E;
-            const unsigned long long bal = __ballot(m);
-            if (m) {
-                const int at = pos + __popcll(bal & ((1ull << lane) - 1ull));
-                pairs[at] = b + 64 * u + lane;
-                if (sscore) sscore[at] = mx::bf16_to_f32(scores[b + 64 * u + lane]);
+#pragma unroll
+            for (int k = 0; k < kRouteEpw; ++k) {
+                const bool m = E0 + k < n_exp && id[u] == (int64_t)(E0 + k);
+                const unsigned long long bal = __ballot(m);
+                if (m) list[kb[k] + rank[k] + __popcll(bal & ((1ull << lane) - 1ull))] = make_int2(b + 64 * u + lane, (int)sc[u]);
+                rank[k] += __popcll(bal);
             }
-            pos += __popcll(bal);
         }
-    }
-    if (threadIdx.x == 0) {
-        counts[E] = s_eq[0] + s_eq[1] + s_eq[2] + s_eq[3];
-        offs[E] = off;
+#pragma unroll
+        for (int k = 0; k < kRouteEpw; ++k) {
+            for (int q = lane; q < cnt[k]; q += 64) {
+                const int2 v = list[kb[k] + q];
+                pairs[pos[k] + q] = v.x;
+                if (sscore) sscore[pos[k] + q] = mx::bf16_to_f32((uint16_t)v.y);
+            }
+            pos[k] += cnt[k];
+        }
     }
 }
 
@@ -257,15 +312,15 @@ __device__ __forceinline__ void down_rows(const GArgs& g, int off, int mt, int m
 template <int MODE>
 __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs& g, int n0, int off, int mt,
                                               int mrows, int rbase, int wn, int lr, int h, const int (&pp)[2],
-                                              const float (&ss)[2]) {
-    // acc[i][j] element q of lane l: token wm*64 + 32i + l%32, weight row
-    // wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
+                                              const float (&ss)[2], int istride = 32) {
+    // acc[i][j] element q of lane l: token rbase + istride*i + l%32, weight
+    // row wn*64 + 32j + 8(q/4) + 4h + q%4 of the tile
     if (MODE == MODE_GATEUP) {
         const int fb = n0 + 32 * wn;           // first feature of this wave's 32-block
         const int Mi = g.Nw;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int rloc = rbase + 32 * i + lr;
+            const int rloc = rbase + istride * i + lr;
             float v[16];
             float amax = 0.0f;
 #pragma unroll
@@ -304,7 +359,7 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
         const int H = g.Nw;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int rloc = rbase + 32 * i + lr;
+            const int rloc = rbase + istride * i + lr;
             if (rloc < mrows) {
                 const int p = pp[i];
                 const float sc = ss[i];
@@ -746,13 +801,16 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         const bool more = it + 1 < nsteps;
         const uint8_t* cur = smem + (it & 1) * X_STAGE;
         const uint32_t nxt = ring + ((it + 1) & 1) * X_STAGE;
-        const uint8_t* la = cur + (wm * 128 + lr) * X_ROWB;
+        // token block i of wave (wm, wn) is tile block 2i + wm: the two waves
+        // of a SIMD share the routed rows, so each one's MFMAs run while the
+        // other waits on its operand reads
+        const uint8_t* la = cur + (32 * wm + lr) * X_ROWB;
         const uint8_t* lw = cur + X_A + (wn * 64 + lr) * X_ROWB;
-        const uint8_t* lsa = cur + X_A + X_W + (wm * 128 + lr) * 8;
+        const uint8_t* lsa = cur + X_A + X_W + (32 * wm + lr) * 8;
         const uint8_t* lsw = cur + X_A + X_W + X_SA + (wn * 64 + lr) * 8;
         uint32_t sa[4], sb[2];
 #pragma unroll
-        for (int i = 0; i < NB; ++i) sa[i] = scale_word(lsa + i * 32 * 8, h);
+        for (int i = 0; i < NB; ++i) sa[i] = scale_word(lsa + i * 64 * 8, h);
 #pragma unroll
         for (int j = 0; j < 2; ++j) sb[j] = scale_word(lsw + j * 32 * 8, h);
         // (reading substep ks+1's operands ahead of substep ks's MFMAs needs a
@@ -762,7 +820,7 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         auto load = [&](int ks, int r) {
             const int koff = ((2 * ks + h) ^ key) << 4;
 #pragma unroll
-            for (int i = 0; i < NB; ++i) af[r][i] = *reinterpret_cast<const uint4*>(la + koff + i * 32 * X_ROWB);
+            for (int i = 0; i < NB; ++i) af[r][i] = *reinterpret_cast<const uint4*>(la + koff + i * 64 * X_ROWB);
 #pragma unroll
             for (int j = 0; j < 2; ++j) bf[r][j] = *reinterpret_cast<const uint4*>(lw + koff + j * 32 * X_ROWB);
         };
@@ -803,7 +861,7 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         const float* ls = reinterpret_cast<const float*>(smem + X_PP + 4 * X_BM);
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
-            const float sc = ls[wm * 128 + 32 * i + lr];
+            const float sc = ls[64 * i + 32 * wm + lr];
 #pragma unroll
             for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -819,33 +877,35 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
                         make_uint2(b[0], b[1]);
                 }
         }
-        // lane: row 8*st + lane/8 of the wave's block, 16 bytes at column
-        // chunk lane%8; per-lane bases, so each step's LDS reads take
-        // immediate offsets
+        // lane: buffer row 8*st + lane/8 (tile row 64*(st/4) + 32*wm +
+        // 8*(st%4) + lane/8), 16 bytes at column chunk lane%8; per-lane
+        // bases, so each step's LDS reads take immediate offsets
         const int ch = lane & 7;
         const int col = n0 + wn * 64 + 8 * ch;
-        const int lim = col < g.Nw ? mrows - wm * 128 - (lane >> 3) : 0;   // rows 8*st < lim are routed
+        const int lim = col < g.Nw ? mrows - 32 * wm - (lane >> 3) : 0;   // tile rows r < lim + 32*wm + lane/8 are routed
         const uint8_t* tr = tb + (lane >> 3) * X_TROW + 16 * ch;
-        const int* pr = lp + wm * 128 + (lane >> 3);
+        const int* pr = lp + 32 * wm + (lane >> 3);
         uint16_t* yc = g.yd + col;
 #pragma unroll
         for (int st = 0; st < 4 * NB; ++st) {
-            if (8 * st < lim) {
+            const int toff = 64 * (st >> 2) + 8 * (st & 3);   // tile row - (32*wm + lane/8)
+            if (toff < lim) {
                 const uint4 v = *reinterpret_cast<const uint4*>(tr + 8 * st * X_TROW);
-                *reinterpret_cast<uint4*>(yc + (int64_t)pr[8 * st] * g.Nw) = v;
+                *reinterpret_cast<uint4*>(yc + (int64_t)pr[toff] * g.Nw) = v;
             }
         }
         return;
     }
     if (NB == 0) return;
-    // gate/up: the wave's 128 token rows as two 64-row halves of the 128 x 128 epilogue
+    // gate/up: the wave's token blocks in pairs (tile rows 128*half + 32*wm
+    // + 64*i' + lane%32) through the 128 x 128 epilogue
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         if (2 * half >= NB) continue;
         mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]}, {acc[2 * half + 1][0], acc[2 * half + 1][1]}};
         const int pp[2] = {0, 0};
         const float ss[2] = {0.0f, 0.0f};
-        tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, wm * 128 + 64 * half, wn, lr, h, pp, ss);
+        tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, 128 * half + 32 * wm, wn, lr, h, pp, ss, 64);
     }
 }
 
@@ -867,7 +927,8 @@ __global__ __launch_bounds__(X_THREADS, 1) void grouped_gemm_x8_kernel(GArgs g, 
         const int mrows = min(X_BM, cnt - mt);
         XCopies c;
         x8_plan<MODE>(c, g, w, e, n0, off, mt, mrows, wave, lane);
-        const int nb = min(max((mrows - (wave >> 2) * 128 + 31) >> 5, 0), 4);
+        // the wave's token blocks 2i + wm (i < nb) holding routed rows
+        const int nb = min(((mrows + 31) / 32 - (wave >> 2) + 1) >> 1, 4);
         switch (nb) {
             case 4: x8_tile<MODE, 4>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
             case 3: x8_tile<MODE, 3>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
@@ -974,7 +1035,8 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     const int P = T * topk;
 
     float* sscore = reinterpret_cast<float*>(ws + L.sscore);
-    hipLaunchKernelGGL(route_kernel, dim3(n_exp), dim3(256), 0, st, topi, P, n_exp, counts, offs, pairs, scores,
+    hipLaunchKernelGGL(route_kernel, dim3((n_exp + kRouteEpw - 1) / kRouteEpw), dim3(64 * kRouteWaves), 0, st, topi, P,
+                       n_exp, counts, offs, pairs, scores,
                        sscore);
     int rc = mxh::launch_status("moe_prefill route");
     if (rc != MXFP4_OK) return rc;
@@ -1045,7 +1107,8 @@ extern "C" int mxfp4_moe_group(const int64_t* topi, int T, int topk, int n_exper
     MXH_REQUIRE(topi && counts && offsets && pairs, "moe_group: null pointer");
     MXH_REQUIRE(T > 0 && topk > 0 && (int64_t)T * topk < (1ll << 30), "moe_group: T=%d topk=%d", T, topk);
     MXH_REQUIRE(n_experts > 0 && n_experts <= kMaxExperts, "moe_group: n_experts=%d (1..%d)", n_experts, kMaxExperts);
-    hipLaunchKernelGGL(route_kernel, dim3(n_experts), dim3(256), 0, mxh::as_stream(stream), topi, T * topk, n_experts,
+    hipLaunchKernelGGL(route_kernel, dim3((n_experts + kRouteEpw - 1) / kRouteEpw), dim3(64 * kRouteWaves), 0,
+                       mxh::as_stream(stream), topi, T * topk, n_experts,
                        counts, offsets, pairs, nullptr, nullptr);
     return mxh::launch_status("moe_group");
 }

@@ -71,13 +71,15 @@ def route(g, T, n_exp, k, skew=False):
     return ti, tv.bfloat16()          # int64 ids, bf16 scores (runtime/model_runner_v2.py:100-106)
 
 
-def test_moe_group_matches_stable_sort():
+@pytest.mark.parametrize("T,k,n", [(333, 8, 128), (1000, 4, 6), (4096, 8, 130)])
+def test_moe_group_matches_stable_sort(T, k, n):
     g = torch.Generator(device=DEV)
     g.manual_seed(1)
-    T, k, n = 333, 8, 128
     topi = torch.randint(0, n, (T, k), generator=g, device=DEV)
     topi[5, 3] = -1
     topi[17, 0] = n + 7          # out of range: left out
+    topi[30, 1] = n              # the ids next to the last expert match none
+    topi[31, 2] = n + 1
     counts, offs, pairs = moe_layer.moe_group(topi, n)
     torch.cuda.synchronize()
     flat = np_(topi).reshape(-1)
