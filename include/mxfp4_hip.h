@@ -167,6 +167,22 @@ int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, 
                          float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
                          int max_pos, void* workspace, size_t workspace_bytes, void* stream);
 
+/* mxfp4_attn_decode_fused: mxfp4_qk_norm_rope_kv followed by
+ * mxfp4_attn_decode_mx in one pass over the cache, bit-exact to that pair
+ * (same q, cache bytes, sc and outputs): qkv fp32 (M, (Hq + 2 Hkv) * D) are
+ * the step's projections, the q heads are normalised and rotated inside the
+ * attention kernel and the step's k / v rows (positions *dpos .. *dpos+M-1)
+ * are encoded there, used for the scores and written to kvk / kvv.  It has
+ * no single counterpart in the reference, whose step runs q_norm / k_norm /
+ * RoPE (runtime/model_runner_v2.py:155-163), kv_write and attn_decode
+ * (src/ext/mxfp4_decode.cu:352-490) as separate launches; it saves a launch
+ * and a memory round trip per layer.  M <= 16, D = 128; codec as
+ * mxfp4_qk_norm_rope_kv; workspace as mxfp4_attn_decode. */
+int mxfp4_attn_decode_fused(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                            float theta, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos, float* sc, float* o,
+                            uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, int codec,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * KV write: k, v bf16 (M, Hkv, D) -> the reference's E4M3 bytes (rounding
  * half away from zero, >= 248 saturating to 0x7F) at rows dpos+m < max_pos

@@ -54,6 +54,8 @@ SIGNATURES = {
                                  _c_p, _c_sz, _c_p]),
     "mxfp4_attn_decode_mx": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i,
                                     _c_p, _c_sz, _c_p]),
+    "mxfp4_attn_decode_fused": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_p, _c_p, _c_p,
+                                       _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),
     "mxfp4_kv_write": (_c_i, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_moe_group": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),
     "mxfp4_route_topk": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p]),

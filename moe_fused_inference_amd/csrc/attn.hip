@@ -26,6 +26,7 @@
 // outputs must match it: rounding half away from zero, |v| >= 248 saturating
 // to 0x7F, subnormal codes read as m * 2^-6 (standard E4M3: m * 2^-9) and
 // exponent-15 codes read as 56 * (8 + m).
+#include "head_rope.h"
 #include "mx_device.h"
 #include "mx_host.h"
 #include "kv_codec.h"
@@ -42,6 +43,20 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_floa
 
 constexpr int kPart = 132;       // floats per partial record: max, sum, 128 column sums, pad
 constexpr int kMaxChunks = 1024; // max_pos <= 65536
+constexpr int kMaxFusedM = 16;   // tokens per call of the fused entry (the decode step's M)
+
+// The fused entry's extra inputs: the fp32 q|k|v projection rows (M, (Hq +
+// 2 Hkv) D), the q/k RMSNorm weights, RoPE theta and the KV byte codec; the
+// cache is written through kvk_w / kvv_w.
+struct QkvIn {
+    const float* qkv;
+    const uint16_t* qw;
+    const uint16_t* kw;
+    float eps, theta;
+    int codec;
+    uint8_t* kvk_w;
+    uint8_t* kvv_w;
+};
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
@@ -58,11 +73,15 @@ __device__ __forceinline__ mx::v4f mfma_bf16(uint4 a, uint4 b, mx::v4f c) {
 // codec, 840 included, is a bf16 value, so this is exact.
 __device__ __forceinline__ uint32_t kv_bf16(uint32_t b) { return __float_as_uint(e4m3_ref_decode(b)) >> 16; }
 __device__ __forceinline__ uint32_t pack_bf16(uint32_t lo, uint32_t hi) { return lo | (hi << 16); }
-__device__ __forceinline__ uint4 kv8_bf16(uint2 w) {
-    return make_uint4(pack_bf16(kv_bf16(w.x & 0xFFu), kv_bf16((w.x >> 8) & 0xFFu)),
-                      pack_bf16(kv_bf16((w.x >> 16) & 0xFFu), kv_bf16(w.x >> 24)),
-                      pack_bf16(kv_bf16(w.y & 0xFFu), kv_bf16((w.y >> 8) & 0xFFu)),
-                      pack_bf16(kv_bf16((w.y >> 16) & 0xFFu), kv_bf16(w.y >> 24)));
+// The same through a 256-entry LDS table of the codec's bf16 bits (lut[b]
+// = kv_bf16(b), built once per workgroup): one LDS read per byte instead of
+// the codec's ~12 instructions.
+__device__ __forceinline__ uint32_t kv_lut(const uint16_t* lut, uint32_t b) { return lut[b & 0xFFu]; }
+__device__ __forceinline__ uint4 kv8_bf16(const uint16_t* lut, uint2 w) {
+    return make_uint4(pack_bf16(kv_lut(lut, w.x), kv_lut(lut, w.x >> 8)),
+                      pack_bf16(kv_lut(lut, w.x >> 16), kv_lut(lut, w.x >> 24)),
+                      pack_bf16(kv_lut(lut, w.y), kv_lut(lut, w.y >> 8)),
+                      pack_bf16(kv_lut(lut, w.y >> 16), kv_lut(lut, w.y >> 24)));
 }
 
 // Workgroup (64-position chunk, kv head g, MT consecutive tokens): R = 16*RT
@@ -78,13 +97,21 @@ __device__ __forceinline__ uint4 kv8_bf16(uint2 w) {
 //  4. O = P V on MFMA with p split into bf16 high + low parts (the low part
 //     carries p - high exactly enough that the product is fp32-accurate);
 //  -> one record (max, sum, 128 column sums) per (token, head, chunk).
-template <int G, int RT>
+//
+// FUSED: q and the step's new K / V rows come from the fp32 projections
+// instead (the qk_rope_kv_kernel arithmetic, head_rope.h and kv_codec.h, so
+// the bits are the same): each workgroup normalises and rotates the q rows
+// of its heads into LDS, and a workgroup whose chunk holds positions of this
+// step (dpos .. dpos+M-1) encodes those tokens' k / v rows of its kv head,
+// uses them in place of the cache bytes, which are not written yet, and
+// writes the rows of its own tokens to the cache.
+template <int G, int RT, bool FUSED>
 __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __restrict__ q,
-                                                           const uint8_t* __restrict__ kvk,
-                                                           const uint8_t* __restrict__ kvv, float* __restrict__ sc,
+                                                           const uint8_t* kvk,   // FUSED writes rows of it
+                                                           const uint8_t* kvv, float* __restrict__ sc,
                                                            float* __restrict__ part, const int32_t* __restrict__ dpos,
                                                            int M, int Hq, int Hkv, int max_pos, int nchunk,
-                                                           float invsqrt) {
+                                                           float invsqrt, QkvIn fz) {
     constexpr int R = 16 * RT;
     constexpr int MT = R / G;
     static_assert(R % G == 0 && MT >= 1, "rows hold whole tokens");
@@ -99,6 +126,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
     __shared__ __align__(16) uint16_t plo[R][kChunk + 8];    // p - high, bf16
     __shared__ float red[4][R];
     __shared__ float rstat[2][R];
+    __shared__ uint16_t lut[256];
+    lut[tid] = (uint16_t)kv_bf16((uint32_t)tid);   // 256 threads: one entry each
     // ---- 1. loads
     uint2 kraw[4];
     {
@@ -117,26 +146,131 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                 for (int t = 0; t < 8; ++t)
                     vraw[c][kt][t] = vc[(int64_t)(s0 + min(kt * 32 + lq * 8 + t, rowmax)) * rs + c * 16];
     }
-    for (int i = tid; i < R * 16; i += 256) {
-        const int r = i >> 4, c = i & 15;
-        const int m = m0 + r / G;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (m < M) v = *reinterpret_cast<const uint4*>(q + ((int64_t)m * Hq + g * G + r % G) * kD + c * 8);
-        *reinterpret_cast<uint4*>(&qs[r][c * 8]) = v;
+    const int base = *dpos;
+    if (!FUSED) {
+        for (int i = tid; i < R * 16; i += 256) {
+            const int r = i >> 4, c = i & 15;
+            const int m = m0 + r / G;
+            uint4 v = make_uint4(0, 0, 0, 0);
+            if (m < M) v = *reinterpret_cast<const uint4*>(q + ((int64_t)m * Hq + g * G + r % G) * kD + c * 8);
+            *reinterpret_cast<uint4*>(&qs[r][c * 8]) = v;
+        }
+    }
+    // FUSED: this step's k / v rows that fall in the chunk, [n_lo, n_hi)
+    __shared__ __align__(16) uint8_t knew[FUSED ? kChunk : 1][kD];
+    __shared__ __align__(16) uint8_t vnew[FUSED ? kChunk : 1][kD];
+    const int n_lo = max(base, s0), n_hi = min(min(base + M, s0 + kChunk), max_pos);
+    if (FUSED) {
+        const int nh = Hq + 2 * Hkv;
+        // every projection value the wave needs is loaded first (one memory
+        // round trip, under the K / V loads above): q rows r = wave + 4i,
+        // and the tasks t = wave + 4j of the step's new rows in this chunk
+        // (task t: row n_lo + t/2, its k for even t, its v for odd t)
+        constexpr int QR = (R + 3) / 4;
+        constexpr int NR = (2 * kMaxFusedM + 3) / 4;
+        float qa[QR], qb[QR], ka[NR], kb[NR];
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const int r = wave + 4 * i, m = m0 + r / G;
+            qa[i] = qb[i] = 0.0f;
+            if (r < R && m < M) {   // wave-uniform
+                const float* row = fz.qkv + ((int64_t)m * nh + g * G + r % G) * kD;
+                qa[i] = row[lane];
+                qb[i] = row[lane + 64];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int t = wave + 4 * j, p = n_lo + (t >> 1);
+            ka[j] = kb[j] = 0.0f;
+            if (p < n_hi) {
+                const float* row = fz.qkv + ((int64_t)(p - base) * nh + (t & 1 ? Hq + Hkv : Hq) + g) * kD;
+                ka[j] = row[lane];
+                kb[j] = row[lane + 64];
+            }
+        }
+        // q: RMSNorm + RoPE at the token's position, bf16 into LDS
+        int cs_m = -1;
+        float2 cs = make_float2(1.0f, 0.0f);
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const int r = wave + 4 * i, m = m0 + r / G;
+            if (r >= R) break;
+            uint16_t ba = 0, bb = 0;
+            if (m < M) {   // wave-uniform
+                if (m != cs_m) {
+                    cs = hr::rope_cs(fz.theta, lane, base + m);
+                    cs_m = m;
+                }
+                hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(fz.qw[lane]), mx::bf16_to_f32(fz.qw[lane + 64]), fz.eps, cs,
+                              ba, bb);
+            }
+            qs[r][lane] = ba;
+            qs[r][lane + 64] = bb;
+        }
+        // the new rows: k (RMSNorm + RoPE) and bf16(v) as cache bytes, to
+        // LDS, and the rows of this workgroup's tokens to the cache
+#pragma unroll
+        for (int j = 0; j < NR; ++j) {
+            const int t = wave + 4 * j, p = n_lo + (t >> 1);
+            if (p >= n_hi) break;
+            const int m = p - base;
+            float e0, e1;   // the values to encode
+            if (t & 1) {    // v: bf16(v)
+                e0 = mx::bf16_to_f32(mx::f32_to_bf16_rne(ka[j]));
+                e1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(kb[j]));
+            } else {        // k: RMSNorm + RoPE at its position
+                if (m != cs_m) {
+                    cs = hr::rope_cs(fz.theta, lane, p);
+                    cs_m = m;
+                }
+                uint16_t ba, bb;
+                hr::norm_rope(ka[j], kb[j], mx::bf16_to_f32(fz.kw[lane]), mx::bf16_to_f32(fz.kw[lane + 64]), fz.eps,
+                              cs, ba, bb);
+                e0 = mx::bf16_to_f32(ba);
+                e1 = mx::bf16_to_f32(bb);
+            }
+            const uint8_t b0 = (uint8_t)kv::e4m3_encode(e0, fz.codec);
+            const uint8_t b1 = (uint8_t)kv::e4m3_encode(e1, fz.codec);
+            uint8_t (*dst)[kD] = t & 1 ? vnew : knew;
+            dst[p - s0][lane] = b0;
+            dst[p - s0][lane + 64] = b1;
+            if (m >= m0 && m < m0 + MT) {
+                uint8_t* c = (t & 1 ? fz.kvv_w : fz.kvk_w) + ((int64_t)p * Hkv + g) * kD;
+                c[lane] = b0;
+                c[lane + 64] = b1;
+            }
+        }
     }
     // tokens m0..m0+MT-1 sit at positions base + m; those inside [0, max_pos) count
-    const int base = *dpos;
     const int mv_lo = max(m0, -base);
     const int mv_hi = min(min(M, m0 + MT) - 1, max_pos - 1 - base);
     if (mv_hi < mv_lo || s0 > base + mv_hi) return;   // uniform: no token of this workgroup reaches the chunk
     __syncthreads();
+    if (FUSED && n_lo < n_hi) {
+        // the step's rows in place of the cache bytes loaded above
+        const int kr = s0 + wave * 16 + l16;
+        if (kr >= n_lo && kr < n_hi) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) kraw[kt] = *reinterpret_cast<const uint2*>(&knew[kr - s0][kt * 32 + lq * 8]);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int t = 0; t < 8; ++t) {
+                    const int vr = s0 + kt * 32 + lq * 8 + t;
+                    if (vr >= n_lo && vr < n_hi) vraw[c][kt][t] = vnew[vr - s0][wave * 32 + l16 + c * 16];
+                }
+    }
     // ---- 2. scores, wave = positions 16*wave + l16
     mx::v4f sacc[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) sacc[rt] = mx::v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-        const uint4 kb = kv8_bf16(kraw[kt]);
+        const uint4 kb = kv8_bf16(lut, kraw[kt]);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
             sacc[rt] = mfma_bf16(*reinterpret_cast<const uint4*>(&qs[rt * 16 + l16][kt * 32 + lq * 8]), kb, sacc[rt]);
@@ -188,8 +322,8 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const uint32_t* v = vraw[c][kt];
-            vb[c] = make_uint4(pack_bf16(kv_bf16(v[0]), kv_bf16(v[1])), pack_bf16(kv_bf16(v[2]), kv_bf16(v[3])),
-                               pack_bf16(kv_bf16(v[4]), kv_bf16(v[5])), pack_bf16(kv_bf16(v[6]), kv_bf16(v[7])));
+            vb[c] = make_uint4(pack_bf16(kv_lut(lut, v[0]), kv_lut(lut, v[1])), pack_bf16(kv_lut(lut, v[2]), kv_lut(lut, v[3])),
+                               pack_bf16(kv_lut(lut, v[4]), kv_lut(lut, v[5])), pack_bf16(kv_lut(lut, v[6]), kv_lut(lut, v[7])));
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -381,10 +515,13 @@ extern "C" size_t mxfp4_attn_decode_workspace_size(int M, int Hq, int max_pos) {
     return (size_t)((int64_t)M * Hq * nchunk * kPart * sizeof(float));
 }
 
-extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
-                                    float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
-                                    int max_pos, void* workspace, size_t workspace_bytes, void* stream) {
-    MXH_REQUIRE(q && kvk && kvv && dpos && sc && workspace, "attn_decode: null pointer");
+namespace {
+
+template <bool FUSED>
+int launch_attn(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos, float* sc, float* o,
+                uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
+                size_t workspace_bytes, const QkvIn& fz, hipStream_t st) {
+    MXH_REQUIRE(kvk && kvv && dpos && sc && workspace, "attn_decode: null pointer");
     MXH_REQUIRE(o || oq, "attn_decode: no output (o and oq both null)");
     MXH_REQUIRE(!oq == !os, "attn_decode: oq and os go together");
     MXH_REQUIRE(D == kD, "attn_decode: head_dim D=%d (this build supports %d, as the reference's kernels)", D, kD);
@@ -392,7 +529,6 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     MXH_REQUIRE(max_pos > 0 && max_pos <= kChunk * kMaxChunks, "attn_decode: max_pos=%d (1..%d)", max_pos,
                 kChunk * kMaxChunks);
     MXH_REQUIRE(((uintptr_t)kvk & 15) == 0 && ((uintptr_t)kvv & 3) == 0, "attn_decode: kv cache rows must be aligned");
-    MXH_REQUIRE(((uintptr_t)q & 15) == 0, "attn_decode: q must be 16-byte aligned");
     MXH_REQUIRE(!o || ((uintptr_t)o & 7) == 0, "attn_decode: o must be 8-byte aligned");
     MXH_REQUIRE(!oq || ((uintptr_t)oq & 3) == 0, "attn_decode: oq must be 4-byte aligned");
     MXH_REQUIRE(workspace_bytes >= mxfp4_attn_decode_workspace_size(M, Hq, max_pos) && ((uintptr_t)workspace & 15) == 0,
@@ -400,7 +536,6 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     const int G = Hq / Hkv;
     const int nchunk = (max_pos + kChunk - 1) / kChunk;
     const float invsqrt = 1.0f / sqrtf((float)D);
-    hipStream_t st = mxh::as_stream(stream);
     // row tiles of 16 query rows per workgroup, at most 2: more token groups
     // (workgroups) rather than more rows each -- 4 tiles halved the grid at
     // M = 8 and took 9 % longer
@@ -411,9 +546,9 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     const dim3 gp(nchunk, Hkv, (M + MT - 1) / MT);
     const uint16_t* qh = static_cast<const uint16_t*>(q);
     float* part = static_cast<float*>(workspace);
-#define MXH_ATTN(GG, RR)                                                                                           \
-    hipLaunchKernelGGL((attn_partial_kernel<GG, RR>), gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, M, Hq, Hkv, \
-                       max_pos, nchunk, invsqrt)
+#define MXH_ATTN(GG, RR)                                                                                         \
+    hipLaunchKernelGGL((attn_partial_kernel<GG, RR, FUSED>), gp, dim3(256), 0, st, qh, kvk, kvv, sc, part, dpos, M, \
+                       Hq, Hkv, max_pos, nchunk, invsqrt, fz)
 #define MXH_ATTN_G(GG)                  \
     switch (RT) {                       \
         case 1: MXH_ATTN(GG, 1); break; \
@@ -433,6 +568,30 @@ extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uin
     if (rc != MXFP4_OK) return rc;
     hipLaunchKernelGGL(attn_final_kernel, dim3(Hq, M), dim3(256), 0, st, part, o, oq, os, dpos, Hq, max_pos, nchunk);
     return mxh::launch_status("attn_decode (merge)");
+}
+
+}  // namespace
+
+extern "C" int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
+                                    float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
+                                    int max_pos, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(q, "attn_decode: null pointer");
+    MXH_REQUIRE(((uintptr_t)q & 15) == 0, "attn_decode: q must be 16-byte aligned");
+    return launch_attn<false>(q, kvk, kvv, dpos, sc, o, oq, os, M, Hq, Hkv, D, max_pos, workspace, workspace_bytes,
+                              QkvIn{}, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_attn_decode_fused(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                                       float theta, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos, float* sc,
+                                       float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos,
+                                       int codec, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(qkv && q_norm_w && k_norm_w, "attn_decode_fused: null pointer");
+    MXH_REQUIRE(codec == 0 || codec == 1, "attn_decode_fused: codec %d (0 kv_write's, 1 torch float8_e4m3fn)", codec);
+    MXH_REQUIRE(M > 0 && M <= kMaxFusedM, "attn_decode_fused: M=%d (1..%d)", M, kMaxFusedM);
+    const QkvIn fz{qkv, static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w), eps, theta,
+                   codec, kvk, kvv};
+    return launch_attn<true>(nullptr, kvk, kvv, dpos, sc, o, oq, os, M, Hq, Hkv, D, max_pos, workspace,
+                             workspace_bytes, fz, mxh::as_stream(stream));
 }
 
 extern "C" int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,

@@ -317,3 +317,59 @@ def test_argmax_slices_match_torch(V):
         assert int(dpos.item()) == 7 + M * (call + 1)
     head = (M + 1) * 4
     assert int(ws[:head].count_nonzero()) == 0, "row counters not reset"
+
+
+@pytest.mark.parametrize("M,Hq,Hkv,max_pos,base,codec", [
+    (1, 32, 4, 4096, 4093, 0),    # the config-5 step: the new row in the last chunk
+    (1, 32, 4, 4096, 64, 0),      # the new row first in its chunk
+    (1, 8, 2, 300, 0, 1),         # empty context
+    (3, 8, 2, 300, 62, 1),        # the step's rows straddle a chunk boundary
+    (8, 32, 4, 1024, 700, 1),     # the batch step: two token groups per kv head
+    (5, 16, 4, 200, 197, 0),      # rows past max_pos are not written
+])
+def test_attn_decode_fused_matches_two_ops(M, Hq, Hkv, max_pos, base, codec):
+    """mxfp4_attn_decode_fused equals qk_norm_rope_kv followed by
+    attn_decode_mx on the same projections and cache: the same cache bytes,
+    raw scores, fp32 output and MXFP4 rows, bit for bit."""
+    lib = _lib.load()
+    g = torch.Generator(device=DEV)
+    g.manual_seed(900 + M + base)
+    D = 128
+    qkv = torch.randn((M, (Hq + 2 * Hkv) * D), generator=g, device=DEV) * 2
+    qw = (1 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    dpos = torch.tensor([base], dtype=torch.int32, device=DEV)
+    r = torch.randint(0, 256, (max_pos, Hkv, D), generator=g, device=DEV, dtype=torch.int32)
+    cache = ((r & 0x80) | (r & 0x3F)).to(torch.uint8)        # |v| < 2, no NaN code
+    wsb = lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
+    outs = []
+    for fused in (False, True):
+        kvk, kvv = cache.clone(), cache.flip(0).contiguous()
+        sc = torch.zeros((M, Hq, max_pos), dtype=torch.float32, device=DEV)
+        o = torch.zeros((M, Hq * D), dtype=torch.float32, device=DEV)
+        oq = torch.zeros((M, Hq * D // 2), dtype=torch.uint8, device=DEV)
+        os_ = torch.zeros((M, Hq * D // 32), dtype=torch.uint8, device=DEV)
+        ws = torch.zeros(((wsb + 15) // 16 * 16,), dtype=torch.uint8, device=DEV)
+        if fused:
+            _lib.check(lib.mxfp4_attn_decode_fused(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), 1e-6, 1e6,
+                                                   kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(), sc.data_ptr(),
+                                                   o.data_ptr(), oq.data_ptr(), os_.data_ptr(), M, Hq, Hkv, D, max_pos,
+                                                   codec, ws.data_ptr(), ws.numel(), None), "attn_decode_fused")
+        else:
+            q = torch.zeros((M, Hq, D), dtype=torch.bfloat16, device=DEV)
+            _lib.check(lib.mxfp4_qk_norm_rope_kv(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), 1e-6, 1e6,
+                                                 dpos.data_ptr(), M, Hq, Hkv, D, q.data_ptr(), kvk.data_ptr(),
+                                                 kvv.data_ptr(), max_pos, codec, None), "qk_norm_rope_kv")
+            _lib.check(lib.mxfp4_attn_decode_mx(q.data_ptr(), kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(),
+                                                sc.data_ptr(), o.data_ptr(), oq.data_ptr(), os_.data_ptr(), M, Hq, Hkv,
+                                                D, max_pos, ws.data_ptr(), ws.numel(), None), "attn_decode_mx")
+        torch.cuda.synchronize()
+        outs.append((kvk, kvv, sc, o, oq, os_))
+    live = torch.zeros((M, Hq, max_pos), dtype=torch.bool, device=DEV)
+    for m in range(M):
+        live[m, :, :min(base + m + 1, max_pos)] = True
+    for name, a, b in zip(("kvk", "kvv", "sc", "o", "oq", "os"), outs[0], outs[1]):
+        if name == "sc":
+            a, b = a[live], b[live]
+        assert torch.equal(a, b), f"M={M} base={base}: {name} differs"
+    log(f"  M={M} Hq={Hq} base={base} codec={codec}: fused attention equal to the two launches")
