@@ -666,38 +666,47 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_dma_kernel(GArgs g, W w) 
     }
 }
 
-// ------------------------------------------------------------------ 256 x 256 tiles, 8 waves
-// Tiles of up to 256 tokens x 256 weight rows (gate/up: the gate and up rows
+// ------------------------------------------------------------------ 192 x 256 tiles, 8 waves
+// Tiles of up to 192 tokens x 256 weight rows (gate/up: the gate and up rows
 // of 128 features; down: 256 output columns), 8 waves in 2 (tokens) x 4
-// (weight rows), a wave owning 128 tokens x 64 weight rows as 4 x 2 MFMA
-// accumulators.  K step 256, so every copied row piece is a whole 128-byte
-// line (global -> LDS by buffer_load ... lds, XOR swizzle of the 16-byte
-// chunks), in a 2-stage ring of 68 KB stages (one workgroup per CU).  The
-// token tile is sized to the expert's count in 64-row steps: only
-// ceil(rows / 64) * 64 token rows are copied, and a wave issues the MFMAs of
-// those of its 32-token blocks that hold routed tokens, so an expert with
-// ~130 tokens costs what ~130 tokens need rather than a full 256-row tile.
-// All tiles of one expert take workgroup numbers of one residue mod 8, i.e.
-// run on one XCD (workgroups are dealt to the 8 XCDs round-robin), so the
-// expert's gathered token rows are fetched into one L2.  Requires
-// Kp % 256 == 0.
-constexpr int X_BM = 256, X_BN = 256;
-constexpr int X_ROWB = 128;                        // bytes per row per K step
-constexpr int X_A = X_BM * X_ROWB;                 // 32 KB of token rows
-constexpr int X_W = X_BN * X_ROWB;                 // 32 KB of weight rows
-constexpr int X_SA = X_BM * 8, X_SW = X_BN * 8;    // 8 scale bytes per row
-constexpr int X_STAGE = X_A + X_W + X_SA + X_SW;   // 68 KB
+// (weight rows), a wave owning up to 3 x 2 MFMA accumulators.  K step 256,
+// so every copied row piece is a whole 128-byte line (global -> LDS by
+// buffer_load ... lds, XOR swizzle of the 16-byte chunks).  The weight rows,
+// which stream from HBM, sit in a 3-stage ring and the token rows, which
+// mostly hit L2, in a 2-stage ring: during step k the copies of the token
+// rows of step k+1 and of the weight rows of step k+2 are in flight, in that
+// order, so the wait at the top of step k+1 leaves the last five copies (the
+// weights of step k+2) outstanding.  One workgroup per CU (153 KB of LDS).
+//  * The token tile is sized to the expert's count in 64-row steps (only
+//    ceil(rows / 64) * 64 token rows are copied), and a wave issues the MFMAs
+//    of only those of its 32-token blocks that hold routed tokens, so an
+//    expert with ~130 tokens costs what ~130 tokens need.  Token block i of
+//    wave (wm, wn) is tile block 2i + wm: the two waves of a SIMD share the
+//    routed rows, so each one's MFMAs run while the other waits on its
+//    operand reads, which are issued one MFMA substep ahead.
+//  * All tiles of one expert take workgroup numbers of one residue mod 8,
+//    i.e. run on one XCD (workgroups are dealt to the 8 XCDs round-robin),
+//    so the expert's gathered token rows are fetched into one L2.
+// Requires Kp % 256 == 0.
+constexpr int X_BM = 192, X_BN = 256;
+constexpr int X_ROWB = 128;                           // bytes per row per K step
+constexpr int X_A = X_BM * X_ROWB;                    // 24 KB of token rows
+constexpr int X_W = X_BN * X_ROWB;                    // 32 KB of weight rows
+constexpr int X_AST = X_A + X_BM * 8;                 // token stage: rows + 8 scale bytes per row
+constexpr int X_WST = X_W + X_BN * 8;                 // weight stage
+constexpr int X_ARING = 3 * X_WST;                    // the token ring follows the 3-stage weight ring
 constexpr int X_THREADS = 512;
 constexpr int X_TROW = 144;                           // down transpose: bytes per row (128 + 16 of pad)
-constexpr int X_PP = 8 * 128 * X_TROW;                // after the ring / the 8 waves' transpose buffers
-constexpr int X_LDS = X_PP + 8 * X_BM;                // + the down tile's pair indices and weights
-static_assert(X_PP >= 2 * X_STAGE && X_LDS <= 160 * 1024, "x8 LDS layout");
+constexpr int X_PP = X_ARING + 2 * X_AST;             // the down tile's pair indices and weights
+constexpr int X_LDS = X_PP + 8 * X_BM;
+static_assert(8 * 96 * X_TROW <= X_PP && X_LDS <= 160 * 1024, "x8 LDS layout");
 
-// Per-tile copy plan of one wave: NA token-row blocks (8 rows of 128 bytes
-// each), 4 weight-row blocks and 2 scale copies (32 rows x 8 bytes each).
+// Per-tile copy plan of one wave: na token-row blocks (8 rows of 128 bytes
+// each), 4 weight-row blocks, one weight-scale copy (32 rows x 8 bytes) and,
+// for waves < 2 na, one token-scale copy.
 struct XCopies {
-    mx::v4u ars, wrs, srs[2];
-    uint32_t avo[4], wvo[4], svo[2], sdst[2];
+    mx::v4u ars, wrs, sars, swrs;
+    uint32_t avo[3], wvo[4], savo, swvo;
     int na;
 };
 
@@ -713,7 +722,7 @@ __device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, 
     };
     c.ars = mx::buf_rsrc(g.aq, (int64_t)g.a_rows * cbytes);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 3; ++j) {
         const int r = 64 * j + 8 * wave + lrow;   // block 8j + wave
         c.avo[j] = (uint32_t)src_row(r) * cbytes + ((slot ^ mx::swz_key128(r)) << 4);
     }
@@ -721,6 +730,7 @@ __device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, 
     int proj;
     weight_row<MODE>(32 * wave, n0, proj);
     c.wrs = mx::buf_rsrc(w.p(e, proj), (int64_t)g.Nw * cbytes);
+    c.swrs = mx::buf_rsrc(w.s(e, proj), (int64_t)g.Nw * nch);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int rho = 32 * wave + 8 * j + lrow;
@@ -728,39 +738,40 @@ __device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, 
         const int rr = min(weight_row<MODE>(rho, n0, pj), g.Nw - 1);
         c.wvo[j] = (uint32_t)rr * cbytes + ((slot ^ mx::swz_key128(rho)) << 4);
     }
-    // scale copies q = 2*wave + j of 2*na (token rows) + 8 (weight rows);
-    // the surplus ones repeat an earlier copy (same bytes, same place)
-    const int nq = 2 * c.na + 8;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int q = (2 * wave + j) % nq;
-        const int row = 32 * (q < 2 * c.na ? q : q - 2 * c.na) + (lane >> 1);
-        if (q < 2 * c.na) {
-            c.srs[j] = mx::buf_rsrc(g.as, (int64_t)g.a_rows * nch);
-            c.svo[j] = (uint32_t)src_row(row) * nch + 4 * (lane & 1);
-            c.sdst[j] = X_A + X_W + 256 * q;
-        } else {
-            int pj;   // one projection per 32-row block: wave-uniform
-            const int rr = min(weight_row<MODE>(row, n0, pj), g.Nw - 1);
-            c.srs[j] = mx::buf_rsrc(w.s(e, pj), (int64_t)g.Nw * nch);
-            c.svo[j] = (uint32_t)rr * nch + 4 * (lane & 1);
-            c.sdst[j] = X_A + X_W + X_SA + 256 * (q - 2 * c.na);
-        }
+    {   // scale copies: lane -> row 32 * wave + lane / 2, 4 of its 8 bytes
+        const int row = 32 * wave + (lane >> 1);
+        int pj;
+        const int rr = min(weight_row<MODE>(row, n0, pj), g.Nw - 1);
+        c.swvo = (uint32_t)rr * nch + 4 * (lane & 1);
+        c.sars = mx::buf_rsrc(g.as, (int64_t)g.a_rows * nch);
+        c.savo = (uint32_t)src_row(row) * nch + 4 * (lane & 1);
     }
 }
 
-// Copies of K step `s` into the stage at LDS address `buf`, part `part` of 4
-// (one token block, one weight block and, in parts 0-1, one scale copy), so a
-// step's copies are spread over the MFMA substeps of the previous one.
-__device__ __forceinline__ void x8_issue(const XCopies& c, uint32_t buf, int s, int part, int wave) {
+// The token-row copies of K step s into the token stage at `abuf`, part
+// `part` (parts 0-1), and the weight-row copies of step s into the weight
+// stage at `wbuf`, part `part` (parts 2-3): within a step all token copies
+// come first and the last five are the weight copies.
+__device__ __forceinline__ void x8_issue_a(const XCopies& c, uint32_t abuf, int s, int part, int wave) {
     const uint32_t kofs = (uint32_t)s * X_ROWB;
-    if (part < c.na) mx::dma16(c.avo[part], c.ars, kofs, buf + (8 * part + wave) * 1024);
-    mx::dma16(c.wvo[part], c.wrs, kofs, buf + X_A + (4 * wave + part) * 1024);
-    if (part < 2) mx::dma4(c.svo[part], c.srs[part], (uint32_t)s * 8, buf + c.sdst[part]);
+    if (part == 0) {
+        if (c.na > 0) mx::dma16(c.avo[0], c.ars, kofs, abuf + wave * 1024);
+        if (c.na > 1) mx::dma16(c.avo[1], c.ars, kofs, abuf + (8 + wave) * 1024);
+        if (wave < 2 * c.na) mx::dma4(c.savo, c.sars, (uint32_t)s * 8, abuf + X_A + 256 * wave);
+    } else if (c.na > 2) {
+        mx::dma16(c.avo[2], c.ars, kofs, abuf + (16 + wave) * 1024);
+    }
+}
+__device__ __forceinline__ void x8_issue_w(const XCopies& c, uint32_t wbuf, int s, int part, int wave) {
+    const uint32_t kofs = (uint32_t)s * X_ROWB;
+    const int j0 = 2 * (part - 2);
+    mx::dma16(c.wvo[j0], c.wrs, kofs, wbuf + (4 * wave + j0) * 1024);
+    mx::dma16(c.wvo[j0 + 1], c.wrs, kofs, wbuf + (4 * wave + j0 + 1) * 1024);
+    if (part == 2) mx::dma4(c.swvo, c.swrs, (uint32_t)s * 8, wbuf + X_W + 256 * wave);
 }
 
 // K loop and epilogue of one wave on one token tile; NB = the wave's 32-token
-// blocks holding routed tokens (0..4).
+// blocks holding routed tokens (0..3).
 template <int MODE, int NB>
 __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_t* smem, uint32_t ring, int n0,
                                         int off, int mt, int mrows, int wave, int lane) {
@@ -768,17 +779,17 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
     const int lr = lane & 31, h = lane >> 5;
     const int key = mx::swz_key128(lr);
     const int nsteps = g.Kp / 256;
-    mx::v16f acc[4][2];
+    mx::v16f acc[3][2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    // down: the tile's pair indices and routing weights go to LDS beside the
-    // ring (loaded before the first copies; waiting for them costs nothing
-    // extra, since the first K step waits for those copies anyway)
+    // down: the tile's pair indices and routing weights, loaded before the
+    // first copies and put in LDS after the K loop (a use of a loaded value
+    // makes the compiler wait for every load in flight)
     int rp = 0;
     float rs = 0.0f;
     const int trow = wave * 64 + lane;
@@ -786,37 +797,40 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         rp = g.pairs[off + mt + trow];
         rs = g.sscore[off + mt + trow];
     }
-#pragma unroll
-    for (int q = 0; q < 4; ++q) x8_issue(c, ring, 0, q, wave);
-    if (MODE == MODE_DOWN && trow < X_BM) {
-        reinterpret_cast<int*>(smem + X_PP)[trow] = rp;
-        reinterpret_cast<float*>(smem + X_PP + 4 * X_BM)[trow] = rs;
+    // prologue: weights of step 0, tokens of step 0, weights of step 1
+    x8_issue_w(c, ring, 0, 2, wave);
+    x8_issue_w(c, ring, 0, 3, wave);
+    x8_issue_a(c, ring + X_ARING, 0, 0, wave);
+    x8_issue_a(c, ring + X_ARING, 0, 1, wave);
+    if (nsteps > 1) {
+        x8_issue_w(c, ring + X_WST, 1, 2, wave);
+        x8_issue_w(c, ring + X_WST, 1, 3, wave);
     }
     for (int it = 0; it < nsteps; ++it) {
-        // this wave's copies of step it have landed and its reads of step
+        // this wave's copies of step it have landed (the weights of step
+        // it+1, issued last, may still be in flight) and its reads of step
         // it-1 are done; after the barrier every wave's
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+        if (it + 1 < nsteps) asm volatile("s_waitcnt vmcnt(5) lgkmcnt(0)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
-        const bool more = it + 1 < nsteps;
-        const uint8_t* cur = smem + (it & 1) * X_STAGE;
-        const uint32_t nxt = ring + ((it + 1) & 1) * X_STAGE;
-        // token block i of wave (wm, wn) is tile block 2i + wm: the two waves
-        // of a SIMD share the routed rows, so each one's MFMAs run while the
-        // other waits on its operand reads
-        const uint8_t* la = cur + (32 * wm + lr) * X_ROWB;
-        const uint8_t* lw = cur + X_A + (wn * 64 + lr) * X_ROWB;
-        const uint8_t* lsa = cur + X_A + X_W + (32 * wm + lr) * 8;
-        const uint8_t* lsw = cur + X_A + X_W + X_SA + (wn * 64 + lr) * 8;
-        uint32_t sa[4], sb[2];
+        const bool more_a = it + 1 < nsteps, more_w = it + 2 < nsteps;
+        const uint8_t* wst = smem + (it % 3) * X_WST;
+        const uint8_t* ast = smem + X_ARING + (it & 1) * X_AST;
+        const uint32_t anxt = ring + X_ARING + ((it + 1) & 1) * X_AST;
+        const uint32_t wnxt = ring + ((it + 2) % 3) * X_WST;
+        // token block i of wave (wm, wn) is tile block 2i + wm
+        const uint8_t* la = ast + (32 * wm + lr) * X_ROWB;
+        const uint8_t* lw = wst + (wn * 64 + lr) * X_ROWB;
+        const uint8_t* lsa = ast + X_A + (32 * wm + lr) * 8;
+        const uint8_t* lsw = wst + X_W + (wn * 64 + lr) * 8;
+        uint32_t sa[3], sb[2];
 #pragma unroll
         for (int i = 0; i < NB; ++i) sa[i] = scale_word(lsa + i * 64 * 8, h);
 #pragma unroll
         for (int j = 0; j < 2; ++j) sb[j] = scale_word(lsw + j * 32 * 8, h);
-        // (reading substep ks+1's operands ahead of substep ks's MFMAs needs a
-        // second operand set, which does not fit beside the accumulators at
-        // two waves per SIMD)
-        uint4 af[1][4], bf[1][2];
+        // operands of substep ks+1 are read before the MFMAs of substep ks
+        uint4 af[2][3], bf[2][2];
         auto load = [&](int ks, int r) {
             const int koff = ((2 * ks + h) ^ key) << 4;
 #pragma unroll
@@ -824,13 +838,18 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
 #pragma unroll
             for (int j = 0; j < 2; ++j) bf[r][j] = *reinterpret_cast<const uint4*>(lw + koff + j * 32 * X_ROWB);
         };
+        if (NB > 0) load(0, 0);
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             __builtin_amdgcn_sched_barrier(0);
-            if (more) x8_issue(c, nxt, it + 1, ks, wave);
+            if (ks < 2) {
+                if (more_a) x8_issue_a(c, anxt, it + 1, ks, wave);
+            } else if (more_w) {
+                x8_issue_w(c, wnxt, it + 2, ks, wave);
+            }
             if (NB > 0) {
-                load(ks, 0);
-                const int r = 0;
+                if (ks + 1 < 4) load(ks + 1, (ks + 1) & 1);
+                const int r = ks & 1;
                 // D[weight row][token]: the weight tile is the MFMA A operand
 #pragma unroll
                 for (int i = 0; i < NB; ++i)
@@ -845,18 +864,22 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
     if (MODE == MODE_DOWN) {
         // bf16(bf16(y) * score) goes through LDS, so that each store
         // instruction writes 8 whole 128-byte row segments instead of 16
-        // bytes of 32 rows: wave w transposes its 128 x 64 block in its own
-        // X_TROW-pitched buffer, over the ring (free once every wave is past
+        // bytes of 32 rows: wave w transposes its 96 x 64 block in its own
+        // X_TROW-pitched buffer, over the rings (free once every wave is past
         // its last MFMA)
+        if (trow < X_BM) {
+            reinterpret_cast<int*>(smem + X_PP)[trow] = rp;
+            reinterpret_cast<float*>(smem + X_PP + 4 * X_BM)[trow] = rs;
+        }
         __syncthreads();
         if (NB == 0) return;
-        uint8_t* tb = smem + wave * 128 * X_TROW;
+        uint8_t* tb = smem + wave * 96 * X_TROW;
         const int* lp = reinterpret_cast<const int*>(smem + X_PP);
         const float* ls = reinterpret_cast<const float*>(smem + X_PP + 4 * X_BM);
 #pragma unroll
@@ -899,10 +922,13 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
     if (NB == 0) return;
     // gate/up: the wave's token blocks in pairs (tile rows 128*half + 32*wm
     // + 64*i' + lane%32) through the 128 x 128 epilogue
+    const mx::v16f zero = {};
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
         if (2 * half >= NB) continue;
-        mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]}, {acc[2 * half + 1][0], acc[2 * half + 1][1]}};
+        mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]},
+                              {2 * half + 1 < 3 ? acc[(2 * half + 1) % 3][0] : zero,
+                               2 * half + 1 < 3 ? acc[(2 * half + 1) % 3][1] : zero}};
         const int pp[2] = {0, 0};
         const float ss[2] = {0.0f, 0.0f};
         tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, 128 * half + 32 * wm, wn, lr, h, pp, ss, 64);
@@ -928,16 +954,15 @@ __global__ __launch_bounds__(X_THREADS, 1) void grouped_gemm_x8_kernel(GArgs g, 
         XCopies c;
         x8_plan<MODE>(c, g, w, e, n0, off, mt, mrows, wave, lane);
         // the wave's token blocks 2i + wm (i < nb) holding routed rows
-        const int nb = min(((mrows + 31) / 32 - (wave >> 2) + 1) >> 1, 4);
+        const int nb = min(((mrows + 31) / 32 - (wave >> 2) + 1) >> 1, 3);
         switch (nb) {
-            case 4: x8_tile<MODE, 4>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
             case 3: x8_tile<MODE, 3>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
             case 2: x8_tile<MODE, 2>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
             case 1: x8_tile<MODE, 1>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
             default: x8_tile<MODE, 0>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
         }
-        // every wave is done with the ring before the next token tile
-        // refills it (and its vmcnt counts only the new copies)
+        // every wave is done with the rings before the next token tile
+        // refills them (and its vmcnt counts only the new copies)
         if (mt + X_BM < cnt) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
             __syncthreads();
