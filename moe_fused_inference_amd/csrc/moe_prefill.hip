@@ -183,6 +183,163 @@ __global__ __launch_bounds__(64 * kRouteWaves) void route_kernel(const int64_t* 
     }
 }
 
+// ------------------------------------------------------------------ routing, counting sort
+// The same grouping (a stable sort of the row-major pairs by expert id) as a
+// counting sort in two launches, whose work per id does not grow with the
+// number of experts.  Chunks of kRtChunk ids; a wave takes 64 consecutive
+// ids at a time and finds, for each lane, the lanes holding the same id with
+// one ballot per id bit (the id's bits agree), so its rank among the equal
+// ids of the 64 is a popcount.
+//   route_count_kernel    chunk c: per-expert counts of its valid ids ->
+//                         hist (nchunk, n_exp).
+//   route_scatter_kernel  chunk c: expert e's pairs start at offs[e] (sum of
+//                         the counts of ids below e) + the counts of e in
+//                         chunks below c + in earlier waves of c + the
+//                         earlier 64-id groups of the wave + the rank;
+//                         writes pairs (and the sorted routing weights), and
+//                         chunk 0 writes counts / offs.
+constexpr int kRtWaves = 4;
+constexpr int kRtGroups = 4;                          // 64-id groups per wave
+constexpr int kRtChunk = 64 * kRtWaves * kRtGroups;   // 1024 ids per workgroup
+
+__device__ __forceinline__ uint64_t same_id_lanes(int id, bool valid, int bits) {
+    uint64_t m = __ballot(valid);
+    for (int b = 0; b < bits; ++b) {
+        const uint64_t s = __ballot((id >> b) & 1);
+        m &= ((id >> b) & 1) ? s : ~s;
+    }
+    return m;
+}
+
+__device__ __forceinline__ int id_bits(int n_exp) { return 32 - __clz(max(n_exp - 1, 1)); }
+
+__global__ __launch_bounds__(64 * kRtWaves) void route_count_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
+                                                                   int* __restrict__ hist) {
+    __shared__ int h[kMaxExperts];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    for (int e = tid; e < n_exp; e += 64 * kRtWaves) h[e] = 0;
+    const int bits = id_bits(n_exp);
+    int id[kRtGroups];
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) {   // unconditional (clamped) loads: all in flight at once
+        const int p = blockIdx.x * kRtChunk + (wave * kRtGroups + k) * 64 + lane;
+        const int64_t v = topi[min(p, P - 1)];
+        id[k] = (p < P && v >= 0 && v < n_exp) ? (int)v : -1;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) {
+        const bool valid = id[k] >= 0;
+        const uint64_t m = same_id_lanes(id[k], valid, bits);
+        if (valid && (m & ((1ull << lane) - 1ull)) == 0) atomicAdd(&h[id[k]], __popcll(m));   // group leader
+    }
+    __syncthreads();
+    for (int e = tid; e < n_exp; e += 64 * kRtWaves) hist[(int64_t)blockIdx.x * n_exp + e] = h[e];
+}
+
+__global__ __launch_bounds__(64 * kRtWaves) void route_scatter_kernel(const int64_t* __restrict__ topi, int P,
+                                                                     int n_exp, const int* __restrict__ hist,
+                                                                     int* __restrict__ counts, int* __restrict__ offs,
+                                                                     int* __restrict__ pairs,
+                                                                     const uint16_t* __restrict__ scores,
+                                                                     float* __restrict__ sscore) {
+    __shared__ int base[kMaxExperts];              // where expert e's pairs of this chunk start
+    __shared__ int wh[kRtWaves][kMaxExperts];      // per-wave counts, then exclusive prefix over waves
+    __shared__ int wsum[kRtWaves];
+    __shared__ int carry;                          // running total of the scan over earlier slices
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nchunk = gridDim.x, c = blockIdx.x;
+    if (tid == 0) carry = 0;
+    const int bits = id_bits(n_exp);
+    int id[kRtGroups];
+    int64_t raw[kRtGroups];
+    uint16_t sc[kRtGroups] = {};
+    // all loads first (no use of a loaded value in between: one round trip)
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) raw[k] = topi[min(c * kRtChunk + (wave * kRtGroups + k) * 64 + lane, P - 1)];
+    if (sscore) {
+#pragma unroll
+        for (int k = 0; k < kRtGroups; ++k) sc[k] = scores[min(c * kRtChunk + (wave * kRtGroups + k) * 64 + lane, P - 1)];
+    }
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) {
+        const int p = c * kRtChunk + (wave * kRtGroups + k) * 64 + lane;
+        id[k] = (p < P && raw[k] >= 0 && raw[k] < n_exp) ? (int)raw[k] : -1;
+    }
+    // per expert: the total over all chunks and the count in chunks below c
+    for (int e0 = 0; e0 < n_exp; e0 += 64 * kRtWaves) {
+        const int e = e0 + tid;
+        const int ec = min(e, n_exp - 1);
+        int tot = 0, bef = 0;
+        for (int cb = 0; cb < nchunk; cb += 16) {
+            int v[16];   // 16 unconditional (clamped) loads in flight, then the sums
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = hist[(int64_t)min(cb + i, nchunk - 1) * n_exp + ec];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int x = (cb + i < nchunk && e < n_exp) ? v[i] : 0;
+                tot += x;
+                bef += cb + i < c ? x : 0;
+            }
+        }
+        // exclusive scan of tot over e: waves, then the waves' sums
+        int incl = tot;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int t = __shfl_up(incl, o);
+            if (lane >= o) incl += t;
+        }
+        if (lane == 63) wsum[wave] = incl;
+        __syncthreads();   // wsum, and carry from the previous slice
+        int run = carry;
+        for (int w = 0; w < wave; ++w) run += wsum[w];
+        const int ex = run + incl - tot;
+        if (e < n_exp) {
+            base[e] = ex + bef;
+            if (c == 0) {
+                counts[e] = tot;
+                offs[e] = ex;
+            }
+#pragma unroll
+            for (int w = 0; w < kRtWaves; ++w) wh[w][e] = 0;
+        }
+        __syncthreads();   // every read of carry and wsum is done
+        if (tid == 64 * kRtWaves - 1) carry = run + incl;   // read after the next slice's first barrier
+    }
+    __syncthreads();
+    // this wave's counts per expert (group leaders; one writer per expert and group)
+    uint64_t mk[kRtGroups];
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) {
+        const bool valid = id[k] >= 0;
+        mk[k] = same_id_lanes(id[k], valid, bits);
+        if (valid && (mk[k] & ((1ull << lane) - 1ull)) == 0) wh[wave][id[k]] += __popcll(mk[k]);
+    }
+    __syncthreads();
+    // exclusive prefix over the waves, per expert
+    for (int e = tid; e < n_exp; e += 64 * kRtWaves) {
+        int run = 0;
+        for (int w = 0; w < kRtWaves; ++w) {
+            const int v = wh[w][e];
+            wh[w][e] = run;
+            run += v;
+        }
+    }
+    __syncthreads();
+    // positions: the wave's earlier groups are counted in wh as it goes
+#pragma unroll
+    for (int k = 0; k < kRtGroups; ++k) {
+        if (id[k] < 0) continue;
+        const int at = base[id[k]] + wh[wave][id[k]] + __popcll(mk[k] & ((1ull << lane) - 1ull));
+        const int p = c * kRtChunk + (wave * kRtGroups + k) * 64 + lane;
+        pairs[at] = p;
+        if (sscore) sscore[at] = mx::bf16_to_f32(sc[k]);
+        // after every lane has its position, the group leader moves the
+        // wave's offset of this expert past the group
+        if ((mk[k] & ((1ull << lane) - 1ull)) == 0) wh[wave][id[k]] += __popcll(mk[k]);
+    }
+}
+
 // ------------------------------------------------------------------ weights
 struct StackedW {                // expert e of projection j at base[j] + e * stride
     const uint8_t* wp[3];
@@ -1002,7 +1159,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* __
 
 // ------------------------------------------------------------------ host
 struct WsLayout {
-    size_t counts, offs, pairs, sscore, xq, xs, hq, hs, yd, total;
+    size_t counts, offs, pairs, sscore, hist, xq, xs, hq, hs, yd, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1015,6 +1172,7 @@ WsLayout ws_layout(int T, int topk, int n_exp, int H, int Mi) {
     L.offs = o;   o = align256(o + sizeof(int) * n_exp);
     L.pairs = o;  o = align256(o + sizeof(int) * P);
     L.sscore = o; o = align256(o + sizeof(float) * P);
+    L.hist = o;   o = align256(o + sizeof(int) * ((P + kRtChunk - 1) / kRtChunk) * n_exp);
     L.xq = o;     o = align256(o + (size_t)T * (H / 2));
     L.xs = o;     o = align256(o + (size_t)T * (H / 32));
     L.hq = o;     o = align256(o + P * (Mi / 2));
@@ -1060,9 +1218,11 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     const int P = T * topk;
 
     float* sscore = reinterpret_cast<float*>(ws + L.sscore);
-    hipLaunchKernelGGL(route_kernel, dim3((n_exp + kRouteEpw - 1) / kRouteEpw), dim3(64 * kRouteWaves), 0, st, topi, P,
-                       n_exp, counts, offs, pairs, scores,
-                       sscore);
+    int* hist = reinterpret_cast<int*>(ws + L.hist);
+    const int nchunk = (P + kRtChunk - 1) / kRtChunk;
+    hipLaunchKernelGGL(route_count_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist);
+    hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist, counts,
+                       offs, pairs, scores, sscore);
     int rc = mxh::launch_status("moe_prefill route");
     if (rc != MXFP4_OK) return rc;
     rc = mxh::quantize_rows_impl(x, MXFP4_DT_BF16, 1, H, T, H, H, ws + L.xq, ws + L.xs, st);
