@@ -466,7 +466,8 @@ __device__ __forceinline__ void down_rows(const GArgs& g, int off, int mt, int m
 // Epilogue of a 128 x 128 tile (acc[i][j] of the 2 x 2 wave layout):
 // gate/up -> h = silu(g)*u, fp16, MXFP4 rows in sorted pair order; down ->
 // bf16(bf16(y) * score) at the pair's own index (pp / ss from down_rows).
-template <int MODE>
+// NI: how many of the two token blocks to process (1: only acc[0]).
+template <int MODE, int NI = 2>
 __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs& g, int n0, int off, int mt,
                                               int mrows, int rbase, int wn, int lr, int h, const int (&pp)[2],
                                               const float (&ss)[2], int istride = 32) {
@@ -476,7 +477,7 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
         const int fb = n0 + 32 * wn;           // first feature of this wave's 32-block
         const int Mi = g.Nw;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const int rloc = rbase + istride * i + lr;
             float v[16];
             float amax = 0.0f;
@@ -515,7 +516,7 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
     } else {
         const int H = g.Nw;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NI; ++i) {
             const int rloc = rbase + istride * i + lr;
             if (rloc < mrows) {
                 const int p = pp[i];
@@ -1077,18 +1078,18 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         return;
     }
     if (NB == 0) return;
-    // gate/up: the wave's token blocks in pairs (tile rows 128*half + 32*wm
-    // + 64*i' + lane%32) through the 128 x 128 epilogue
-    const mx::v16f zero = {};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-        if (2 * half >= NB) continue;
-        mx::v16f sub[2][2] = {{acc[2 * half][0], acc[2 * half][1]},
-                              {2 * half + 1 < 3 ? acc[(2 * half + 1) % 3][0] : zero,
-                               2 * half + 1 < 3 ? acc[(2 * half + 1) % 3][1] : zero}};
-        const int pp[2] = {0, 0};
-        const float ss[2] = {0.0f, 0.0f};
-        tile_epilogue<MODE>(sub, g, n0, off, mt, mrows, 128 * half + 32 * wm, wn, lr, h, pp, ss, 64);
+    // gate/up: the wave's token blocks (tile rows 64*i + 32*wm + lane%32)
+    // through the 128 x 128 epilogue, in pairs, the last one alone when NB
+    // is odd (the epilogue is VALU-bound: no work on empty blocks)
+    const int pp[2] = {0, 0};
+    const float ss[2] = {0.0f, 0.0f};
+    if (NB >= 2) {
+        mx::v16f sub[2][2] = {{acc[0][0], acc[0][1]}, {acc[1][0], acc[1][1]}};
+        tile_epilogue<MODE, 2>(sub, g, n0, off, mt, mrows, 32 * wm, wn, lr, h, pp, ss, 64);
+    }
+    if (NB == 1 || NB == 3) {
+        mx::v16f sub[2][2] = {{acc[NB - 1][0], acc[NB - 1][1]}, {acc[NB - 1][0], acc[NB - 1][1]}};
+        tile_epilogue<MODE, 1>(sub, g, n0, off, mt, mrows, 64 * (NB - 1) + 32 * wm, wn, lr, h, pp, ss, 64);
     }
 }
 
