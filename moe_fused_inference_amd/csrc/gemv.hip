@@ -90,9 +90,9 @@ __device__ __forceinline__ EntryMap map_entry(const GemvArgs& a, int tg) {
 // all register indices static.
 struct SegBuf {
     uint4 b[kSeg];
-    uint32_t bs[kSeg];
+    mx::SegScales bs;
     uint4 a[kSeg];
-    uint32_t as[kSeg];
+    mx::SegScales as;
 };
 
 struct SegCtx {
@@ -119,9 +119,9 @@ __device__ __forceinline__ void load_seg(SegBuf& sb, const SegCtx& cx, int s0) {
             sb.a[j] = aok ? *reinterpret_cast<const uint4*>(cx.arow + c * 16) : make_uint4(0, 0, 0, 0);
         }
     }
-    static_assert(kSeg == 4, "mx::seg_scales covers 4 K-steps");
-    mx::seg_scales(sb.bs, cx.srow, true, cx.g, s0, cx.steps, cx.nch);
-    if (AMODE == A_FP4) mx::seg_scales(sb.as, cx.asrow, cx.arow_ok, cx.g, s0, cx.steps, cx.nch);
+    static_assert(kSeg == 4, "mx::seg_scales_issue covers 4 K-steps");
+    mx::seg_scales_issue(sb.bs, cx.srow, cx.g, s0, cx.nch);
+    if (AMODE == A_FP4) mx::seg_scales_issue(sb.as, cx.asrow, cx.g, s0, cx.nch);   // asrow is valid even when !arow_ok
 }
 
 template <int AMODE>
@@ -134,7 +134,7 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
             uint32_t asc;
             if (AMODE == A_FP4) {
                 aq = sb.a[j];
-                asc = sb.as[j];
+                asc = mx::seg_scale_at(sb.as, j, cx.arow_ok, cx.g, s0, cx.steps, cx.nch);
             } else {
                 // rows past the group (arow_ok false) are zero: their LDS rows are not built
                 const int c = 4 * s + cx.g;
@@ -142,7 +142,7 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
                 aq = ok ? *reinterpret_cast<const uint4*>(cx.lq + c * 16) : make_uint4(0, 0, 0, 0);
                 asc = ok ? (uint32_t)cx.lsc[c] : 127u;
             }
-            acc = mx::mfma16_fp4(aq, sb.b[j], acc, asc, sb.bs[j]);
+            acc = mx::mfma16_fp4(aq, sb.b[j], acc, asc, mx::seg_scale_at(sb.bs, j, true, cx.g, s0, cx.steps, cx.nch));
         }
     }
     return acc;
@@ -218,19 +218,39 @@ __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, Gemv
                         sq + r * (a.Kp >> 1) + boff * 16, ssc + r * nch + boff,
                         g, se - sb, nch - (int)boff, arow_ok};
         SegBuf s0buf, s1buf;
+        // A_SILU: the thread's first 8 g / u values are loaded before the
+        // weights (loads complete in issue order: loaded after them, h would
+        // wait for the weight segment too)
+        const int upr = a.Kp >> 3;
+        const int nbr = min(16, cnt - rt);
+        float pg[8] = {}, pu[8] = {};
+        if (AMODE == A_SILU && (int)threadIdx.x < nbr * upr) {
+            const int u = threadIdx.x;
+            const int rr = u / upr;
+            const int k0 = (u - rr * upr) * 8;
+            const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
+            const float* grow = a.gu + (int64_t)em.src * 2 * a.K;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {   // clamped: every load issued before any is used
+                const int k = min(k0 + i, a.K - 1);
+                pg[i] = grow[k];
+                pu[i] = grow[a.K + k];
+            }
+        }
         if (sb < se) load_seg<AMODE>(s0buf, cx, 0);   // the weights stream while h is built
         if (AMODE == A_SILU) {
             // Build the group's rows of the 16-row A tile: h = silu(g)*u (fp32)
             // quantized per 32-block with the bit-exact rule (rows past the
             // group are read as zeros by compute_seg, so they are not built).
-            const int upr = a.Kp >> 3;
-            const int nb = min(16, cnt - rt);
-            for (int u = threadIdx.x; u < nb * upr; u += 64 * NW * S) {   // quads stay together
+            for (int u = threadIdx.x; u < nbr * upr; u += 64 * NW * S) {   // quads stay together
                 const int rr = u / upr;
                 const int uu = u - rr * upr;
                 const int k0 = uu * 8;
                 float h[8];
-                {
+                if (u == (int)threadIdx.x) {   // the values loaded above
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) h[i] = (k0 + i < a.K) ? mx::silu_mul(pg[i], pu[i]) : 0.0f;
+                } else {
                     const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
                     const float* grow = a.gu + (int64_t)em.src * 2 * a.K;
 #pragma unroll
