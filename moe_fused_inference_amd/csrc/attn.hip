@@ -189,21 +189,26 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                 kb[j] = row[lane + 64];
             }
         }
+        // RoPE cos / sin of every position the workgroup needs -- its own
+        // tokens and the step's rows in its chunk -- once per (token, lane)
+        // in LDS: a wave would otherwise evaluate them for each of its
+        // tokens (pow, cos and sin cost hundreds of instructions)
+        __shared__ float2 rcs[kMaxFusedM][64];
+        for (int jm = wave; jm < M; jm += 4) {   // token jm
+            const bool own = jm >= m0 && jm < m0 + MT;
+            const bool newrow = base + jm >= n_lo && base + jm < n_hi;
+            if (own || newrow) rcs[jm][lane] = hr::rope_cs(fz.theta, lane, base + jm);
+        }
+        __syncthreads();
         // q: RMSNorm + RoPE at the token's position, bf16 into LDS
-        int cs_m = -1;
-        float2 cs = make_float2(1.0f, 0.0f);
 #pragma unroll
         for (int i = 0; i < QR; ++i) {
             const int r = wave + 4 * i, m = m0 + r / G;
             if (r >= R) break;
             uint16_t ba = 0, bb = 0;
             if (m < M) {   // wave-uniform
-                if (m != cs_m) {
-                    cs = hr::rope_cs(fz.theta, lane, base + m);
-                    cs_m = m;
-                }
-                hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(fz.qw[lane]), mx::bf16_to_f32(fz.qw[lane + 64]), fz.eps, cs,
-                              ba, bb);
+                hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(fz.qw[lane]), mx::bf16_to_f32(fz.qw[lane + 64]), fz.eps,
+                              rcs[m][lane], ba, bb);
             }
             qs[r][lane] = ba;
             qs[r][lane + 64] = bb;
@@ -220,13 +225,9 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                 e0 = mx::bf16_to_f32(mx::f32_to_bf16_rne(ka[j]));
                 e1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(kb[j]));
             } else {        // k: RMSNorm + RoPE at its position
-                if (m != cs_m) {
-                    cs = hr::rope_cs(fz.theta, lane, p);
-                    cs_m = m;
-                }
                 uint16_t ba, bb;
                 hr::norm_rope(ka[j], kb[j], mx::bf16_to_f32(fz.kw[lane]), mx::bf16_to_f32(fz.kw[lane + 64]), fz.eps,
-                              cs, ba, bb);
+                              rcs[m][lane], ba, bb);
                 e0 = mx::bf16_to_f32(ba);
                 e1 = mx::bf16_to_f32(bb);
             }
