@@ -15,15 +15,18 @@
 //                        -- moe_down's own activation quantization
 //                        (src/ext/mxfp4_decode.cu:218-279), bit-exact to it
 //                        given g and u.
-//   batch_down_kernel    workgroup (16 output columns): 12 waves share out the
-//                        distinct experts (slot order); per expert, its down
-//                        rows for the columns times the h rows of its tokens,
-//                        weighted by the routing weights (moe_combine,
-//                        src/ext/mxfp4_decode.cu:285-299) into per-wave
-//                        token sums in LDS; the 12 wave sums are added in a
-//                        fixed order.  (150 VGPRs: 3 waves per SIMD, so 12
-//                        waves fit one CU; each wave walks a third fewer
-//                        experts than with 8.)  No gu / yd round trip through HBM and
+//   batch_down_kernel    two workgroups per 16 output columns, each with
+//                        every other distinct expert (slot order); 12 waves
+//                        share out a workgroup's experts; per expert, its
+//                        down rows for the columns times the h rows of its
+//                        tokens, weighted by the routing weights
+//                        (moe_combine, src/ext/mxfp4_decode.cu:285-299) into
+//                        per-wave token sums in LDS; the 12 wave sums are
+//                        added in a fixed order and the two workgroups' sums
+//                        are added into y, which the gate/up launch clears
+//                        (two addends onto zero: the same bits in either
+//                        order).  (150 VGPRs: 3 waves per SIMD, so 12 waves
+//                        fit one CU.)  No gu / yd round trip through HBM and
 //                        no separate combine launch.
 //
 // The results match the drop-in chain up to fp32 summation order (the
@@ -38,7 +41,7 @@ namespace {
 constexpr int kMaxTok = 16;     // tokens per step: one MFMA row tile
 constexpr int kMaxE = 8;        // slots per token (moe_combine's cap)
 constexpr int kMaxSlots = kMaxTok * kMaxE;
-constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment (mx::seg_scales covers 4)
+constexpr int kSegB = 4;        // MFMA K-steps per prefetch segment (mx::seg_scales_issue covers 4)
 constexpr int kDownWaves = 12;   // 3 waves per SIMD at 150 VGPRs
 
 struct BatchArgs {
@@ -62,9 +65,9 @@ struct BatchArgs {
 // their scale bytes for kSegB MFMA K-steps.
 struct Seg {
     uint4 b[kSegB];
-    uint32_t bs[kSegB];
+    mx::SegScales bs;
     uint4 a[kSegB];
-    uint32_t as[kSegB];
+    mx::SegScales as;
 };
 
 // Lane (row l%16, group q = l/16) takes 32-block 4*st + q at K-step st (64
@@ -79,14 +82,16 @@ __device__ __forceinline__ void load_seg(Seg& sg, const uint8_t* wrow, const uin
         sg.b[j] = ok ? *reinterpret_cast<const uint4*>(wrow + c * 16) : make_uint4(0, 0, 0, 0);
         sg.a[j] = (ok && aok) ? *reinterpret_cast<const uint4*>(arow + c * 16) : make_uint4(0, 0, 0, 0);
     }
-    mx::seg_scales(sg.bs, srow, true, q, st0, steps, nch);
-    mx::seg_scales(sg.as, asrow, aok, q, st0, steps, nch);
+    mx::seg_scales_issue(sg.bs, srow, q, st0, nch);
+    mx::seg_scales_issue(sg.as, asrow, q, st0, nch);   // asrow is a valid row even when !aok
 }
 
-__device__ __forceinline__ mx::v4f mma_seg(const Seg& sg, int st0, int steps, mx::v4f acc) {
+__device__ __forceinline__ mx::v4f mma_seg(const Seg& sg, bool aok, int q, int st0, int steps, int nch, mx::v4f acc) {
 #pragma unroll
     for (int j = 0; j < kSegB; ++j)
-        if (st0 + j < steps) acc = mx::mfma16_fp4(sg.a[j], sg.b[j], acc, sg.as[j], sg.bs[j]);
+        if (st0 + j < steps)
+            acc = mx::mfma16_fp4(sg.a[j], sg.b[j], acc, mx::seg_scale_at(sg.as, j, aok, q, st0, steps, nch),
+                                 mx::seg_scale_at(sg.bs, j, true, q, st0, steps, nch));
     return acc;
 }
 
@@ -98,10 +103,10 @@ __device__ __forceinline__ mx::v4f kloop(const uint8_t* wrow, const uint8_t* sro
     load_seg(s0, wrow, srow, arow, asrow, aok, q, 0, steps, nch);
     for (int st = 0; st < steps; st += 2 * kSegB) {
         if (st + kSegB < steps) load_seg(s1, wrow, srow, arow, asrow, aok, q, st + kSegB, steps, nch);
-        acc = mma_seg(s0, st, steps, acc);
+        acc = mma_seg(s0, aok, q, st, steps, nch, acc);
         if (st + kSegB >= steps) break;
         if (st + 2 * kSegB < steps) load_seg(s0, wrow, srow, arow, asrow, aok, q, st + 2 * kSegB, steps, nch);
-        acc = mma_seg(s1, st + kSegB, steps, acc);
+        acc = mma_seg(s1, aok, q, st + kSegB, steps, nch, acc);
     }
     return acc;
 }
@@ -114,6 +119,11 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
     const int S = a.M * a.E;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int e = a.ids[s];
+    // the down launch adds two halves into y: the workgroups of slot 0 clear it
+    if (s == 0) {
+        const int n = a.M * a.H, per = (n + gridDim.x - 1) / gridDim.x;
+        for (int i = rb * per + tid; i < min(n, (rb + 1) * per); i += 256) a.y[i] = 0.0f;
+    }
     // ---- the first slot naming expert e owns it and gathers its tokens
     if (wave == 0) {
         bool dup = false;
@@ -179,6 +189,10 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
     }
 }
 
+// Two workgroups per column block, each with every other owner (owners k
+// with k % 2 == half): a wave walks half as many experts.  Each adds its
+// partial sums into y, which the gate/up launch cleared: y = (0 + p_a) + p_b,
+// the same bits in either arrival order (fp32 addition commutes).
 __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a) {
     __shared__ int s_ids[kMaxSlots];
     __shared__ int s_owner[kMaxSlots];
@@ -186,7 +200,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     __shared__ int s_nown;
     __shared__ int s_mem[kDownWaves][kMaxTok];
     __shared__ float ypart[kDownWaves][kMaxTok][17];
-    const int cb = blockIdx.x;
+    const int cb = blockIdx.x >> 1, half = blockIdx.x & 1;
     const int S = a.M * a.E;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q = lane >> 4;
@@ -217,8 +231,8 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     const int H = a.H, Mi = a.Mi;
     const int nch = Mi / 32, steps = (nch + 3) / 4;
     const int col = cb * 16 + l16;   // this lane's weight row of down = output column
-    // wave w: owners w, w + kDownWaves, ...
-    for (int k = wave; k < nown; k += kDownWaves) {
+    // wave w of half h: owners 2 w + h, 2 (w + kDownWaves) + h, ...
+    for (int k = 2 * wave + half; k < nown; k += 2 * kDownWaves) {
         const int slot0 = s_owner[k];
         const int e = s_ids[slot0];
         // the owner's slots (one per token), in slot order
@@ -259,7 +273,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
         float v = 0.0f;
 #pragma unroll
         for (int w = 0; w < kDownWaves; ++w) v += ypart[w][m][c];
-        a.y[(int64_t)m * H + cb * 16 + c] = v;
+        __hip_atomic_fetch_add(a.y + (int64_t)m * H + cb * 16 + c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -316,7 +330,7 @@ int launch_batch(const BatchArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(batch_gateup_kernel, dim3(a.Mi / 32, S), dim3(256), 0, st, a);
     const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
     if (rc != MXFP4_OK) return rc;
-    hipLaunchKernelGGL(batch_down_kernel, dim3(a.H / 16), dim3(64 * kDownWaves), 0, st, a);
+    hipLaunchKernelGGL(batch_down_kernel, dim3(2 * (a.H / 16)), dim3(64 * kDownWaves), 0, st, a);
     return mxh::launch_status("moe_decode_batch (down)");
 }
 
