@@ -96,33 +96,39 @@ __device__ __forceinline__ uint32_t e2m1_pack8(const float v[8], float inv) {
 // MFMA K-steps st0 .. st0+3 of a lane in group q (block 4*st + q at step st)
 // need the scale bytes 4*(st0 + j) + q, j < 4, of one row: bytes [4*st0,
 // 4*st0 + 16) of the row hold them all, so when that span lies inside the
-// row one 16-byte load (or two 8-byte loads on 8-byte aligned rows) replaces
-// the four byte loads; byte j of the lane is byte q of dword j.
-__device__ __forceinline__ void seg_scales(uint32_t out[4], const uint8_t* srow, bool ok, int q, int st0,
-                                           int steps, int nch) {
+// row and the row address is 8-byte aligned, two 8-byte loads replace the
+// four byte loads (byte j of the lane is then byte q of dword j); otherwise
+// the lane loads its four bytes (addresses clamped into the row).
+//
+// The loads only fill registers: the byte is picked at use (seg_scale_at).
+// A load result consumed while a segment is still being issued makes the
+// compiler wait for every load in flight there, which turns the prefetch of
+// a segment into one memory round trip per segment.
+struct SegScales {
+    uint32_t d[4];
+    bool words;   // d holds dwords (pick byte q) rather than the lane's bytes
+};
+
+__device__ __forceinline__ void seg_scales_issue(SegScales& r, const uint8_t* srow, int q, int st0, int nch) {
     const uint8_t* p = srow + 4 * st0;
-    const uintptr_t ad = reinterpret_cast<uintptr_t>(p);
-    if (ok && 4 * st0 + 16 <= nch && (ad & 7) == 0) {
-        uint32_t d[4];
-        if ((ad & 15) == 0) {
-            const uint4 v = *reinterpret_cast<const uint4*>(p);
-            d[0] = v.x; d[1] = v.y; d[2] = v.z; d[3] = v.w;
-        } else {
-            const uint2 v0 = *reinterpret_cast<const uint2*>(p), v1 = *reinterpret_cast<const uint2*>(p + 8);
-            d[0] = v0.x; d[1] = v0.y; d[2] = v1.x; d[3] = v1.y;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) out[j] = (st0 + j < steps) ? (d[j] >> (8 * q)) & 0xFFu : 127u;
+    r.words = 4 * st0 + 16 <= nch && (reinterpret_cast<uintptr_t>(p) & 7) == 0;
+    if (r.words) {
+        const uint2 v0 = *reinterpret_cast<const uint2*>(p), v1 = *reinterpret_cast<const uint2*>(p + 8);
+        r.d[0] = v0.x; r.d[1] = v0.y; r.d[2] = v1.x; r.d[3] = v1.y;
     } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int c = 4 * (st0 + j) + q;
-            out[j] = (ok && st0 + j < steps && c < nch) ? (uint32_t)srow[c] : 127u;
-        }
+        for (int j = 0; j < 4; ++j) r.d[j] = srow[min(4 * (st0 + j) + q, nch - 1)];
     }
 }
 
-// Out-of-range steps or blocks, and !ok, give code 127 (scale 1, zero data).
+// The scale code of step st0 + j; out-of-range steps or blocks, and !ok,
+// give code 127 (scale 1, zero data).
+__device__ __forceinline__ uint32_t seg_scale_at(const SegScales& r, int j, bool ok, int q, int st0, int steps,
+                                                 int nch) {
+    const uint32_t v = r.words ? (r.d[j] >> (8 * q)) & 0xFFu : r.d[j];
+    return (ok && st0 + j < steps && 4 * (st0 + j) + q < nch) ? v : 127u;
+}
+
 
 // ---------------------------------------------------------------- FP4 decode
 // E2M1 nibble -> fp32 (used by reference-style epilogues and tests only).
