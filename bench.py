@@ -238,26 +238,41 @@ def time_graph(torch, graph, steps, warmup):
     return start.elapsed_time(end) / steps  # ms per replay
 
 
-def dropin_graph(torch, dext, layers, routes, x0):
+def dropin_step_fn(torch, dext, layers, routes, x0):
     """The drop-in operator path of runtime/model_runner_v2.py:185-208 (prequant,
-    moe_gateup, moe_down, moe_combine, residual add) for the same routing."""
+    moe_gateup, moe_down, moe_combine, residual add) for the same routing, as a
+    function that runs the 48 layers once.  Each routed expert's six tensors
+    are resident per-expert tensors, as the reference's weight store hands
+    them out (runtime/weight_store.py load_layer_experts); the per-layer
+    tables are built from them in the loop, as the reference's runner does."""
     ti, tv = routes
+    w_dev = [tv[0, L].view(1, TOPK).cuda() for L in range(len(layers))]
+    ids_all = [ti[0, L].tolist() for L in range(len(layers))]
+    experts = [{e: {"gate": {"wp": lay.gate_wp[e], "wsc": lay.gate_ws[e]},
+                    "up": {"wp": lay.up_wp[e], "wsc": lay.up_ws[e]},
+                    "down": {"wp": lay.down_wp[e], "wsc": lay.down_ws[e]}} for e in set(ids_all[L])}
+               for L, lay in enumerate(layers)]
 
     def step_fn():
         x = x0.view(1, H)
-        for L, lay in enumerate(layers):
-            ids = ti[0, L].tolist()
+        for L in range(len(layers)):
+            ids, ex = ids_all[L], experts[L]
             xq, xs = dext.prequant(x)
-            gw = [lay.gate_wp[e] for e in ids] + [lay.up_wp[e] for e in ids]
-            gs = [lay.gate_ws[e] for e in ids] + [lay.up_ws[e] for e in ids]
+            gw = [ex[e]["gate"]["wp"] for e in ids] + [ex[e]["up"]["wp"] for e in ids]
+            gs = [ex[e]["gate"]["wsc"] for e in ids] + [ex[e]["up"]["wsc"] for e in ids]
             gu = dext.moe_gateup(xq, xs, gw, gs, TOPK, 1, MI, H)
-            yd = dext.moe_down(gu, [lay.down_wp[e] for e in ids], [lay.down_ws[e] for e in ids],
+            yd = dext.moe_down(gu, [ex[e]["down"]["wp"] for e in ids], [ex[e]["down"]["wsc"] for e in ids],
                                TOPK, 1, H, MI)
             moe = dext.moe_combine(yd, w_dev[L], 1)[0]
             x = x + moe.bfloat16().unsqueeze(0)
         return x
 
-    w_dev = [tv[0, L].view(1, TOPK).cuda() for L in range(len(layers))]
+    return step_fn
+
+
+def dropin_graph(torch, dext, layers, routes, x0):
+    """The drop-in path captured in one graph (device time without host overhead)."""
+    step_fn = dropin_step_fn(torch, dext, layers, routes, x0)
     step_fn()
     torch.cuda.synchronize()
     side = torch.cuda.Stream()
@@ -270,6 +285,36 @@ def dropin_graph(torch, dext, layers, routes, x0):
             step_fn()
     torch.cuda.synchronize()
     return graph
+
+
+def dropin_eager(torch, layers, routes, x0, reps=20):
+    """The drop-in path run eagerly, as the reference's eager runner calls it,
+    through each binding: wall time per layer (host issue or device, whichever
+    bounds), and the time until the host has issued the whole loop (before
+    the final synchronisation; equal to the wall time when the host bounds).
+    The outputs of the two bindings are checked bit-equal."""
+    from moe_fused_inference_amd import get_decode_ext
+    res, outs = {}, {}
+    for binding in ("compiled", "ctypes"):
+        fn = dropin_step_fn(torch, get_decode_ext(binding), layers, routes, x0)
+        outs[binding] = fn()
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        t1 = time.perf_counter()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) / (reps * len(layers)) * 1e6
+        issue = (t1 - t0) / (reps * len(layers)) * 1e6
+        res[binding] = {"us_per_layer": round(wall, 3), "host_issue_us_per_layer": round(issue, 3)}
+    if not torch.equal(outs["compiled"], outs["ctypes"]):
+        raise RuntimeError("the compiled and ctypes bindings give different drop-in outputs")
+    res["note"] = ("eager (no graph) 48-layer drop-in loop as the reference's runner issues it: table lists "
+                   "from resident per-expert tensors, 4 ops, a bf16 cast and a torch add per layer; wall time "
+                   "per layer; outputs of both bindings bit-equal")
+    return res
 
 
 # ----------------------------------------------------------------------------- prefill
@@ -634,6 +679,7 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
         dg = dropin_graph(torch, dext, layers, routes, x0)
         ms_d = time_graph(torch, dg, args.steps, args.warmup)
         log(f"drop-in path: {ms_d * 1e3 / LAYERS:.3f} us/layer")
+        log(f"drop-in path, eager: {dropin_eager(torch, layers, routes, x0)}")
     elif args.only == "gemm":
         for (M, N, K) in ((512, 1536, 2048), (2048, 2048, 768), (4096, 4096, 2048)):
             log(f"gemm {M}x{N}x{K}: {bench_gemm(torch, lext, dext, M, N, K)}")
@@ -740,6 +786,8 @@ def main():
                                 "note": "prequant + moe_gateup + moe_down + moe_combine + bf16 residual "
                                         "(torch add), graph-captured, activations MXFP4 as the reference"}
         log(f"drop-in path: {us_d:.3f} us/layer")
+        extra["dropin_eager"] = dropin_eager(torch, layers, routes, x0)
+        log(f"drop-in path, eager: {extra['dropin_eager']}")
         rg, keep = devroute_graph(torch, layers, draw_logits(torch, S_ROUTES, LAYERS, seed=7), x0, ws, outs,
                                   bufs, routes)
         ms_r = time_graph(torch, rg, max(3, args.steps // 2), 2)

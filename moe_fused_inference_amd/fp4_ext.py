@@ -11,10 +11,24 @@ src/ext/mxfp4_decode_binding.cpp:44-243.  Underneath, every op is one or
 two calls into the C ABI of include/mxfp4_hip.h (libmxfp4_hip.so, gfx950),
 launched on torch's current HIP stream; outputs are allocated with torch's
 caching allocator on the input's device, as the reference does.
+
+Two bindings carry that surface:
+  * ``binding="compiled"`` (the default, as the reference's loaders return
+    compiled pybind modules): the submodules ``linear`` and ``decode`` of
+    ``lib/mxfp4_ext.so``, built by ``build.py`` from ``csrc/torch_binding.cpp``;
+  * ``binding="ctypes"``: the Python classes below, over ctypes.
+Both check the same arguments with the same messages and make the same
+C-ABI calls, so their outputs are bit-identical; they differ in host time
+per call.  Neither has a fallback: a missing library raises ImportError.
 """
+import importlib.util
+import os
+
 import torch
 
 from . import _lib
+
+EXT_PATH = os.path.join(os.path.dirname(_lib.LIB_PATH), "mxfp4_ext.so")
 
 _DT = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
 
@@ -133,6 +147,7 @@ class DecodeExt:
         """out[m,c] = sum_{e<min(E,8)} w[m,e]*yd[m*E+e,c] -> f32 (M,N); E = w.numel()/M."""
         yd, w = yd.contiguous(), w.contiguous()
         M = int(M)
+        _require(M > 0, "w (M,E)")
         E = int(w.numel()) // M
         N = int(yd.shape[1])
         _require(M * E == w.numel(), "w (M,E)")
@@ -206,21 +221,41 @@ class DecodeExt:
                                             dpos.data_ptr(), M, Hkv, D, max_pos, _stream(k)), "kv_write")
 
 
-_ext = None
-_dext = None
+_compiled = None
+_ctypes = {}
 
 
-def get_ext():
+def load_compiled():
+    """The compiled binding module (once).  Raises ImportError if it is not built."""
+    global _compiled
+    if _compiled is None:
+        _lib.load()
+        if not os.path.exists(EXT_PATH):
+            raise ImportError(
+                f"moe_fused_inference_amd: torch binding not built ({EXT_PATH}); "
+                "run `python -m moe_fused_inference_amd.build` (or __graft_entry__.build())")
+        spec = importlib.util.spec_from_file_location("mxfp4_ext", EXT_PATH)
+        mod = importlib.util.module_from_spec(spec)
+        spec.loader.exec_module(mod)
+        _compiled = mod
+    return _compiled
+
+
+def _get(binding, sub, cls):
+    if binding == "compiled":
+        return getattr(load_compiled(), sub)
+    if binding == "ctypes":
+        if cls not in _ctypes:
+            _ctypes[cls] = cls()
+        return _ctypes[cls]
+    raise ValueError(f"binding must be 'compiled' or 'ctypes', got {binding!r}")
+
+
+def get_ext(binding="compiled"):
     """Counterpart of runtime/fp4_ext.py:21-39 (module ``mxfp4_linear_ext``)."""
-    global _ext
-    if _ext is None:
-        _ext = LinearExt()
-    return _ext
+    return _get(binding, "linear", LinearExt)
 
 
-def get_decode_ext():
+def get_decode_ext(binding="compiled"):
     """Counterpart of runtime/fp4_ext.py:46-62 (module ``mxfp4_decode_ext``)."""
-    global _dext
-    if _dext is None:
-        _dext = DecodeExt()
-    return _dext
+    return _get(binding, "decode", DecodeExt)

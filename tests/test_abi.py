@@ -82,10 +82,12 @@ def test_argument_checks_fail_on_host(lib, call, msg):
     assert msg in lib.mxfp4_last_error().decode()
 
 
-def test_python_surface_checks_mirror_reference(lib):
-    """RuntimeError messages of src/ext/*_binding.cpp, raised before launch."""
+@pytest.mark.parametrize("binding", ["compiled", "ctypes"])
+def test_python_surface_checks_mirror_reference(lib, binding):
+    """RuntimeError messages of src/ext/*_binding.cpp, raised before launch,
+    through the compiled binding and the ctypes one."""
     from moe_fused_inference_amd import get_decode_ext, get_ext
-    d, l = get_decode_ext(), get_ext()
+    d, l = get_decode_ext(binding), get_ext(binding)
     x = torch.zeros(1, 64, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="x must be cuda"):
         d.prequant(x)
@@ -104,11 +106,30 @@ def test_python_surface_checks_mirror_reference(lib):
         d.moe_down(torch.zeros(2, 128), [w8] * 2, [w8] * 2, 2, 1, 8, 64)
     with pytest.raises(RuntimeError, match="w \\(M,E\\)"):
         d.moe_combine(torch.zeros(4, 8), torch.zeros(5), 2)
+    with pytest.raises(RuntimeError, match="w \\(M,E\\)"):
+        d.moe_combine(torch.zeros(4, 8), torch.zeros(4), 0)
     with pytest.raises(RuntimeError, match="yd \\(M\\*E,N\\)"):
         d.moe_combine(torch.zeros(5, 8), torch.zeros(4), 2)
     with pytest.raises(TypeError):
         d.moe_down(torch.zeros(2, 128), [w8] * 2, [w8] * 2, 2, 8, 64)  # stale 6-arg call
+    kv = torch.zeros(16, 4, 128, dtype=torch.uint8)
+    dpos = torch.zeros(1, dtype=torch.int32)
     with pytest.raises(RuntimeError, match="q must be a cuda bf16"):
-        d.attn_decode(torch.zeros(1, 32, 128, dtype=torch.bfloat16), None, None, None, None, 1)
+        d.attn_decode(torch.zeros(1, 32, 128, dtype=torch.bfloat16), kv, kv, dpos, torch.zeros(1), 1)
     with pytest.raises(RuntimeError, match="k/v must be cuda bf16"):
-        d.kv_write(torch.zeros(1, 4, 128), torch.zeros(1, 4, 128), None, None, None, 1)
+        d.kv_write(torch.zeros(1, 4, 128), torch.zeros(1, 4, 128), kv, kv, dpos, 1)
+
+
+def test_compiled_binding_surface(lib):
+    """The compiled module carries exactly the reference extensions' op names
+    (src/ext/mxfp4_binding.cpp:47-50, src/ext/mxfp4_decode_binding.cpp:232-243)."""
+    from moe_fused_inference_amd import fp4_ext, get_decode_ext, get_ext
+    d, l = get_decode_ext(), get_ext()
+    assert d.__file__ == l.__file__ == fp4_ext.EXT_PATH
+    assert d.__name__ == "mxfp4_decode_ext" and l.__name__ == "mxfp4_linear_ext"
+    ops = {n for n in dir(d) if not n.startswith("_")}
+    assert ops == {"prequant", "lin_pq", "moe_gateup", "moe_down", "moe_combine", "moe_gateup_tab",
+                   "moe_down_tab", "attn_decode", "kv_write"}
+    assert {n for n in dir(l) if not n.startswith("_")} == {"forward"}
+    with pytest.raises(ValueError):
+        get_decode_ext("eager")

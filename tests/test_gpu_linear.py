@@ -12,6 +12,7 @@ import torch
 
 from oracle import mxfp4 as fmt
 from oracle import ops
+from moe_fused_inference_amd import _lib
 from tests.gpu_helpers import DEV, assert_close, log, np_
 
 pytestmark = pytest.mark.gpu
@@ -77,7 +78,7 @@ def test_forward_equals_prequant_then_lin_pq(dext, lext):
     wp, wsc, _, _ = _w(dext, N, K, seed=5)
     x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(DEV).half()
     y1 = lext.forward(x, wp, wsc)
-    lib = dext._lib
+    lib = _lib.load()
     Kp = 2048
     xq = torch.empty((M, Kp // 2), dtype=torch.uint8, device=DEV)
     xs = torch.empty((M, Kp // 32), dtype=torch.uint8, device=DEV)

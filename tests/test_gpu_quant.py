@@ -12,6 +12,7 @@ import torch
 
 from oracle import mxfp4 as fmt
 from oracle import ops
+from moe_fused_inference_amd import _lib
 from tests.gpu_helpers import DEV, log, np_
 
 pytestmark = pytest.mark.gpu
@@ -82,7 +83,7 @@ def test_prequant_edge_blocks(dext):
 
 def test_prequant_strided_and_unaligned_input(dext):
     """Row stride > K and a 2-byte-aligned base take the element path."""
-    lib = dext._lib
+    lib = _lib.load()
     rng = np.random.default_rng(3)
     big = torch.from_numpy(rng.standard_normal((6, 200)).astype(np.float32)).to(DEV).bfloat16()
     for off, K in [(0, 150), (1, 150), (3, 64)]:
@@ -103,7 +104,7 @@ def test_prequant_strided_and_unaligned_input(dext):
 def test_quantize_rows_dtypes_and_f16_rounding(dext, src):
     """mxfp4_quantize_rows on fp16/fp32 input, and the fp16 pre-rounding of
     `forward` (round_to_f16=1) on bf16/fp32 input."""
-    lib = dext._lib
+    lib = _lib.load()
     rng = np.random.default_rng(4)
     x = (rng.standard_normal((7, 300)) * np.exp2(rng.integers(-20, 20, size=(7, 1)))).astype(np.float32)
     dt = {"bf16": (torch.bfloat16, 0), "f16": (torch.float16, 1), "f32": (torch.float32, 2)}[src]
