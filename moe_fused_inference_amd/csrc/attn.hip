@@ -169,25 +169,28 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         constexpr int QR = (R + 3) / 4;
         constexpr int NR = (2 * kMaxFusedM + 3) / 4;
         float qa[QR], qb[QR], ka[NR], kb[NR];
+        const uint16_t wqa = fz.qw[lane], wqb = fz.qw[lane + 64], wka = fz.kw[lane], wkb = fz.kw[lane + 64];
+        // (unconditional loads of clamped rows, unused values zeroed after:
+        // a load inside a branch would be waited for before the branch joins)
 #pragma unroll
         for (int i = 0; i < QR; ++i) {
             const int r = wave + 4 * i, m = m0 + r / G;
-            qa[i] = qb[i] = 0.0f;
-            if (r < R && m < M) {   // wave-uniform
-                const float* row = fz.qkv + ((int64_t)m * nh + g * G + r % G) * kD;
-                qa[i] = row[lane];
-                qb[i] = row[lane + 64];
-            }
+            const float* row = fz.qkv + ((int64_t)min(m, M - 1) * nh + g * G + r % G) * kD;
+            qa[i] = row[lane];
+            qb[i] = row[lane + 64];
         }
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
-            const int t = wave + 4 * j, p = n_lo + (t >> 1);
-            ka[j] = kb[j] = 0.0f;
-            if (p < n_hi) {
-                const float* row = fz.qkv + ((int64_t)(p - base) * nh + (t & 1 ? Hq + Hkv : Hq) + g) * kD;
-                ka[j] = row[lane];
-                kb[j] = row[lane + 64];
-            }
+            const int t = wave + 4 * j, tok = min(max(n_lo + (t >> 1) - base, 0), M - 1);
+            const float* row = fz.qkv + ((int64_t)tok * nh + (t & 1 ? Hq + Hkv : Hq) + g) * kD;
+            ka[j] = row[lane];
+            kb[j] = row[lane + 64];
+        }
+#pragma unroll
+        for (int i = 0; i < QR; ++i) {
+            const bool ok = m0 + (wave + 4 * i) / G < M;
+            qa[i] = ok ? qa[i] : 0.0f;
+            qb[i] = ok ? qb[i] : 0.0f;
         }
         // RoPE cos / sin of every position the workgroup needs -- its own
         // tokens and the step's rows in its chunk -- once per (token, lane)
@@ -201,17 +204,16 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
         __syncthreads();
         // q: RMSNorm + RoPE at the token's position, bf16 into LDS
+        // (no branch per row, so the rows' reductions can interleave; rows
+        // of tokens past M are computed on zeros and stored as zeros)
 #pragma unroll
         for (int i = 0; i < QR; ++i) {
             const int r = wave + 4 * i, m = m0 + r / G;
-            if (r >= R) break;
-            uint16_t ba = 0, bb = 0;
-            if (m < M) {   // wave-uniform
-                hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(fz.qw[lane]), mx::bf16_to_f32(fz.qw[lane + 64]), fz.eps,
-                              rcs[m][lane], ba, bb);
-            }
-            qs[r][lane] = ba;
-            qs[r][lane + 64] = bb;
+            uint16_t ba, bb;
+            hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(wqa), mx::bf16_to_f32(wqb), fz.eps, rcs[min(m, M - 1)][lane],
+                          ba, bb);
+            qs[r][lane] = m < M ? ba : (uint16_t)0;
+            qs[r][lane + 64] = m < M ? bb : (uint16_t)0;
         }
         // the new rows: k (RMSNorm + RoPE) and bf16(v) as cache bytes, to
         // LDS, and the rows of this workgroup's tokens to the cache
@@ -226,8 +228,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
                 e1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(kb[j]));
             } else {        // k: RMSNorm + RoPE at its position
                 uint16_t ba, bb;
-                hr::norm_rope(ka[j], kb[j], mx::bf16_to_f32(fz.kw[lane]), mx::bf16_to_f32(fz.kw[lane + 64]), fz.eps,
-                              rcs[m][lane], ba, bb);
+                hr::norm_rope(ka[j], kb[j], mx::bf16_to_f32(wka), mx::bf16_to_f32(wkb), fz.eps, rcs[m][lane], ba, bb);
                 e0 = mx::bf16_to_f32(ba);
                 e1 = mx::bf16_to_f32(bb);
             }
@@ -288,9 +289,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
             const bool ok = m >= mv_lo && m <= mv_hi && s <= base + m;
             if (ok) sc[((int64_t)m * Hq + g * G + r % G) * max_pos + s] = sacc[rt][i];
             x[rt][i] = ok ? sacc[rt][i] * invsqrt : -INFINITY;
-            float mxv = x[rt][i];
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) mxv = fmaxf(mxv, __shfl_xor(mxv, o));
+            const float mxv = mx::row16_reduce<true>(x[rt][i]);
             if (l16 == 0) red[wave][r] = mxv;
         }
     __syncthreads();
@@ -306,9 +305,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
             const uint16_t hi = mx::f32_to_bf16_rne(p);
             phi[r][wave * 16 + l16] = hi;
             plo[r][wave * 16 + l16] = mx::f32_to_bf16_rne(p - mx::bf16_to_f32(hi));
-            float sum = p;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sum += __shfl_xor(sum, o);
+            const float sum = mx::row16_reduce<false>(p);
             if (l16 == 0) red[wave][r] = sum;
         }
     __syncthreads();
@@ -478,14 +475,12 @@ __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict
         // MXFP4 of bf16(o): a 32-block is 16 lanes; the quantizer's rule
         const float v0 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r0));
         const float v1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r1));
-        float am = fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1));
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) am = fmaxf(am, __shfl_xor(am, off));
+        const float am = mx::row16_reduce<true>(fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1)));
         const uint32_t code = mx::e8m0_code(am);
         const float inv = mx::e8m0_inv_scale(code);
         uint32_t byte = mx::e2m1_code(v0 * inv) | (mx::e2m1_code(v1 * inv) << 4);
-        byte |= (uint32_t)__shfl_down((int)byte, 1) << 8;
-        byte |= (uint32_t)__shfl_down((int)byte, 2) << 16;
+        byte |= (uint32_t)mx::dpp<mx::kDppQuadNext1>((int)byte) << 8;    // lane 4j: bytes of 4j..4j+3
+        byte |= (uint32_t)mx::dpp<mx::kDppQuadNext2>((int)byte) << 16;
         const int64_t rowq = (int64_t)m * (Hq * kD / 2) + h * (kD / 2);
         if ((lane & 3) == 0) *reinterpret_cast<uint32_t*>(oq + rowq + lane) = byte;
         if ((lane & 15) == 0) os[(int64_t)m * (Hq * kD / 32) + h * (kD / 32) + lane / 16] = (uint8_t)code;

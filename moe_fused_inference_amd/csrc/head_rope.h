@@ -18,12 +18,11 @@ __device__ __forceinline__ float2 rope_cs(float theta, int lane, int pos) {
 
 // RMSNorm of the fp32 head (a = element lane, b = element lane + 64) with the
 // bf16 weight (wa, wb), rounded to bf16, then RoPE in fp32 and bf16 again.
-// Every lane of the wave must call it (the sum of squares is a wave sum).
+// Every lane of the wave must call it (the sum of squares is a wave sum, by
+// DPP within rows of 16 lanes and then across the four rows).
 __device__ __forceinline__ void norm_rope(float a, float b, float wa, float wb, float eps, float2 cs,
                                           uint16_t& ba, uint16_t& bb) {
-    float ss = fmaf(a, a, b * b);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    const float ss = mx::wave_reduce_dpp<false>(fmaf(a, a, b * b));
     const float r = 1.0f / sqrtf(ss / 128.0f + eps);
     const float na = mx::bf16_to_f32(mx::f32_to_bf16_rne((a * r) * wa));
     const float nb = mx::bf16_to_f32(mx::f32_to_bf16_rne((b * r) * wb));

@@ -215,18 +215,44 @@ __device__ __forceinline__ float silu_mul_fast(float g, float u) {
     return g * __builtin_amdgcn_rcpf(1.0f + e) * u;
 }
 
-// Reduction over the wave, result in every lane: DPP within rows of 16 lanes
-// (quad xor 1, xor 2, half-row mirror, row mirror: each step combines
-// disjoint lane sets, so every lane ends with its row's total), then the four
-// row results.  For the maximum, NaN inputs are ignored (maxNum), so NaN can
-// mark "no value".
+// Lane exchanges by DPP (a VALU operand modifier, no LDS round trip; a
+// shuffle through ds_bpermute costs an LDS-path latency per step).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, true));
+}
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true);
+}
+constexpr int kDppQuadXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppQuadNext1 = 0xF9;       // quad_perm [1,2,3,3]: lane q*4 reads q*4+1
+constexpr int kDppQuadNext2 = 0xEE;       // quad_perm [2,3,2,3]: lane q*4 reads q*4+2
+constexpr int kDppRowHalfMirror = 0x141;  // lane i of 8 reads 7 - i
+constexpr int kDppRowMirror = 0x140;      // lane i of 16 reads 15 - i
+
+// Reduction over each row of 16 lanes, the row's total in every lane of it.
+// Quad xor 1, quad xor 2, half-row mirror, row mirror: after the quad steps
+// every lane of a quad holds the same value, so the mirrors pair each quad
+// (half-row) with the same other one as xor 4 (xor 8) would, and the result
+// has the bits of the xor-1,2,4,8 butterfly (the operations are commutative).
+template <bool MAX>
+__device__ __forceinline__ float row16_reduce(float v) {
+    auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
+    v = op(v, dpp<kDppQuadXor1>(v));
+    v = op(v, dpp<kDppQuadXor2>(v));
+    v = op(v, dpp<kDppRowHalfMirror>(v));
+    return op(v, dpp<kDppRowMirror>(v));
+}
+
+// Reduction over the wave, result in every lane: the row reduction above,
+// then the four row results ((r0 op r1) op (r2 op r3)).  For the maximum,
+// NaN inputs are ignored (maxNum), so NaN can mark "no value".
 template <bool MAX>
 __device__ __forceinline__ float wave_reduce_dpp(float v) {
     auto op = [](float a, float b) { return MAX ? fmaxf(a, b) : a + b; };
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)));
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)));
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)));
-    v = op(v, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)));
+    v = row16_reduce<MAX>(v);
     return op(op(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0)),
                  __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16))),
               op(__int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32)),
