@@ -162,7 +162,9 @@ int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, con
  * be the MXFP4 rows of bf16(o), the activation of the o_proj lin_pq
  * (runtime/model_runner_v2.py:175-178: o.bfloat16() -> prequant): oq u8
  * (M, Hq*D/2) and os u8 (M, Hq*D/32), bit-exact to mxfp4_quantize_rows of
- * o with bf16 rounding (mode 2).  o may be NULL when oq/os are given. */
+ * o with bf16 rounding (mode 2).  o may be NULL when oq/os are given, and
+ * sc may be NULL (the raw scores are then not kept: a caller that never
+ * reads them saves M*Hq*(dpos+M) four-byte stores). */
 int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
                          float* sc, float* o, uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D,
                          int max_pos, void* workspace, size_t workspace_bytes, void* stream);
@@ -177,7 +179,8 @@ int mxfp4_attn_decode_mx(const void* q, const uint8_t* kvk, const uint8_t* kvv, 
  * RoPE (runtime/model_runner_v2.py:155-163), kv_write and attn_decode
  * (src/ext/mxfp4_decode.cu:352-490) as separate launches; it saves a launch
  * and a memory round trip per layer.  M <= 16, D = 128; codec as
- * mxfp4_qk_norm_rope_kv; workspace as mxfp4_attn_decode. */
+ * mxfp4_qk_norm_rope_kv; workspace as mxfp4_attn_decode; o and sc may be
+ * NULL as for mxfp4_attn_decode_mx. */
 int mxfp4_attn_decode_fused(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
                             float theta, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos, float* sc, float* o,
                             uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, int codec,

@@ -203,17 +203,43 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
             if (own || newrow) rcs[jm][lane] = hr::rope_cs(fz.theta, lane, base + jm);
         }
         __syncthreads();
-        // q: RMSNorm + RoPE at the token's position, bf16 into LDS
-        // (no branch per row, so the rows' reductions can interleave; rows
-        // of tokens past M are computed on zeros and stored as zeros)
+        // q: RMSNorm + RoPE at the token's position, bf16 into LDS; rows of
+        // tokens past M are zeros.  No branch per row, so the rows'
+        // reductions can interleave.  With G % 4 == 0 a wave's rows of token
+        // m0 + tt are i = tt*G/4 .. (tt+1)*G/4 - 1 (r / G = tt), so one
+        // uniform branch per token skips the tokens past M.
+        if constexpr (G % 4 == 0) {
+            constexpr int RPT = G / 4;
 #pragma unroll
-        for (int i = 0; i < QR; ++i) {
-            const int r = wave + 4 * i, m = m0 + r / G;
-            uint16_t ba, bb;
-            hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(wqa), mx::bf16_to_f32(wqb), fz.eps, rcs[min(m, M - 1)][lane],
-                          ba, bb);
-            qs[r][lane] = m < M ? ba : (uint16_t)0;
-            qs[r][lane + 64] = m < M ? bb : (uint16_t)0;
+            for (int tt = 0; tt < MT; ++tt) {
+                if (m0 + tt < M) {
+#pragma unroll
+                    for (int ii = 0; ii < RPT; ++ii) {
+                        const int i = tt * RPT + ii, r = wave + 4 * i;
+                        uint16_t ba, bb;
+                        hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(wqa), mx::bf16_to_f32(wqb), fz.eps,
+                                      rcs[m0 + tt][lane], ba, bb);
+                        qs[r][lane] = ba;
+                        qs[r][lane + 64] = bb;
+                    }
+                } else {
+#pragma unroll
+                    for (int ii = 0; ii < RPT; ++ii) {
+                        const int r = wave + 4 * (tt * RPT + ii);
+                        qs[r][lane] = qs[r][lane + 64] = 0;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < QR; ++i) {
+                const int r = wave + 4 * i, m = m0 + r / G;
+                uint16_t ba, bb;
+                hr::norm_rope(qa[i], qb[i], mx::bf16_to_f32(wqa), mx::bf16_to_f32(wqb), fz.eps,
+                              rcs[min(m, M - 1)][lane], ba, bb);
+                qs[r][lane] = m < M ? ba : (uint16_t)0;
+                qs[r][lane + 64] = m < M ? bb : (uint16_t)0;
+            }
         }
         // the new rows: k (RMSNorm + RoPE) and bf16(v) as cache bytes, to
         // LDS, and the rows of this workgroup's tokens to the cache
@@ -287,7 +313,7 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
             const int r = rt * 16 + 4 * lq + i;
             const int m = m0 + r / G;
             const bool ok = m >= mv_lo && m <= mv_hi && s <= base + m;
-            if (ok) sc[((int64_t)m * Hq + g * G + r % G) * max_pos + s] = sacc[rt][i];
+            if (ok && sc) sc[((int64_t)m * Hq + g * G + r % G) * max_pos + s] = sacc[rt][i];
             x[rt][i] = ok ? sacc[rt][i] * invsqrt : -INFINITY;
             const float mxv = mx::row16_reduce<true>(x[rt][i]);
             if (l16 == 0) red[wave][r] = mxv;
@@ -517,7 +543,7 @@ template <bool FUSED>
 int launch_attn(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos, float* sc, float* o,
                 uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
                 size_t workspace_bytes, const QkvIn& fz, hipStream_t st) {
-    MXH_REQUIRE(kvk && kvv && dpos && sc && workspace, "attn_decode: null pointer");
+    MXH_REQUIRE(kvk && kvv && dpos && workspace, "attn_decode: null pointer");   // sc may be null: no scores kept
     MXH_REQUIRE(o || oq, "attn_decode: no output (o and oq both null)");
     MXH_REQUIRE(!oq == !os, "attn_decode: oq and os go together");
     MXH_REQUIRE(D == kD, "attn_decode: head_dim D=%d (this build supports %d, as the reference's kernels)", D, kD);
@@ -593,7 +619,7 @@ extern "C" int mxfp4_attn_decode_fused(const float* qkv, const void* q_norm_w, c
 extern "C" int mxfp4_attn_decode(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos,
                                  float* sc, float* o, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
                                  size_t workspace_bytes, void* stream) {
-    MXH_REQUIRE(o, "attn_decode: null pointer");
+    MXH_REQUIRE(o && sc, "attn_decode: null pointer");
     return mxfp4_attn_decode_mx(q, kvk, kvv, dpos, sc, o, nullptr, nullptr, M, Hq, Hkv, D, max_pos, workspace,
                                 workspace_bytes, stream);
 }

@@ -182,7 +182,6 @@ class DecodeStep:
         buf("yq", (M, H // 2), u8)
         buf("ys", (M, H // 32), u8)
         buf("qkv", (M, c.qkv_rows), f32)
-        buf("sc", (M, Hq, self.max_pos), f32)
         buf("aq", (M, Hq * D // 2), u8)
         buf("as_", (M, Hq * D // 32), u8)
         buf("oproj", (M, H), f32)
@@ -267,10 +266,11 @@ class DecodeStep:
                 xa, xb = xb, xa
             kvk, kvv = b.kvk[l], b.kvv[l]
             # q/k head norm + RoPE, the step's KV rows and attention in one
-            # pass, its output straight to MXFP4 of bf16(o) for o_proj
+            # pass, its output straight to MXFP4 of bf16(o) for o_proj (the raw
+            # scores are not kept)
             self._ck(lib.mxfp4_attn_decode_fused(b.qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(),
                                                  c.rms_eps, c.rope_theta, kvk.data_ptr(), kvv.data_ptr(),
-                                                 b.dpos.data_ptr(), b.sc.data_ptr(), None, b.aq.data_ptr(),
+                                                 b.dpos.data_ptr(), None, None, b.aq.data_ptr(),
                                                  b.as_.data_ptr(), M, Hq, Hkv, D, self.max_pos, self.kv_codec,
                                                  b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode_fused")
             self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)

@@ -201,7 +201,7 @@ def test_rmsnorm_lin_pq_equals_the_two_calls(M, N, resid):
     ws = torch.empty((N, H // 32), dtype=torch.uint8, device=DEV)
     _lib.check(lib.mxfp4_prequant(w.data_ptr(), H, N, H, H, wp.data_ptr(), ws.data_ptr(), None), "prequant")
     outs = []
-    for fused in (False, True):
+    for fused in (False, True, "bare"):
         xo = torch.zeros_like(x)
         y = torch.zeros_like(x)
         yq = torch.zeros((M, H // 2), dtype=torch.uint8, device=DEV)
@@ -330,7 +330,8 @@ def test_argmax_slices_match_torch(V):
 def test_attn_decode_fused_matches_two_ops(M, Hq, Hkv, max_pos, base, codec):
     """mxfp4_attn_decode_fused equals qk_norm_rope_kv followed by
     attn_decode_mx on the same projections and cache: the same cache bytes,
-    raw scores, fp32 output and MXFP4 rows, bit for bit."""
+    raw scores, fp32 output and MXFP4 rows, bit for bit; and with sc and o
+    NULL (how the step calls it) the same cache bytes and MXFP4 rows."""
     lib = _lib.load()
     g = torch.Generator(device=DEV)
     g.manual_seed(900 + M + base)
@@ -343,7 +344,7 @@ def test_attn_decode_fused_matches_two_ops(M, Hq, Hkv, max_pos, base, codec):
     cache = ((r & 0x80) | (r & 0x3F)).to(torch.uint8)        # |v| < 2, no NaN code
     wsb = lib.mxfp4_attn_decode_workspace_size(M, Hq, max_pos)
     outs = []
-    for fused in (False, True):
+    for fused in (False, True, "bare"):
         kvk, kvv = cache.clone(), cache.flip(0).contiguous()
         sc = torch.zeros((M, Hq, max_pos), dtype=torch.float32, device=DEV)
         o = torch.zeros((M, Hq * D), dtype=torch.float32, device=DEV)
@@ -351,9 +352,11 @@ def test_attn_decode_fused_matches_two_ops(M, Hq, Hkv, max_pos, base, codec):
         os_ = torch.zeros((M, Hq * D // 32), dtype=torch.uint8, device=DEV)
         ws = torch.zeros(((wsb + 15) // 16 * 16,), dtype=torch.uint8, device=DEV)
         if fused:
+            bare = fused == "bare"
             _lib.check(lib.mxfp4_attn_decode_fused(qkv.data_ptr(), qw.data_ptr(), kw.data_ptr(), 1e-6, 1e6,
-                                                   kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(), sc.data_ptr(),
-                                                   o.data_ptr(), oq.data_ptr(), os_.data_ptr(), M, Hq, Hkv, D, max_pos,
+                                                   kvk.data_ptr(), kvv.data_ptr(), dpos.data_ptr(),
+                                                   None if bare else sc.data_ptr(), None if bare else o.data_ptr(),
+                                                   oq.data_ptr(), os_.data_ptr(), M, Hq, Hkv, D, max_pos,
                                                    codec, ws.data_ptr(), ws.numel(), None), "attn_decode_fused")
         else:
             q = torch.zeros((M, Hq, D), dtype=torch.bfloat16, device=DEV)
@@ -372,4 +375,9 @@ def test_attn_decode_fused_matches_two_ops(M, Hq, Hkv, max_pos, base, codec):
         if name == "sc":
             a, b = a[live], b[live]
         assert torch.equal(a, b), f"M={M} base={base}: {name} differs"
+    for name, a, b in zip(("kvk", "kvv", "sc", "o", "oq", "os"), outs[0], outs[2]):
+        if name == "sc":
+            assert not b.any(), "sc NULL: nothing written"
+        elif name != "o":
+            assert torch.equal(a, b), f"M={M} base={base}: {name} differs without sc / o"
     log(f"  M={M} Hq={Hq} base={base} codec={codec}: fused attention equal to the two launches")
