@@ -111,6 +111,22 @@ __device__ __forceinline__ mx::v4f kloop(const uint8_t* wrow, const uint8_t* sro
     return acc;
 }
 
+// Owners: slot j owns its expert when its id is valid and no earlier slot
+// names the same id.  Every thread of the workgroup holds the ids in LDS; the
+// first-occurrence test reads them as broadcast 16-byte words, so it costs S/4
+// LDS reads per slot with no data-dependent exit.
+__device__ __forceinline__ bool first_occurrence(const int* s_ids, int S, int j, int n_experts) {
+    if (j >= S) return false;
+    const int e = s_ids[j];
+    bool own = e >= 0 && e < n_experts;
+    for (int k0 = 0; k0 < S; k0 += 4) {
+        const int4 v = *reinterpret_cast<const int4*>(s_ids + k0);
+        own &= !((k0 < j && v.x == e) || (k0 + 1 < j && v.y == e) || (k0 + 2 < j && v.z == e) ||
+                 (k0 + 3 < j && v.w == e));
+    }
+    return own;
+}
+
 __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
     __shared__ int s_slot[kMaxTok];
     __shared__ int s_cnt, s_own;
@@ -124,23 +140,22 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
         const int n = a.M * a.H, per = (n + gridDim.x - 1) / gridDim.x;
         for (int i = rb * per + tid; i < min(n, (rb + 1) * per); i += 256) a.y[i] = 0.0f;
     }
-    // ---- the first slot naming expert e owns it and gathers its tokens
+    // ---- the first slot naming expert e owns it and gathers its tokens: all
+    // S <= 128 ids in one round of loads (two per lane), then ballots
     if (wave == 0) {
-        bool dup = false;
-        for (int j = lane; j < s; j += 64) dup |= a.ids[j] == e;
-        const bool any = __ballot(dup) != 0ull;
-        int cnt = 0;
+        const int v0 = lane < S ? a.ids[lane] : -1;
+        const int v1 = 64 + lane < S ? a.ids[64 + lane] : -1;
+        const bool any = __ballot((lane < s && v0 == e) || (64 + lane < s && v1 == e)) != 0ull;
+        const unsigned long long b0 = __ballot(lane >= s && lane < S && v0 == e);
+        const unsigned long long b1 = __ballot(64 + lane >= s && 64 + lane < S && v1 == e);
+        const unsigned long long below = (1ull << lane) - 1ull;
         if (!any) {
-            for (int j0 = s; j0 < S; j0 += 64) {
-                const int j = j0 + lane;
-                const bool mm = j < S && a.ids[j] == e;
-                const unsigned long long b = __ballot(mm);
-                if (mm && cnt + __popcll(b & ((1ull << lane) - 1ull)) < kMaxTok)
-                    s_slot[cnt + __popcll(b & ((1ull << lane) - 1ull))] = j;
-                cnt += __popcll(b);
-            }
+            const int p0 = __popcll(b0 & below), p1 = __popcll(b0) + __popcll(b1 & below);
+            if (((b0 >> lane) & 1ull) && p0 < kMaxTok) s_slot[p0] = lane;
+            if (((b1 >> lane) & 1ull) && p1 < kMaxTok) s_slot[p1] = 64 + lane;
         }
         if (lane == 0) {
+            const int cnt = __popcll(b0) + __popcll(b1);
             s_own = any ? 0 : 1;
             s_cnt = cnt < kMaxTok ? cnt : kMaxTok;
         }
@@ -194,7 +209,7 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
 // partial sums into y, which the gate/up launch cleared: y = (0 + p_a) + p_b,
 // the same bits in either arrival order (fp32 addition commutes).
 __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a) {
-    __shared__ int s_ids[kMaxSlots];
+    __shared__ __align__(16) int s_ids[kMaxSlots];
     __shared__ int s_owner[kMaxSlots];
     __shared__ int s_flag[kMaxSlots];
     __shared__ int s_nown;
@@ -204,16 +219,11 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     const int S = a.M * a.E;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q = lane >> 4;
-    if (tid < S) s_ids[tid] = a.ids[tid];
+    if (tid < kMaxSlots) s_ids[tid] = tid < S ? a.ids[tid] : -1;
     for (int i = tid; i < kDownWaves * kMaxTok * 17; i += 64 * kDownWaves) (&ypart[0][0][0])[i] = 0.0f;
     __syncthreads();
     // owners: slots whose expert no earlier slot names (slot order)
-    if (tid < S) {
-        const int e = s_ids[tid];
-        bool own = e >= 0 && e < a.n_experts;
-        for (int k = 0; k < tid && own; ++k) own = s_ids[k] != e;
-        s_flag[tid] = own ? 1 : 0;
-    }
+    if (tid < S) s_flag[tid] = first_occurrence(s_ids, S, tid, a.n_experts) ? 1 : 0;
     __syncthreads();
     if (wave == 0) {
         int n = 0;
