@@ -213,13 +213,17 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     __shared__ int s_owner[kMaxSlots];
     __shared__ int s_flag[kMaxSlots];
     __shared__ int s_nown;
+    __shared__ float s_w[kMaxSlots];
     __shared__ int s_mem[kDownWaves][kMaxTok];
     __shared__ float ypart[kDownWaves][kMaxTok][17];
     const int cb = blockIdx.x >> 1, half = blockIdx.x & 1;
     const int S = a.M * a.E;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, q = lane >> 4;
-    if (tid < kMaxSlots) s_ids[tid] = tid < S ? a.ids[tid] : -1;
+    if (tid < kMaxSlots) {
+        s_ids[tid] = tid < S ? a.ids[tid] : -1;
+        s_w[tid] = tid < S ? a.w[tid] : 0.0f;   // routing weights: read once, not per owner after its MFMAs
+    }
     for (int i = tid; i < kDownWaves * kMaxTok * 17; i += 64 * kDownWaves) (&ypart[0][0][0])[i] = 0.0f;
     __syncthreads();
     // owners: slots whose expert no earlier slot names (slot order)
@@ -271,7 +275,7 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
             const int r = 4 * q + i;
             if (r < cnt) {
                 const int sl = s_mem[wave][r];
-                ypart[wave][sl / a.E][l16] = fmaf(a.w[sl], acc[i], ypart[wave][sl / a.E][l16]);
+                ypart[wave][sl / a.E][l16] = fmaf(s_w[sl], acc[i], ypart[wave][sl / a.E][l16]);
             }
         }
         __builtin_amdgcn_s_waitcnt(0xC07F);

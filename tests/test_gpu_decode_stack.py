@@ -73,6 +73,42 @@ def test_stack_matches_chained_layers_and_oracle(dext, n_exp, E, H, Mi):
             assert_close(np_(y_all[l]), ref, COS_TIGHT, REL_TIGHT, what=what + " (tight)")
 
 
+@pytest.mark.parametrize("L", [48, 131])
+def test_stack_long_runs(dext, L):
+    """A whole config-2 step (48 layers) and a run past the 128 layers whose
+    routing and weight pointers the kernel stages in LDS (layers 128.. take the
+    scalar-load path): bit-exact against chained one-layer launches, and the
+    oracle on the first, a middle and the last layers.  Every layer has its
+    own seeded weights, as in config 2 (a few stacks reused along the run
+    amplify the residual stream layer after layer until it overflows)."""
+    n_exp, E, H, Mi = 8, 8, 2048, 768
+    layers = [make_stack(dext, n_exp, H, Mi, seed=9100 + 31 * l) for l in range(L)]
+    stack = moe_layer.LayerStack(layers)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(17 + L)
+    x0 = torch.randn(H, generator=g, device=DEV).bfloat16()
+    ids, w = stack_routes(g, n_exp, E, L)
+    # beyond ~50 random layers the residual stream of this synthetic model
+    # grows without bound (x reaches inf near layer 64 in both paths): damp
+    # the long run's combine weights so every layer stays finite
+    w = (w * (0.25 if L > 48 else 1.0)).contiguous()
+    ws = moe_layer.stack_workspace(E, H, Mi)
+    log(f"stack L={L}")
+    x_out, x_all, y_all = moe_layer.decode_stack(x0, ids, w, stack, ws=ws, want_all=True)
+    torch.cuda.synchronize()
+    assert moe_layer.stack_status(ws) == 0
+    cx, cy = chained(x0, ids, w, layers, E)
+    assert torch.equal(y_all, cy), "moe outputs differ from chained one-layer launches"
+    assert torch.equal(x_all, cx), "residual stream differs from chained one-layer launches"
+    assert torch.equal(x_out, cx[-1])
+    assert bool(torch.isfinite(y_all).all()), "non-finite moe output"
+    for l in (0, L // 2, 127 if L > 128 else L - 2, L - 1):
+        xl = x0 if l == 0 else x_all[l - 1]
+        ref = oracle_out(layers[l], xl, ids[l].tolist(), w[l].tolist())
+        assert_close(np_(y_all[l]), ref, COS_NS, REL_NS, what=f"  layer {l}")
+        assert_close(np_(y_all[l]), ref, COS_TIGHT, REL_TIGHT, what=f"  layer {l} (tight)")
+
+
 def test_stack_strict_equals_prefetch(dext):
     n_exp, E, H, Mi = 10, 8, 2048, 768
     layers = [make_stack(dext, n_exp, H, Mi, seed=8100 + i) for i in range(2)] * 3
