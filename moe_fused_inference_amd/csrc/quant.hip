@@ -7,8 +7,8 @@
 //
 // Layout of the work: four consecutive lanes own one 32-block, eight
 // consecutive elements each.  A wave therefore reads 64 x 16 contiguous bytes
-// of bf16 input (fully coalesced), reduces the block amax with two xor
-// shuffles inside each lane quad, and each lane writes the 4 bytes holding
+// of bf16 input (fully coalesced), reduces the block amax with two DPP quad
+// exchanges, and each lane writes the 4 bytes holding
 // its 8 nibbles -- again contiguous across the wave.  The lane with quad index
 // 0 writes the block's scale byte.  HBM-bound: 2 B read + 0.53 B written per
 // element for bf16 input.
@@ -57,16 +57,19 @@ __device__ __forceinline__ void load8(const void* x, int64_t base, int k0, int K
 }
 
 // RND: 0 none, 1 round each element to fp16 first, 2 to bf16 first.
+// Workgroup (row group blockIdx.x, unit segment blockIdx.y): 2^lt threads per
+// row (the units of a row rounded up to a power of two, at most 256), so the
+// row and unit of a thread are shifts and masks, not a division.
 template <int SRC, int RND>
 __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restrict__ x, int64_t ldx,
-                                                            int M, int K, int Kp, int vec,
+                                                            int M, int K, int Kp, int vec, int lt,
                                                             uint8_t* __restrict__ q,
                                                             uint8_t* __restrict__ s) {
     const int upr = Kp >> 3;  // 8-element units per row
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t row = gid / upr;
-    const int u = (int)(gid - row * upr);
-    const bool valid = row < M;
+    const int tid = threadIdx.x;
+    const int64_t row = (int64_t)blockIdx.x * (256 >> lt) + (tid >> lt);
+    const int u = (int)blockIdx.y * (1 << lt) + (tid & ((1 << lt) - 1));
+    const bool valid = row < M && u < upr;
     const int k0 = u * 8;
     float v[8];
     if (valid) {
@@ -86,8 +89,9 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
     float am = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
-    am = fmaxf(am, __shfl_xor(am, 1));
-    am = fmaxf(am, __shfl_xor(am, 2));
+    // the block's four lanes: quad max by DPP
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor1>(am));
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor2>(am));
     const uint32_t code = mx::e8m0_code(am);
     const uint32_t packed = mx::e2m1_pack8(v, mx::e8m0_inv_scale(code));
     if (valid) {
@@ -99,10 +103,13 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
 template <int SRC, int RND>
 void launch_quant(const void* x, int64_t ldx, int M, int K, int Kp, int vec, uint8_t* q, uint8_t* s,
                   hipStream_t st) {
-    const int64_t units = (int64_t)M * (Kp >> 3);
-    const int64_t blocks = (units + 255) / 256;
-    hipLaunchKernelGGL((quantize_rows_kernel<SRC, RND>), dim3((unsigned)blocks), dim3(256), 0, st,
-                       x, ldx, M, K, Kp, vec, q, s);
+    const int upr = Kp >> 3;
+    int lt = 2;                                    // Kp >= 32: at least 4 units per row
+    while ((1 << lt) < upr && lt < 8) ++lt;
+    const int rpw = 256 >> lt;
+    const unsigned gx = (unsigned)((M + rpw - 1) / rpw), gy = (unsigned)((upr + (1 << lt) - 1) >> lt);
+    hipLaunchKernelGGL((quantize_rows_kernel<SRC, RND>), dim3(gx, gy), dim3(256), 0, st,
+                       x, ldx, M, K, Kp, vec, lt, q, s);
 }
 
 }  // namespace
