@@ -489,12 +489,11 @@ __device__ __forceinline__ void tile_epilogue(mx::v16f (&acc)[2][2], const GArgs
             amax = fmaxf(amax, __shfl_xor(amax, 32));
             const uint32_t code = mx::e8m0_code(amax);
             const float inv = mx::e8m0_inv_scale(code);
-            uint32_t piece[4];
+            uint32_t piece[4];   // v is exact in fp16: the hardware codes (mx::e2m1_hw_arg)
 #pragma unroll
             for (int q4 = 0; q4 < 4; ++q4) {
-                piece[q4] = 0;
-#pragma unroll
-                for (int r = 0; r < 4; ++r) piece[q4] |= mx::e2m1_code(v[4 * q4 + r] * inv) << (4 * r);
+                piece[q4] = mx::e2m1_hw_pair<0>(0u, v[4 * q4] * inv, v[4 * q4 + 1] * inv);
+                piece[q4] = mx::e2m1_hw_pair<1>(piece[q4], v[4 * q4 + 2] * inv, v[4 * q4 + 3] * inv);
             }
             // lane h holds features 8*q4 + 4h + 0..3 -> bytes 4*q4 + 2h, +1
             const uint32_t send = h ? (piece[0] | (piece[1] << 16)) : (piece[2] | (piece[3] << 16));

@@ -93,7 +93,9 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const void* __restri
     am = fmaxf(am, mx::dpp<mx::kDppQuadXor1>(am));
     am = fmaxf(am, mx::dpp<mx::kDppQuadXor2>(am));
     const uint32_t code = mx::e8m0_code(am);
-    const uint32_t packed = mx::e2m1_pack8(v, mx::e8m0_inv_scale(code));
+    // fp32 input without rounding keeps the software codes (up to 24 significant bits)
+    const uint32_t packed = (SRC == MXFP4_DT_F32 && RND == 0) ? mx::e2m1_pack8(v, mx::e8m0_inv_scale(code))
+                                                              : mx::e2m1_pack8_short(v, mx::e8m0_inv_scale(code));
     if (valid) {
         *reinterpret_cast<uint32_t*>(q + row * (int64_t)(Kp >> 1) + (u << 2)) = packed;
         if ((u & 3) == 0) s[row * (int64_t)(Kp >> 5) + (u >> 2)] = (uint8_t)code;

@@ -63,6 +63,32 @@ def test_prequant_every_bf16_pattern(dext):
     _check(dext, alone, "alone")
 
 
+def test_quantize_rows_every_f16_pattern(dext):
+    """Every finite fp16 value through mxfp4_quantize_rows (fp16 input), grouped
+    32 per block in a shuffled order and alone in its block: the quantizer's
+    hardware E2M1 conversion on values with 11 significant bits."""
+    lib = _lib.load()
+    v = np.arange(1 << 16, dtype=np.uint16).view(np.float16)
+    v = v[np.isfinite(v)].astype(np.float32)
+    rng = np.random.default_rng(12)
+    pad = (-v.size) % 32
+    grouped = np.concatenate([rng.permutation(v), np.zeros(pad, np.float32)]).reshape(-1, 32)
+    alone = np.zeros((v.size, 32), np.float32)
+    alone[:, 9] = v
+    for what, x in (("grouped", grouped), ("alone", alone)):
+        xt = torch.from_numpy(x).to(DEV).half()
+        M, K = xt.shape
+        xq = torch.empty((M, K // 2), dtype=torch.uint8, device=DEV)
+        xs = torch.empty((M, K // 32), dtype=torch.uint8, device=DEV)
+        rc = lib.mxfp4_quantize_rows(xt.data_ptr(), 1, 0, K, M, K, K, xq.data_ptr(), xs.data_ptr(),
+                                     torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        q, s = fmt.quantize_rows(np_(xt.float()))
+        log(f"  quantize_rows every fp16 {what} {tuple(x.shape)}")
+        assert np.array_equal(np_(xs), s), what
+        assert np.array_equal(np_(xq), q), what
+
+
 def test_prequant_edge_blocks(dext):
     rows = []
     r = np.zeros(96, np.float32)
