@@ -168,6 +168,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     // logits routing: lane r < E of every wave holds rank r (id, weight)
     int rid = 0;
     float rw = 0.0f;
+    // gate/up workgroups: x is loaded before the routing, so its latency
+    // overlaps the top-k (the weight loads need the routing, x does not)
+    const int k0 = threadIdx.x * 8;
+    uint4 xq = make_uint4(0, 0, 0, 0);
+    if (bid < nA && k0 < a.H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
     if constexpr (ROUTE == ROUTE_LOGITS) {
         mx::wave_topk<kRouteNpl>(a.logits, a.n_experts, a.E, a.norm, rid, rw);
         if (bid == 0 && wave == 0 && lane < a.E && a.ids_out) {
@@ -186,10 +191,6 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int bpw = hb >> 2;                // blocks per wave (16)
         const int sa = bpw >> 2;                // K-steps per wave (H/512, <= 4)
 
-        // x first: its value is needed before the MFMAs, the weights only by them
-        const int k0 = threadIdx.x * 8;
-        uint4 xq = make_uint4(0, 0, 0, 0);
-        if (k0 < H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
         int* memo = reinterpret_cast<int*>(a.ws + kMemoAOff) + s * 32 + jb;
         const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
         const int launch = *memo;
