@@ -251,6 +251,31 @@ int mxfp4_moe_decode_layer_routed(const void* x, const float* logits, int norm, 
                                   float* out, void* resid_out, void* workspace, size_t workspace_bytes,
                                   void* stream);
 
+/* As mxfp4_moe_decode_layer_routed with the step's post-attention residual,
+ * RMSNorm and router projection in the same launch: the reference's
+ *   x = x + o.bfloat16(); h2 = rms_norm(x) * w; logits = router(h2)
+ *   (runtime/model_runner_v2.py:185-189, RMSNorm runtime/model_runner.py:20-25,
+ *   the router through prequant + lin_pq on the MXFP4 rows of h2)
+ * followed by the MoE of h2.  n_experts / 16 router workgroups compute the
+ * logits and hand them to the launch's other workgroups (bounded wait, as
+ * for h); the MoE runs on the un-quantized h2, as mxfp4_moe_decode_layer.
+ * It has no single counterpart in the reference, whose step runs these as
+ * separate launches (rmsnorm_lin_pq's pair of ops and the MoE); it saves a
+ * launch per layer.  x bf16 (H), resid fp32 (H), norm_w bf16 (H); H = 2048;
+ * router_wp / router_ws the MXFP4 router (n_experts, H/2) + (n_experts,
+ * H/32), n_experts a multiple of 16 up to 256; optional outputs x_out (bf16
+ * x + bf16(resid), the residual stream), y_out (bf16 h2), logits_out (fp32
+ * logits), ids_out / w_out (both or neither).  Same workspace as
+ * mxfp4_moe_decode_layer (launches of all three entry points may share one).
+ */
+int mxfp4_moe_decode_layer_fused_router(const void* x, const float* resid, const void* norm_w, float eps,
+                                        const uint8_t* router_wp, const uint8_t* router_ws, int norm,
+                                        void* x_out, void* y_out, float* logits_out, int32_t* ids_out,
+                                        float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                        const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                        const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                        float* out, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * A run of consecutive decode MoE layers in one launch (batch 1).  No single
  * reference entry point: it replaces the per-layer loop of

@@ -76,7 +76,10 @@ constexpr int kCfgOff = 0;            // int32 config word written by reset
 constexpr int kErrOff = 256;          // int32 error flag
 constexpr int kMemoAOff = 1024;       // int32 launch count of gate/up workgroup (s, jb): [8][32]
 constexpr int kMemoBOff = 2048;       // int32 launch count of down workgroup cb: [128]
-constexpr int kHOff = 4096;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart
+constexpr int kMemoROff = 2560;       // int32 launch count of router workgroup r (fused router): [16]
+constexpr int kLogOff = 4096;         // fused router: (logit, tag) 64-bit words, n_experts <= 256
+constexpr int kHOff = 8192;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart
+constexpr int kMaxRouterWg = 16;      // fused router: 16 logits per workgroup
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -93,6 +96,18 @@ struct LayerArgs {
     int32_t ids[kMaxE];       // by-value ids when ids_dev is null
     float w[kMaxE];           // by-value weights when w_dev is null
     const float* logits;      // (n_experts) fp32 router logits: routing computed in-kernel
+    // fused router (ROUTE_FUSED): the post-attention residual, RMSNorm and the
+    // router projection run inside the launch
+    const uint16_t* xres;     // (H) bf16 residual stream
+    const float* oproj;       // (H) fp32 added to it as bf16
+    const uint16_t* nw;       // (H) bf16 norm weight
+    float eps;
+    const uint8_t* rwp;       // (n_experts, H/2) + (n_experts, H/32) MXFP4 router weight
+    const uint8_t* rws;
+    uint16_t* x_out;          // optional (H) bf16(xres + bf16(oproj))
+    uint16_t* y_out;          // optional (H) the normed row (the MoE input)
+    float* logits_out;        // optional (n_experts) the router logits
+    int nr;                   // router workgroups (n_experts / 16)
     int n_experts;            // experts per layer (logits routing)
     int norm;                 // renormalise the top-E weights (logits routing)
     int32_t* ids_out;         // optional (E) ids / weights written by workgroup 0 (logits routing)
@@ -144,12 +159,156 @@ union Smem {
         float red[4][16];
         int abort;
     } b;
+    struct {                                       // router workgroups (fused router)
+        uint4 zero[2];
+        uint8_t xq[1024];                          // the normed row's MXFP4 (H <= 2048)
+        uint8_t xs[64];
+        float red[4][16];
+    } r;
 };
+
+// The post-attention residual and RMSNorm of one row for the fused router,
+// thread t holding elements 8t .. 8t+7 (H = 2048, 256 threads): v = bf16(x +
+// bf16(o)), y = bf16(bf16(v * rstd) * w) -- the arithmetic of
+// mxfp4_rmsnorm_quant / mxfp4_rmsnorm_lin_pq (runtime/model_runner.py:20-25),
+// including its order of the sum of squares, so y equals theirs bit for bit.
+// Every thread of the workgroup must call it (one barrier).
+__device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, float (&v)[8], float (&y)[8]) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int k0 = 8 * tid;
+    const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
+    const float4 o0 = *reinterpret_cast<const float4*>(a.oproj + k0);
+    const float4 o1 = *reinterpret_cast<const float4*>(a.oproj + k0 + 4);
+    const uint4 wq4 = *reinterpret_cast<const uint4*>(a.nw + k0);
+    const uint32_t xw[4] = {q.x, q.y, q.z, q.w};
+    const float of[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float xi = mx::bf16_to_f32((uint16_t)(xw[i / 2] >> (16 * (i & 1))));
+        v[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(xi + mx::bf16_to_f32(mx::f32_to_bf16_rne(of[i]))));
+        ss = fmaf(v[i], v[i], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) nred[wave] = ss;
+    __syncthreads();
+    const float var = ((nred[0] + nred[1]) + (nred[2] + nred[3])) / (float)2048;
+    const float rr = 1.0f / sqrtf(var + a.eps);
+    const uint32_t ww[4] = {wq4.x, wq4.y, wq4.z, wq4.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float wi = mx::bf16_to_f32((uint16_t)(ww[i / 2] >> (16 * (i & 1))));
+        const float t = mx::bf16_to_f32(mx::f32_to_bf16_rne(v[i] * rr));
+        y[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(t * wi));
+    }
+}
+
+// The router logits of this launch from the workspace: element i*64 + lane
+// into lv[i], waiting (bounded) until every word carries this launch's tag.
+template <int NPL>
+__device__ __forceinline__ bool poll_logits(const LayerArgs& a, uint32_t tag, float (&lv)[NPL]) {
+    const uint64_t* words = reinterpret_cast<const uint64_t*>(a.ws + kLogOff);
+    const int lane = threadIdx.x & 63;
+    int spins = 0;
+    while (true) {
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < NPL; ++i) {
+            const int idx = i * 64 + lane;
+            lv[i] = 0.0f;
+            if (idx < a.n_experts) {
+                const uint64_t w = __hip_atomic_load(words + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                lv[i] = __uint_as_float((uint32_t)w);
+                pending |= (uint32_t)(w >> 32) != tag;
+            }
+        }
+        if (__builtin_amdgcn_ballot_w64(pending) == 0) return true;
+        if (++spins >= kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");
+    }
+}
+
+// Router workgroup r (fused router): logits [16r, 16r + 16) of the normed
+// row -- its MXFP4 (the reference quantizes the bf16 row, prequant) times
+// the router's MXFP4 rows on v_mfma_scale_f32_16x16x128_f8f6f4 (row 0 of A is
+// the row, rows 1..15 zero), K split over the four waves, partial sums
+// added in wave order -- published as (value, tag) words for every other
+// workgroup of the launch.  Workgroup 0 also writes x_out / y_out.
+__device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* nred, int ri) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoROff) + ri;
+    const int launch = *memo;
+    const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+    // weights first: row 16ri + r, blocks 16*wave + 4g .. +3 (64 contiguous bytes) and their scales
+    const int blk0 = 16 * wave + 4 * g;
+    const int row = min(16 * ri + r, a.n_experts - 1);
+    const uint8_t* wr = a.rwp + (int64_t)row * 1024 + blk0 * 16;
+    uint4 wq[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) wq[i] = *reinterpret_cast<const uint4*>(wr + 16 * i);
+    const uint32_t wsc = *reinterpret_cast<const uint32_t*>(a.rws + (int64_t)row * 64 + blk0);
+    float v[8], y[8];
+    fused_norm_row(a, nred, v, y);
+    // MXFP4 of y (bf16-exact values): block tid / 4, the block's four threads
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(y[i]));
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor1>(am));
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor2>(am));
+    const uint32_t code = mx::e8m0_code(am);
+    *reinterpret_cast<uint32_t*>(sm.r.xq + 4 * tid) = mx::e2m1_pack8_short(y, mx::e8m0_inv_scale(code));
+    if ((tid & 3) == 0) sm.r.xs[tid >> 2] = (uint8_t)code;
+    if (tid < 2) sm.r.zero[tid] = make_uint4(0, 0, 0, 0);
+    if (ri == 0) {
+        const int k0 = 8 * tid;
+        uint32_t xo[4], yo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xo[i] = (uint32_t)mx::f32_to_bf16_rne(v[2 * i]) | ((uint32_t)mx::f32_to_bf16_rne(v[2 * i + 1]) << 16);
+            yo[i] = (uint32_t)mx::f32_to_bf16_rne(y[2 * i]) | ((uint32_t)mx::f32_to_bf16_rne(y[2 * i + 1]) << 16);
+        }
+        if (a.x_out) *reinterpret_cast<uint4*>(a.x_out + k0) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
+        if (a.y_out) *reinterpret_cast<uint4*>(a.y_out + k0) = make_uint4(yo[0], yo[1], yo[2], yo[3]);
+    }
+    __syncthreads();
+    mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint4* pa = r == 0 ? reinterpret_cast<const uint4*>(sm.r.xq + (blk0 + i) * 16) : &sm.r.zero[0];
+        const uint32_t asc = r == 0 ? (uint32_t)sm.r.xs[blk0 + i] : 127u;
+        acc = mx::mfma16_fp4(*pa, wq[i], acc, asc, (wsc >> (8 * i)) & 0xFFu);
+    }
+    mx::pin(acc);
+    // D[0][lane] (lane < 16): the wave's K quarter of logit 16ri + lane
+    if (lane < 16) sm.r.red[wave][lane] = acc[0];
+    __syncthreads();
+    if (tid < 16) {
+        const float lg = (sm.r.red[0][tid] + sm.r.red[1][tid]) + (sm.r.red[2][tid] + sm.r.red[3][tid]);
+        const int idx = 16 * ri + tid;
+        if (idx < a.n_experts) {
+            uint64_t* words = reinterpret_cast<uint64_t*>(a.ws + kLogOff);
+            __hip_atomic_store(words + idx, (uint64_t)__float_as_uint(lg) | ((uint64_t)(uint32_t)(launch + 1) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (a.logits_out) a.logits_out[idx] = lg;
+        }
+    }
+    if (tid == 0) {
+        // launch counts of the router slots this launch has no workgroup for
+        // move on with it (workgroup 0), so every count stays in step
+        if (ri == 0)
+            for (int k = a.nr; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
+        *memo = launch + 1;
+        if (cfg != a.cfg) set_error(a);
+    }
+}
 
 // Where the routing comes from: kernel arguments, device arrays, or router
 // logits in device memory (softmax / top-E / renormalise computed by every
 // wave at entry, mx::wave_topk).
-enum { ROUTE_HOST = 0, ROUTE_DEV_IDS = 1, ROUTE_LOGITS = 2 };
+enum { ROUTE_HOST = 0, ROUTE_DEV_IDS = 1, ROUTE_LOGITS = 2, ROUTE_FUSED = 3 };
 constexpr int kRouteNpl = 4;          // logits routing: up to 256 experts
 
 template <int ROUTE, int MS>
@@ -163,18 +322,48 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int rr = r < kTerms ? r : 0;     // A-operand term row read by this lane (rows >= 3 are zero)
     const int nblk_mi = a.Mi >> 5;
     const int nA = a.E * nblk_mi;
-    const int bid = blockIdx.x;
+    constexpr bool kLogitRoute = ROUTE == ROUTE_LOGITS || ROUTE == ROUTE_FUSED;
+    // fused router: workgroups [0, nr) compute the logits; the gate/up and
+    // down workgroups follow them
+    const int bid = (int)blockIdx.x - (ROUTE == ROUTE_FUSED ? a.nr : 0);
+    __shared__ float nred[4];
+    if constexpr (ROUTE == ROUTE_FUSED) {
+        if (bid < 0) {
+            router_wg(a, sm, nred, (int)blockIdx.x);
+            return;
+        }
+    }
     uint32_t* hbuf = reinterpret_cast<uint32_t*>(a.ws + kHOff);
     // logits routing: lane r < E of every wave holds rank r (id, weight)
     int rid = 0;
     float rw = 0.0f;
     // gate/up workgroups: x is loaded before the routing, so its latency
-    // overlaps the top-k (the weight loads need the routing, x does not)
+    // overlaps the top-k (the weight loads need the routing, x does not);
+    // with the fused router, x is the normed row, computed here from the
+    // residual inputs while the router workgroups run
     const int k0 = threadIdx.x * 8;
     uint4 xq = make_uint4(0, 0, 0, 0);
-    if (bid < nA && k0 < a.H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
+    float yf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (ROUTE == ROUTE_FUSED) {
+        if (bid < nA) {
+            float vf[8];
+            fused_norm_row(a, nred, vf, yf);
+        }
+    } else {
+        if (bid < nA && k0 < a.H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
+    }
     if constexpr (ROUTE == ROUTE_LOGITS) {
         mx::wave_topk<kRouteNpl>(a.logits, a.n_experts, a.E, a.norm, rid, rw);
+    }
+    if constexpr (ROUTE == ROUTE_FUSED) {
+        // this launch's tag: the workgroup's own launch count + 1
+        const int* memo0 = reinterpret_cast<const int*>(a.ws) +
+                           (bid < nA ? kMemoAOff / 4 + (bid % a.E) * 32 + bid / a.E : kMemoBOff / 4 + (bid - nA));
+        float lv[kRouteNpl];
+        if (!poll_logits<kRouteNpl>(a, (uint32_t)(*memo0 + 1), lv)) set_error(a);
+        mx::wave_topk_regs<kRouteNpl>(lv, a.n_experts, a.E, a.norm, rid, rw);
+    }
+    if constexpr (kLogitRoute) {
         if (bid == 0 && wave == 0 && lane < a.E && a.ids_out) {
             a.ids_out[lane] = rid;
             a.w_out[lane] = rw;
@@ -195,7 +384,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
         const int launch = *memo;
 
-        const int e = ROUTE == ROUTE_LOGITS ? __builtin_amdgcn_readfirstlane(__shfl(rid, s))
+        const int e = kLogitRoute ? __builtin_amdgcn_readfirstlane(__shfl(rid, s))
                       : ROUTE == ROUTE_DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[s]) : pick_id(a, s);
         const uint8_t* gw = a.gate_wp + (int64_t)e * a.wp_stride_gu;
         const uint8_t* gs = a.gate_ws + (int64_t)e * a.ws_stride_gu;
@@ -231,8 +420,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             const uint32_t w4[4] = {xq.x, xq.y, xq.z, xq.w};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                v[2 * i] = mx::bf16_to_f32((uint16_t)(w4[i] & 0xFFFFu));
-                v[2 * i + 1] = mx::bf16_to_f32((uint16_t)(w4[i] >> 16));
+                v[2 * i] = ROUTE == ROUTE_FUSED ? yf[2 * i] : mx::bf16_to_f32((uint16_t)(w4[i] & 0xFFFFu));
+                v[2 * i + 1] = ROUTE == ROUTE_FUSED ? yf[2 * i + 1] : mx::bf16_to_f32((uint16_t)(w4[i] >> 16));
             }
             uint64_t w8[kTerms];
             uint32_t codes;
@@ -304,6 +493,10 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             if (lane == 0) {
                 *memo = launch + 1;
                 if (!cfg_ok) set_error(a);
+                // launches without router workgroups move the router launch
+                // counts on (workgroup 0), so a later fused launch agrees
+                if (ROUTE != ROUTE_FUSED && bid == 0)
+                    for (int k = 0; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
             }
         }
         return;
@@ -326,9 +519,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     for (int q = 0; q < 2; ++q) {
         slot[q] = 2 * wave + q;
         const int sl = slot[q] < a.E ? slot[q] : 0;
-        eid[q] = ROUTE == ROUTE_LOGITS ? __builtin_amdgcn_readfirstlane(__shfl(rid, sl))
+        eid[q] = kLogitRoute ? __builtin_amdgcn_readfirstlane(__shfl(rid, sl))
                  : ROUTE == ROUTE_DEV_IDS ? __builtin_amdgcn_readfirstlane(a.ids_dev[sl]) : pick_id(a, sl);
-        wgt[q] = ROUTE == ROUTE_LOGITS ? __shfl(rw, sl) : ROUTE == ROUTE_DEV_IDS ? a.w_dev[sl] : pick_w(a, sl);
+        wgt[q] = kLogitRoute ? __shfl(rw, sl) : ROUTE == ROUTE_DEV_IDS ? a.w_dev[sl] : pick_w(a, sl);
     }
     uint4 bq[2][MS];
     uint32_t bsw[2][3];   // dwords holding the scale bytes of blocks g*steps..
@@ -595,9 +788,10 @@ template <int ROUTE>
 int launch_layer(const LayerArgs& a, hipStream_t st) {
     const int nA = a.E * (a.Mi / 32);
     const int nB = a.H / 16;
+    const int nR = ROUTE == ROUTE_FUSED ? a.nr : 0;
     const int steps = (a.Mi / 32 + 3) / 4;
-    if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), dim3(nA + nB), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), dim3(nA + nB), dim3(256), 0, st, a);
+    if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), dim3(nR + nA + nB), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), dim3(nR + nA + nB), dim3(256), 0, st, a);
     return mxh::launch_status("moe_decode_layer");
 }
 }  // namespace
@@ -645,4 +839,42 @@ extern "C" int mxfp4_moe_decode_layer_routed(const void* x, const float* logits,
     a.ids_out = ids_out;
     a.w_out = w_out;
     return launch_layer<ROUTE_LOGITS>(a, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_decode_layer_fused_router(const void* x, const float* resid, const void* norm_w, float eps,
+                                                   const uint8_t* router_wp, const uint8_t* router_ws, int norm,
+                                                   void* x_out, void* y_out, float* logits_out, int32_t* ids_out,
+                                                   float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                                   const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                                   const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                                   float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    LayerArgs a;
+    const int rc = layer_args(a, x, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E, H, Mi, out,
+                              nullptr, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE(resid && norm_w && router_wp && router_ws, "moe_decode_layer_fused_router: null pointer");
+    MXH_REQUIRE(H == 2048, "moe_decode_layer_fused_router: H=%d (the fused norm is built for 2048)", H);
+    MXH_REQUIRE(n_experts % 16 == 0 && n_experts <= 16 * kMaxRouterWg,
+                "moe_decode_layer_fused_router: n_experts=%d must be a multiple of 16 up to %d", n_experts,
+                16 * kMaxRouterWg);
+    MXH_REQUIRE((ids_out != nullptr) == (w_out != nullptr),
+                "moe_decode_layer_fused_router: give ids_out and w_out both or neither");
+    MXH_REQUIRE(((uintptr_t)resid & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)router_wp & 15) == 0 &&
+                    ((uintptr_t)router_ws & 3) == 0 && ((uintptr_t)x_out & 15) == 0 && ((uintptr_t)y_out & 15) == 0,
+                "moe_decode_layer_fused_router: resid, norm_w, router_wp, x_out, y_out must be 16-byte aligned, "
+                "router_ws 4-byte");
+    a.xres = static_cast<const uint16_t*>(x);
+    a.oproj = resid;
+    a.nw = static_cast<const uint16_t*>(norm_w);
+    a.eps = eps;
+    a.rwp = router_wp;
+    a.rws = router_ws;
+    a.norm = norm ? 1 : 0;
+    a.x_out = static_cast<uint16_t*>(x_out);
+    a.y_out = static_cast<uint16_t*>(y_out);
+    a.logits_out = logits_out;
+    a.ids_out = ids_out;
+    a.w_out = w_out;
+    a.nr = n_experts / 16;
+    return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
 }

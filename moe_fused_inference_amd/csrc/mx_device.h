@@ -299,16 +299,15 @@ __device__ __forceinline__ float wave_reduce_dpp(float v) {
 // the row.  Lane r < k receives rank r.  The row has n <= 64*NPL entries,
 // element i*64 + lane held by the lane; k <= 64.  NaN logits are never
 // chosen.
+// wave_topk_regs takes the row from registers: lv[i] = element i*64 + lane
+// (any value for i*64 + lane >= n).
 template <int NPL>
-__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int n, int k, int norm, int& id, float& w) {
+__device__ __forceinline__ void wave_topk_regs(const float (&lv)[NPL], int n, int k, int norm, int& id, float& w) {
     const int lane = threadIdx.x & 63;
     const float kNone = __builtin_nanf("");
     float v[NPL];
 #pragma unroll
-    for (int i = 0; i < NPL; ++i) {
-        const int idx = i * 64 + lane;
-        v[i] = idx < n ? lg[idx] : kNone;
-    }
+    for (int i = 0; i < NPL; ++i) v[i] = i * 64 + lane < n ? lv[i] : kNone;
     float my_l = 0.0f;
     int my_i = 0;
     for (int r = 0; r < k; ++r) {
@@ -341,11 +340,23 @@ __device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int n, i
         float s = 0.0f;
 #pragma unroll
         for (int i = 0; i < NPL; ++i)
-            if (i * 64 + lane < n) s += expf(lg[i * 64 + lane] - lmax);
+            if (i * 64 + lane < n) s += expf(lv[i] - lmax);
         den = wave_reduce_dpp<false>(s);
     }
     id = my_i;
     w = e / den;
+}
+
+template <int NPL>
+__device__ __forceinline__ void wave_topk(const float* __restrict__ lg, int n, int k, int norm, int& id, float& w) {
+    const int lane = threadIdx.x & 63;
+    float lv[NPL];
+#pragma unroll
+    for (int i = 0; i < NPL; ++i) {
+        const int idx = i * 64 + lane;
+        lv[i] = idx < n ? lg[idx] : 0.0f;
+    }
+    wave_topk_regs<NPL>(lv, n, k, norm, id, w);
 }
 
 }  // namespace mx

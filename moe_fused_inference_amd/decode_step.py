@@ -32,7 +32,8 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
-from .moe_layer import RoutedLayerCall, StackedExperts, layer_status, workspace as layer_workspace
+from .moe_layer import (FusedRouterLayerCall, RoutedLayerCall, StackedExperts, layer_status,
+                        workspace as layer_workspace)
 
 
 @dataclass
@@ -157,11 +158,16 @@ class DecodeStep:
     stay on the device: each step reads them and leaves the greedy next
     tokens and dpos + M for the next step."""
 
-    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda"):
+    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True):
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
         self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
         self.fused_norm = cfg.hidden == 2048 and self.M == 1   # at M > 1 the per-workgroup norm costs more than the launch it saves
+        # M = 1: post-attention residual + RMSNorm + router inside the MoE launch
+        # (mxfp4_moe_decode_layer_fused_router), one launch per layer fewer
+        self.fused_router = (bool(fused_router) and self.M == 1 and cfg.hidden == 2048 and cfg.n_experts % 16 == 0
+                             and cfg.n_experts <= 256)
+        self._fr_calls = {}
         c = cfg
         if c.head_dim != 128:
             raise RuntimeError("head_dim must be 128 (attention kernels)")
@@ -274,14 +280,26 @@ class DecodeStep:
                                                  b.as_.data_ptr(), M, Hq, Hkv, D, self.max_pos, self.kv_codec,
                                                  b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode_fused")
             self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
-            # x = x + bf16(o); post-attention norm (y, MXFP4 rows for the MoE); router logits
-            self._norm_lin(xa, b.oproj, lw.post_norm, xb, True, lw.gate, b.glog, s)
-            xa, xb = xb, xa
-            # MoE
-            if M == 1:
-                self.moe_calls[l](s)
+            if self.fused_router:
+                # x = x + bf16(o), its RMSNorm (y), the router logits and the MoE in one launch
+                key = (l, xa.data_ptr())
+                call = self._fr_calls.get(key)
+                if call is None:
+                    call = FusedRouterLayerCall(xa[0], b.oproj[0], lw.post_norm, c.rms_eps, lw.gate.wp, lw.gate.ws,
+                                                c.top_k, lw.experts, b.moe[0], self.layer_ws, x_out=xb[0],
+                                                y_out=b.y[0], logits_out=b.glog[0])
+                    self._fr_calls[key] = call
+                call(s)
+                xa, xb = xb, xa
             else:
-                self._moe_batch(lw.experts, s)
+                # x = x + bf16(o); post-attention norm (y, MXFP4 rows for the MoE); router logits
+                self._norm_lin(xa, b.oproj, lw.post_norm, xb, True, lw.gate, b.glog, s)
+                xa, xb = xb, xa
+                # MoE
+                if M == 1:
+                    self.moe_calls[l](s)
+                else:
+                    self._moe_batch(lw.experts, s)
             if on_layer is not None:
                 on_layer(l, xa, b.moe)
         # final norm (+ the last MoE residual), lm_head, greedy next tokens

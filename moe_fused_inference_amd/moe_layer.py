@@ -124,6 +124,38 @@ class RoutedLayerCall:
         _lib.check(self.lib.mxfp4_moe_decode_layer_routed(*self.args, s), "moe_decode_layer_routed")
 
 
+class FusedRouterLayerCall:
+    """Pre-bound arguments of one fused-layer launch that also runs the
+    post-attention residual add, RMSNorm and router projection
+    (mxfp4_moe_decode_layer_fused_router): x bf16 (H,) and resid fp32 (H,)
+    in, x_out = bf16(x + bf16(resid)), the MoE of h2 = rms_norm(x_out) * norm_w
+    in `out` (fp32 (H,)), routed on the logits of the MXFP4 router
+    (router_wp, router_ws) computed in the same launch."""
+
+    def __init__(self, x, resid, norm_w, eps, router_wp, router_ws, E, experts, out, ws, norm=True, x_out=None,
+                 y_out=None, logits_out=None, ids_out=None, w_out=None):
+        self.lib = _lib.load()
+        if (ids_out is None) != (w_out is None):
+            raise RuntimeError("give ids_out and w_out both or neither")
+        n = experts.n_experts
+        if tuple(router_wp.shape) != (n, experts.hidden // 2) or tuple(router_ws.shape) != (n, experts.hidden // 32):
+            raise RuntimeError(f"router weights must be ({n}, {experts.hidden // 2}) + ({n}, {experts.hidden // 32})")
+        if resid.dtype != torch.float32 or x.dtype != torch.bfloat16 or norm_w.dtype != torch.bfloat16:
+            raise RuntimeError("x and norm_w must be bfloat16, resid float32")
+        ptr = (lambda t: t.data_ptr() if t is not None else None)
+        self.keep = (x, resid, norm_w, router_wp, router_ws, experts, out, ws, x_out, y_out, logits_out, ids_out, w_out)
+        self.args = (x.data_ptr(), resid.data_ptr(), norm_w.data_ptr(), float(eps), router_wp.data_ptr(),
+                     router_ws.data_ptr(), int(bool(norm)), ptr(x_out), ptr(y_out), ptr(logits_out), ptr(ids_out),
+                     ptr(w_out), experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
+                     experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
+                     experts.down_wp.data_ptr(), experts.down_ws.data_ptr(),
+                     n, int(E), experts.hidden, experts.inter, out.data_ptr(), ws.data_ptr(), ws.numel())
+
+    def __call__(self, stream=None):
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        _lib.check(self.lib.mxfp4_moe_decode_layer_fused_router(*self.args, s), "moe_decode_layer_fused_router")
+
+
 def decode_layer_routed(x, logits, E, experts, norm=True, out=None, resid=None, ws=None, want_routing=False):
     """One token through the layer, routing included: softmax / top-E /
     renormalise of the fp32 router logits (n_experts,) computed in the same

@@ -1,0 +1,142 @@
+"""GPU parity of mxfp4_moe_decode_layer_fused_router: the post-attention
+residual, RMSNorm and router projection inside the MoE launch.
+
+Checked against the same step run as separate calls of this library:
+  * x_out and y_out bit for bit against mxfp4_rmsnorm_lin_pq's residual and
+    normed row (the same arithmetic, runtime/model_runner.py:20-25);
+  * the logits against rmsnorm_lin_pq's router projection (the same MXFP4
+    operands, another split of K over the waves: fp32 rounding only) and
+    against the float64 oracle of the MXFP4 product;
+  * ids / weights against mxfp4_route_topk on the launch's own logits, exact;
+  * the MoE output bit for bit against mxfp4_moe_decode_layer on y_out with
+    those ids and weights.
+Several launches share one workspace, interleaved with plain fused-layer
+launches, and a captured graph replays them."""
+import numpy as np
+import pytest
+import torch
+
+from moe_fused_inference_amd import _lib, moe_layer
+from oracle import mxfp4 as fmt
+from tests.gpu_helpers import DEV, log, np_, rand_weight
+from tests.test_gpu_decode_layer import make_stack
+
+pytestmark = pytest.mark.gpu
+H, MI, E = 2048, 768, 8
+EPS = 1e-6
+
+
+def _inputs(g, scale_o=1.0):
+    xa = torch.randn(H, generator=g, device=DEV).bfloat16()
+    o = torch.randn(H, generator=g, device=DEV) * scale_o
+    nw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+    return xa, o.contiguous(), nw
+
+
+def _reference(lib, xa, o, nw, rwp, rws, n_exp, experts):
+    """The separate calls: rmsnorm_lin_pq (residual, norm, router), then the
+    fused layer on the normed row with the given routing."""
+    xr = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    yr = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    yq = torch.empty(H // 2, dtype=torch.uint8, device=DEV)
+    ys = torch.empty(H // 32, dtype=torch.uint8, device=DEV)
+    lr = torch.empty(n_exp, dtype=torch.float32, device=DEV)
+    _lib.check(lib.mxfp4_rmsnorm_lin_pq(xa.data_ptr(), o.data_ptr(), nw.data_ptr(), EPS, 1, H, xr.data_ptr(),
+                                        yr.data_ptr(), yq.data_ptr(), ys.data_ptr(), rwp.data_ptr(), rws.data_ptr(),
+                                        n_exp, lr.data_ptr(), None), "rmsnorm_lin_pq")
+    return xr, yr, yq, ys, lr
+
+
+@pytest.mark.parametrize("n_exp", [32, 128])
+def test_fused_router_matches_separate_calls(dext, n_exp):
+    lib = _lib.load()
+    experts = make_stack(dext, n_exp, H, MI, seed=12000 + n_exp)
+    rwp, rws = rand_weight(dext, n_exp, H, seed=12500 + n_exp, std=0.05)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(n_exp)
+    ws = moe_layer.workspace(E, MI, H)
+    plain_out = torch.empty(H, dtype=torch.float32, device=DEV)
+    for it in range(4):
+        xa, o, nw = _inputs(g)
+        outs = dict(out=torch.empty(H, dtype=torch.float32, device=DEV),
+                    x_out=torch.empty(H, dtype=torch.bfloat16, device=DEV),
+                    y_out=torch.empty(H, dtype=torch.bfloat16, device=DEV),
+                    logits_out=torch.empty(n_exp, dtype=torch.float32, device=DEV),
+                    ids_out=torch.empty(E, dtype=torch.int32, device=DEV),
+                    w_out=torch.empty(E, dtype=torch.float32, device=DEV))
+        call = moe_layer.FusedRouterLayerCall(xa, o, nw, EPS, rwp, rws, E, experts, outs["out"], ws,
+                                              x_out=outs["x_out"], y_out=outs["y_out"],
+                                              logits_out=outs["logits_out"], ids_out=outs["ids_out"],
+                                              w_out=outs["w_out"])
+        call()
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(ws) == 0
+        xr, yr, yq, ys, lr = _reference(lib, xa, o, nw, rwp, rws, n_exp, experts)
+        torch.cuda.synchronize()
+        assert torch.equal(outs["x_out"], xr), "residual differs from rmsnorm_lin_pq"
+        assert torch.equal(outs["y_out"], yr), "normed row differs from rmsnorm_lin_pq"
+        lg, lref = np_(outs["logits_out"]).astype(np.float64), np_(lr).astype(np.float64)
+        # float64 oracle of the MXFP4 product
+        a = fmt.dequant_rows(np_(yq)[None], np_(ys)[None], H).astype(np.float64)
+        wd = fmt.dequant_rows(np_(rwp), np_(rws), H).astype(np.float64)
+        lor = (a @ wd.T)[0]
+        span = np.abs(lor).max()
+        d1, d2 = np.abs(lg - lref).max() / span, np.abs(lg - lor).max() / span
+        log(f"  n_exp={n_exp} launch {it}: logits vs rmsnorm_lin_pq {d1:.2e}, vs oracle {d2:.2e}")
+        assert d1 <= 1e-5 and d2 <= 1e-5
+        ids, w = moe_layer.route_topk(outs["logits_out"][None], E)
+        assert torch.equal(outs["ids_out"], ids[0]), "ids differ from route_topk on the launch's logits"
+        assert torch.equal(outs["w_out"], w[0])
+        ref = torch.empty(H, dtype=torch.float32, device=DEV)
+        moe_layer.decode_layer(outs["y_out"], outs["ids_out"], outs["w_out"], experts, out=ref, ws=ws)
+        torch.cuda.synchronize()
+        assert torch.equal(outs["out"], ref), "MoE output differs from the fused layer on y_out"
+        # a plain launch on the same workspace between fused ones keeps the launch counts in step
+        moe_layer.decode_layer(outs["y_out"], [int(i) for i in ids[0].tolist()], [float(v) for v in w[0].tolist()],
+                               experts, out=plain_out, ws=ws)
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(ws) == 0
+
+
+def test_fused_router_graph_replays(dext):
+    n_exp = 32
+    experts = make_stack(dext, n_exp, H, MI, seed=13000)
+    rwp, rws = rand_weight(dext, n_exp, H, seed=13100, std=0.05)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(5)
+    xa, o, nw = _inputs(g)
+    ws = moe_layer.workspace(E, MI, H)
+    out = torch.empty(H, dtype=torch.float32, device=DEV)
+    x_out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    call = moe_layer.FusedRouterLayerCall(xa, o, nw, EPS, rwp, rws, E, experts, out, ws, x_out=x_out)
+    call()
+    torch.cuda.synchronize()
+    eager = (out.clone(), x_out.clone())
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            call()
+            call()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        out.zero_()
+        x_out.zero_()
+        _ = torch.randn(1024, device=DEV).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager[0]) and torch.equal(x_out, eager[1]), f"replay {rep}"
+    assert moe_layer.layer_status(ws) == 0
+
+
+def test_fused_router_argument_checks(dext):
+    lib = _lib.load()
+    p = 256
+    args = [p, p, p, 1e-6, p, p, 1, None, None, None, None, None, p, p, p, p, p, p]
+    ws = moe_layer.workspace(E, MI, H)
+    tail = [ws.data_ptr(), ws.numel(), None]
+    assert lib.mxfp4_moe_decode_layer_fused_router(*args, 40, E, H, MI, p, *tail) == -1
+    assert "multiple of 16" in lib.mxfp4_last_error().decode()
+    assert lib.mxfp4_moe_decode_layer_fused_router(*args, 32, E, 1024, MI, p, *tail) == -1
+    assert "2048" in lib.mxfp4_last_error().decode()
