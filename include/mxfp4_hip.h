@@ -276,6 +276,30 @@ int mxfp4_moe_decode_layer_fused_router(const void* x, const float* resid, const
                                         const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
                                         float* out, void* workspace, size_t workspace_bytes, void* stream);
 
+/* As mxfp4_moe_decode_layer_fused_router with the NEXT layer's input
+ * residual, RMSNorm and q|k|v projection in the same launch, after the MoE:
+ *   x_next = x_out + out.bfloat16(); qkv = lin_pq(MXFP4(rms_norm(x_next) * w))
+ *   (runtime/model_runner_v2.py:208 then :147-152 of the next layer; the
+ *   arithmetic of mxfp4_rmsnorm_lin_pq, whose outputs these equal bit for bit
+ *   for Nq from 4081 to 8192, where that call also splits K in four)
+ * ceil(Nq / 64) workgroups load the q|k|v rows while the MoE runs and wait
+ * (bounded) for its output columns.  No single counterpart in the reference
+ * (separate launches there); it saves the step another launch per layer.
+ * qkv_norm_w bf16 (H); qkv_wp / qkv_ws the MXFP4 (Nq, H/2) + (Nq, H/32)
+ * projection, Nq <= 8192; qkv_out fp32 (Nq); x_next_out optional bf16 (H),
+ * which must not alias x or x_out.  16-byte aligned.  Same workspace as
+ * mxfp4_moe_decode_layer.
+ */
+int mxfp4_moe_decode_layer_fused_router_qkv(const void* x, const float* resid, const void* norm_w, float eps,
+                                            const uint8_t* router_wp, const uint8_t* router_ws, int norm,
+                                            void* x_out, void* y_out, float* logits_out, int32_t* ids_out,
+                                            float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                            const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                            const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                            const void* qkv_norm_w, const uint8_t* qkv_wp, const uint8_t* qkv_ws,
+                                            int Nq, float* qkv_out, void* x_next_out, float* out,
+                                            void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * A run of consecutive decode MoE layers in one launch (batch 1).  No single
  * reference entry point: it replaces the per-layer loop of

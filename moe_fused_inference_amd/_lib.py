@@ -40,6 +40,12 @@ SIGNATURES = {
                                                    _c_p, _c_p, _c_p, _c_p, _c_p,
                                                    _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                                    _c_i, _c_i, _c_i, _c_i, _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_moe_decode_layer_fused_router_qkv": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_i,
+                                                       _c_p, _c_p, _c_p, _c_p, _c_p,
+                                                       _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                                       _c_i, _c_i, _c_i, _c_i,
+                                                       _c_p, _c_p, _c_p, _c_i, _c_p, _c_p,
+                                                       _c_p, _c_p, _c_sz, _c_p]),
     "mxfp4_decode_stack_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
     "mxfp4_decode_stack_reset": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_decode_stack_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),

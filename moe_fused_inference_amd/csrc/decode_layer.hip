@@ -33,8 +33,9 @@
 //     (kEmpty's byte 1 is not), so no published word equals kEmpty.
 //     Producers store with agent-scope
 //     atomic stores (write-through to the device coherence point).  A
-//     consumer first polls one word per thread with agent-scope atomic loads
-//     (little traffic while the weights stream), then reloads all of its
+//     consumer first polls one word per wave with agent-scope atomic loads
+//     (one request per wave and round while the weights stream: polling a
+//     word per thread cost the step ~0.5 us per layer), then reloads all of its
 //     words with 16-byte buffer loads carrying the same agent-scope cache
 //     policy until none is empty.  (A release/acquire fence pair would
 //     instead write back and invalidate a whole L2 per workgroup.)
@@ -77,9 +78,13 @@ constexpr int kErrOff = 256;          // int32 error flag
 constexpr int kMemoAOff = 1024;       // int32 launch count of gate/up workgroup (s, jb): [8][32]
 constexpr int kMemoBOff = 2048;       // int32 launch count of down workgroup cb: [128]
 constexpr int kMemoROff = 2560;       // int32 launch count of router workgroup r (fused router): [16]
+constexpr int kMemoQOff = 3072;       // int32 launch count of q|k|v workgroup q (fused router tail): [128]
 constexpr int kLogOff = 4096;         // fused router: (logit, tag) 64-bit words, n_experts <= 256
-constexpr int kHOff = 8192;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart
+constexpr int kHOff = 8192;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
+                                      // then (out[c], tag) 64-bit words, c < H, for the q|k|v tail
 constexpr int kMaxRouterWg = 16;      // fused router: 16 logits per workgroup
+constexpr int kMaxQkvWg = 128;        // q|k|v tail: 64 rows per workgroup, up to 8192 rows
+constexpr int kMaxH = 2048;
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -108,6 +113,15 @@ struct LayerArgs {
     uint16_t* y_out;          // optional (H) the normed row (the MoE input)
     float* logits_out;        // optional (n_experts) the router logits
     int nr;                   // router workgroups (n_experts / 16)
+    // q|k|v tail (ROUTE_FUSED with nq > 0): the next layer's input RMSNorm
+    // and q|k|v projection of x_next = bf16(x_out + bf16(out)), in the same
+    // launch after the MoE
+    const uint16_t* qnw;      // (H) bf16 next layer's input norm weight
+    const uint8_t* qwp;       // (Nq, H/2) + (Nq, H/32) MXFP4 q|k|v weight
+    const uint8_t* qws;
+    float* qkv_out;           // (Nq) fp32
+    uint16_t* xn_out;         // optional (H) bf16 x_next
+    int nq, Nq;               // tail workgroups (ceil(Nq / 64)) and rows
     int n_experts;            // experts per layer (logits routing)
     int norm;                 // renormalise the top-E weights (logits routing)
     int32_t* ids_out;         // optional (E) ids / weights written by workgroup 0 (logits routing)
@@ -211,6 +225,13 @@ __device__ __forceinline__ bool poll_logits(const LayerArgs& a, uint32_t tag, fl
     const uint64_t* words = reinterpret_cast<const uint64_t*>(a.ws + kLogOff);
     const int lane = threadIdx.x & 63;
     int spins = 0;
+    // the last logit first, one request per wave and round
+    while (true) {
+        const uint64_t w = __hip_atomic_load(words + (a.n_experts - 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane((uint32_t)(w >> 32)) == tag) break;
+        if (++spins >= kSpinLimit) return false;
+        __builtin_amdgcn_s_sleep(2);
+    }
     while (true) {
         bool pending = false;
 #pragma unroll
@@ -305,6 +326,153 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
     }
 }
 
+// The (out[c], tag) words the down workgroups publish for the q|k|v tail.
+__device__ __forceinline__ uint64_t* out_words(const LayerArgs& a) {
+    return reinterpret_cast<uint64_t*>(a.ws + kHOff + (size_t)2 * a.bufwords * 4);
+}
+
+// q|k|v tail workgroup qi (fused router, nq > 0): rows 64qi .. 64qi+63 of
+// the next layer's q|k|v projection, wave w rows 64qi + 16w .. +15.  The
+// weights are loaded first and stream while the MoE runs; the workgroup then
+// waits (bounded) for this launch's MoE output words of its thread's eight
+// columns, forms x_next = bf16(x' + bf16(out)) with x' = bf16(x + bf16(o)) as
+// fused_norm_row computes it, and runs mxfp4_rmsnorm_lin_pq's arithmetic:
+// the RMSNorm (same order of the sum of squares), the MXFP4 row, and the
+// GEMV with K split in four parts of four MFMA steps (block 16p + 4s + g at
+// step s of part p), the parts added in order -- so x_next equals a separate
+// mxfp4_rmsnorm_lin_pq call's bit for bit, and so does qkv_out where that
+// call splits K in four (4081 to 8192 rows: 5120 for 32 + 2 x 4 heads of 128).
+__device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred, int qi) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoQOff) + qi;
+    const int launch = *memo;
+    const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+    const int row_i = 64 * qi + 16 * wave + r;
+    const int row = min(row_i, a.Nq - 1);
+    const uint8_t* wr = a.qwp + (int64_t)row * (kMaxH / 2) + g * 16;
+    uint4 wq[4][4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wq[p][s] = *reinterpret_cast<const uint4*>(wr + (16 * p + 4 * s) * 16);
+    uint4 sc4[4];   // the row's 64 scale bytes: block 16p + 4s + g is byte g of dword s of sc4[p]
+#pragma unroll
+    for (int p = 0; p < 4; ++p) sc4[p] = *reinterpret_cast<const uint4*>(a.qws + (int64_t)row * (kMaxH / 32) + 16 * p);
+    const int k0 = 8 * tid;
+    const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
+    const float4 o0 = *reinterpret_cast<const float4*>(a.oproj + k0);
+    const float4 o1 = *reinterpret_cast<const float4*>(a.oproj + k0 + 4);
+    const uint4 wn = *reinterpret_cast<const uint4*>(a.qnw + k0);
+    // this launch's MoE output of columns k0 .. k0+7
+    const uint64_t* yw = out_words(a) + k0;
+    const uint32_t tag = (uint32_t)(launch + 1);
+    float yo[8];
+    // one probe word per wave first (the first column of the wave's last
+    // thread; one request per round while the weights stream), then every
+    // thread's words until all carry the tag
+    bool ok = cfg == a.cfg;
+    int spins = 0;
+    while (ok) {
+        const uint64_t w0 = __hip_atomic_load(out_words(a) + 8 * (64 * wave + 63), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane((uint32_t)(w0 >> 32)) == tag) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    while (ok) {
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint64_t w = __hip_atomic_load(yw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            yo[i] = __uint_as_float((uint32_t)w);
+            pending |= (uint32_t)(w >> 32) != tag;
+        }
+        if (!pending) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");
+    }
+    if (__syncthreads_or(!ok)) {
+        if (tid == 0) {
+            set_error(a);
+            *memo = launch + 1;
+        }
+        return;
+    }
+    const uint32_t xw[4] = {q.x, q.y, q.z, q.w};
+    const float of[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+    float v[8];
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float xi = mx::bf16_to_f32((uint16_t)(xw[i / 2] >> (16 * (i & 1))));
+        const float xp = mx::bf16_to_f32(mx::f32_to_bf16_rne(xi + mx::bf16_to_f32(mx::f32_to_bf16_rne(of[i]))));
+        v[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(xp + mx::bf16_to_f32(mx::f32_to_bf16_rne(yo[i]))));
+        ss = fmaf(v[i], v[i], ss);
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if (lane == 0) nred[wave] = ss;
+    __syncthreads();
+    const float var = ((nred[0] + nred[1]) + (nred[2] + nred[3])) / (float)kMaxH;
+    const float rr = 1.0f / sqrtf(var + a.eps);
+    const uint32_t ww[4] = {wn.x, wn.y, wn.z, wn.w};
+    float y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float wi = mx::bf16_to_f32((uint16_t)(ww[i / 2] >> (16 * (i & 1))));
+        const float t = mx::bf16_to_f32(mx::f32_to_bf16_rne(v[i] * rr));
+        y[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(t * wi));
+    }
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(y[i]));
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor1>(am));
+    am = fmaxf(am, mx::dpp<mx::kDppQuadXor2>(am));
+    const uint32_t code = mx::e8m0_code(am);
+    *reinterpret_cast<uint32_t*>(sm.r.xq + 4 * tid) = mx::e2m1_pack8_short(y, mx::e8m0_inv_scale(code));
+    if ((tid & 3) == 0) sm.r.xs[tid >> 2] = (uint8_t)code;
+    if (qi == 0 && a.xn_out) {
+        uint32_t xo[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            xo[i] = (uint32_t)mx::f32_to_bf16_rne(v[2 * i]) | ((uint32_t)mx::f32_to_bf16_rne(v[2 * i + 1]) << 16);
+        *reinterpret_cast<uint4*>(a.xn_out + k0) = make_uint4(xo[0], xo[1], xo[2], xo[3]);
+    }
+    __syncthreads();
+    // every A row is the normed row (as mxfp4_rmsnorm_lin_pq at M = 1), D[0][r] = row 16w + r
+    mx::v4f acc[4];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        acc[p] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
+        const uint32_t sw[4] = {sc4[p].x, sc4[p].y, sc4[p].z, sc4[p].w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = 16 * p + 4 * s + g;
+            const uint4 aq = *reinterpret_cast<const uint4*>(sm.r.xq + c * 16);
+            acc[p] = mx::mfma16_fp4(aq, wq[p][s], acc[p], (uint32_t)sm.r.xs[c], (sw[s] >> (8 * g)) & 0xFFu);
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) mx::pin(acc[p]);   // the whole MFMA chain before the lane < 16 branch
+    float t = acc[0][0];
+    t += acc[1][0];
+    t += acc[2][0];
+    t += acc[3][0];
+    if (lane < 16 && row_i < a.Nq) a.qkv_out[row_i] = t;
+    if (tid == 0) {
+        *memo = launch + 1;
+        if (cfg != a.cfg) set_error(a);
+    }
+}
+
 // Where the routing comes from: kernel arguments, device arrays, or router
 // logits in device memory (softmax / top-E / renormalise computed by every
 // wave at entry, mx::wave_topk).
@@ -330,6 +498,11 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     if constexpr (ROUTE == ROUTE_FUSED) {
         if (bid < 0) {
             router_wg(a, sm, nred, (int)blockIdx.x);
+            return;
+        }
+        // q|k|v tail workgroups follow the down workgroups
+        if (bid >= nA + (a.H >> 4)) {
+            qkv_wg(a, sm, nred, bid - nA - (a.H >> 4));
             return;
         }
     }
@@ -498,6 +671,14 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 if (ROUTE != ROUTE_FUSED && bid == 0)
                     for (int k = 0; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
             }
+            // likewise the q|k|v tail slots this launch has no workgroup for
+            if (bid == 0) {
+                const int nq = ROUTE == ROUTE_FUSED ? a.nq : 0;
+                int* mq = reinterpret_cast<int*>(a.ws + kMemoQOff);
+#pragma unroll
+                for (int k = lane; k < kMaxQkvWg; k += 64)
+                    if (k >= nq) mq[k] += 1;
+            }
         }
         return;
     }
@@ -568,7 +749,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     bool ok = cfg_ok;
     if (cfg_ok) {
         int spins = 0;
-        const int w0 = min(8 * (int)threadIdx.x, nwords - 1);
+        const int w0 = min(8 * (64 * wave + 63), nwords - 1);   // one probe word per wave
         uint32_t probe = __hip_atomic_load(cur + w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         while (probe == kEmpty) {
             if (++spins >= kSpinLimit) {
@@ -696,6 +877,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const float y = sm.b.red[0][threadIdx.x] + sm.b.red[1][threadIdx.x] + sm.b.red[2][threadIdx.x] +
                         sm.b.red[3][threadIdx.x];
         a.out[c] = y;
+        if (ROUTE == ROUTE_FUSED && a.nq > 0)   // for the q|k|v tail: (value, this launch's tag)
+            __hip_atomic_store(out_words(a) + c, (uint64_t)__float_as_uint(y) | ((uint64_t)(uint32_t)(launch + 1) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (a.resid) {
             // runtime/model_runner_v2.py:208: x = x + moe.bfloat16() in bf16
             const float yb = mx::bf16_to_f32(mx::f32_to_bf16_rne(y));
@@ -711,6 +895,7 @@ __global__ void reset_workspace_kernel(uint32_t* ws, int cfg, int hwords) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < kHOff / 4) ws[i] = (i == kCfgOff / 4) ? (uint32_t)cfg : 0u;
     if (i < hwords) ws[kHOff / 4 + i] = kEmpty;
+    if (i < 2 * kMaxH) ws[kHOff / 4 + hwords + i] = 0u;   // output words: tag 0, which no launch uses
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -722,7 +907,7 @@ int buf_words(int E, int Mi) { return (int)(align256((size_t)E * (Mi / 32) * kRe
 
 extern "C" size_t mxfp4_decode_layer_workspace_size(int E, int Mi) {
     if (E <= 0 || Mi <= 0) return 0;
-    return kHOff + (size_t)2 * buf_words(E, Mi) * 4;
+    return kHOff + (size_t)2 * buf_words(E, Mi) * 4 + (size_t)kMaxH * 8;
 }
 
 extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream) {
@@ -730,7 +915,7 @@ extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, v
     MXH_REQUIRE(E >= 1 && E <= kMaxE && Mi >= 32 && Mi <= 1024 && Mi % 32 == 0 && H >= 512 && H <= 2048 && H % 512 == 0,
                 "decode_layer_reset: E=%d H=%d Mi=%d out of range", E, H, Mi);
     const int hw = 2 * buf_words(E, Mi);
-    const int n = hw > kHOff / 4 ? hw : kHOff / 4;
+    const int n = max(max(hw, kHOff / 4), 2 * kMaxH);
     hipLaunchKernelGGL(reset_workspace_kernel, dim3((n + 255) / 256), dim3(256), 0, mxh::as_stream(stream),
                        static_cast<uint32_t*>(workspace), layer_cfg(E, H, Mi), hw);
     return mxh::launch_status("decode_layer_reset");
@@ -789,9 +974,11 @@ int launch_layer(const LayerArgs& a, hipStream_t st) {
     const int nA = a.E * (a.Mi / 32);
     const int nB = a.H / 16;
     const int nR = ROUTE == ROUTE_FUSED ? a.nr : 0;
+    const int nQ = ROUTE == ROUTE_FUSED ? a.nq : 0;
     const int steps = (a.Mi / 32 + 3) / 4;
-    if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), dim3(nR + nA + nB), dim3(256), 0, st, a);
-    else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), dim3(nR + nA + nB), dim3(256), 0, st, a);
+    const dim3 grid(nR + nA + nB + nQ);
+    if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), grid, dim3(256), 0, st, a);
     return mxh::launch_status("moe_decode_layer");
 }
 }  // namespace
@@ -841,14 +1028,13 @@ extern "C" int mxfp4_moe_decode_layer_routed(const void* x, const float* logits,
     return launch_layer<ROUTE_LOGITS>(a, mxh::as_stream(stream));
 }
 
-extern "C" int mxfp4_moe_decode_layer_fused_router(const void* x, const float* resid, const void* norm_w, float eps,
-                                                   const uint8_t* router_wp, const uint8_t* router_ws, int norm,
-                                                   void* x_out, void* y_out, float* logits_out, int32_t* ids_out,
-                                                   float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
-                                                   const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
-                                                   const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
-                                                   float* out, void* workspace, size_t workspace_bytes, void* stream) {
-    LayerArgs a;
+namespace {
+int fused_router_args(LayerArgs& a, const void* x, const float* resid, const void* norm_w, float eps,
+                      const uint8_t* router_wp, const uint8_t* router_ws, int norm, void* x_out, void* y_out,
+                      float* logits_out, int32_t* ids_out, float* w_out, const uint8_t* gate_wp,
+                      const uint8_t* gate_ws, const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                      const uint8_t* down_ws, int n_experts, int E, int H, int Mi, float* out, void* workspace,
+                      size_t workspace_bytes) {
     const int rc = layer_args(a, x, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E, H, Mi, out,
                               nullptr, workspace, workspace_bytes);
     if (rc != MXFP4_OK) return rc;
@@ -876,5 +1062,51 @@ extern "C" int mxfp4_moe_decode_layer_fused_router(const void* x, const float* r
     a.ids_out = ids_out;
     a.w_out = w_out;
     a.nr = n_experts / 16;
+    return MXFP4_OK;
+}
+}  // namespace
+
+extern "C" int mxfp4_moe_decode_layer_fused_router(const void* x, const float* resid, const void* norm_w, float eps,
+                                                   const uint8_t* router_wp, const uint8_t* router_ws, int norm,
+                                                   void* x_out, void* y_out, float* logits_out, int32_t* ids_out,
+                                                   float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws,
+                                                   const uint8_t* up_wp, const uint8_t* up_ws, const uint8_t* down_wp,
+                                                   const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+                                                   float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    LayerArgs a;
+    const int rc = fused_router_args(a, x, resid, norm_w, eps, router_wp, router_ws, norm, x_out, y_out, logits_out,
+                                     ids_out, w_out, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E,
+                                     H, Mi, out, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_moe_decode_layer_fused_router_qkv(
+    const void* x, const float* resid, const void* norm_w, float eps, const uint8_t* router_wp,
+    const uint8_t* router_ws, int norm, void* x_out, void* y_out, float* logits_out, int32_t* ids_out, float* w_out,
+    const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp, const uint8_t* up_ws,
+    const uint8_t* down_wp, const uint8_t* down_ws, int n_experts, int E, int H, int Mi, const void* qkv_norm_w,
+    const uint8_t* qkv_wp, const uint8_t* qkv_ws, int Nq, float* qkv_out, void* x_next_out, float* out,
+    void* workspace, size_t workspace_bytes, void* stream) {
+    LayerArgs a;
+    const int rc = fused_router_args(a, x, resid, norm_w, eps, router_wp, router_ws, norm, x_out, y_out, logits_out,
+                                     ids_out, w_out, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E,
+                                     H, Mi, out, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE(qkv_norm_w && qkv_wp && qkv_ws && qkv_out, "moe_decode_layer_fused_router_qkv: null pointer");
+    MXH_REQUIRE(Nq >= 1 && Nq <= 64 * kMaxQkvWg, "moe_decode_layer_fused_router_qkv: Nq=%d (1..%d)", Nq,
+                64 * kMaxQkvWg);
+    MXH_REQUIRE(((uintptr_t)qkv_norm_w & 15) == 0 && ((uintptr_t)qkv_wp & 15) == 0 && ((uintptr_t)qkv_ws & 15) == 0 &&
+                    ((uintptr_t)x_next_out & 15) == 0,
+                "moe_decode_layer_fused_router_qkv: qkv_norm_w, qkv_wp, qkv_ws, x_next_out must be 16-byte aligned");
+    MXH_REQUIRE(!x_next_out || (x_next_out != x && x_next_out != x_out),
+                "moe_decode_layer_fused_router_qkv: x_next_out must not alias x or x_out");
+    a.qnw = static_cast<const uint16_t*>(qkv_norm_w);
+    a.qwp = qkv_wp;
+    a.qws = qkv_ws;
+    a.qkv_out = qkv_out;
+    a.xn_out = static_cast<uint16_t*>(x_next_out);
+    a.Nq = Nq;
+    a.nq = (Nq + 63) / 64;
     return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
 }

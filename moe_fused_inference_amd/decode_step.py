@@ -158,7 +158,7 @@ class DecodeStep:
     stay on the device: each step reads them and leaves the greedy next
     tokens and dpos + M for the next step."""
 
-    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True):
+    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True, qkv_tail=True):
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
         self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
@@ -167,6 +167,10 @@ class DecodeStep:
         # (mxfp4_moe_decode_layer_fused_router), one launch per layer fewer
         self.fused_router = (bool(fused_router) and self.M == 1 and cfg.hidden == 2048 and cfg.n_experts % 16 == 0
                              and cfg.n_experts <= 256)
+        # with the fused router, the next layer's input residual + RMSNorm +
+        # q|k|v projection also run in the MoE launch
+        # (mxfp4_moe_decode_layer_fused_router_qkv): another launch per layer fewer
+        self.qkv_tail = self.fused_router and bool(qkv_tail)
         self._fr_calls = {}
         c = cfg
         if c.head_dim != 128:
@@ -184,10 +188,12 @@ class DecodeStep:
         buf("dpos", (1,), i32)
         buf("x", (M, H), bf16)
         buf("x2", (M, H), bf16)
+        buf("x3", (M, H), bf16)
         buf("y", (M, H), bf16)
         buf("yq", (M, H // 2), u8)
         buf("ys", (M, H // 32), u8)
         buf("qkv", (M, c.qkv_rows), f32)
+        buf("qkv2", (M, c.qkv_rows), f32)   # odd layers' q|k|v with the q|k|v tail
         buf("aq", (M, Hq * D // 2), u8)
         buf("as_", (M, Hq * D // 32), u8)
         buf("oproj", (M, H), f32)
@@ -253,6 +259,58 @@ class DecodeStep:
                                              b.y.data_ptr(), b.yq.data_ptr(), b.ys.data_ptr(), s), "rmsnorm_quant")
             self._lin(b.yq, b.ys, w, w.n, H, out, s)
 
+    def qkv_buf(self, l):
+        """The buffer that holds layer l's q|k|v projection (M, qkv_rows) from
+        before its attention to the end of the step (read it from an
+        on_layer hook): with the q|k|v tail, layer l's projection is written
+        by layer l-1's MoE launch, so odd and even layers alternate buffers."""
+        return self.b.qkv2 if (self.qkv_tail and l % 2) else self.b.qkv
+
+    def _attn_oproj(self, l, lw, qkv, s):
+        """q/k head norm + RoPE, the step's KV rows and attention in one pass,
+        its output straight to MXFP4 of bf16(o) (the raw scores are not kept),
+        then o_proj into b.oproj."""
+        lib, c, b, M = self.lib, self.cfg, self.b, self.M
+        H, D, Hq, Hkv = c.hidden, c.head_dim, c.n_heads, c.n_kv_heads
+        kvk, kvv = b.kvk[l], b.kvv[l]
+        self._ck(lib.mxfp4_attn_decode_fused(qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(),
+                                             c.rms_eps, c.rope_theta, kvk.data_ptr(), kvv.data_ptr(),
+                                             b.dpos.data_ptr(), None, None, b.aq.data_ptr(),
+                                             b.as_.data_ptr(), M, Hq, Hkv, D, self.max_pos, self.kv_codec,
+                                             b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode_fused")
+        self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
+
+    def _layers_qkv_tail(self, on_layer, s):
+        """The layers at M = 1 with the q|k|v tail: per layer the attention,
+        o_proj and one MoE launch that also runs the router and the next
+        layer's input norm + q|k|v.  The residual stream rotates through
+        three buffers (a launch's x, x_out and x_next are distinct).
+        Returns (x_out of the last layer, a free buffer)."""
+        c, b, m = self.cfg, self.b, self.model
+        xs = (b.x, b.x2, b.x3)
+        L = len(m.layers)
+        self._norm_lin(b.x, None, m.layers[0].in_norm, None, False, m.layers[0].qkv, self.qkv_buf(0), s)
+        cur = 0                      # xs[cur]: the layer's input residual stream
+        for l, lw in enumerate(m.layers):
+            self._attn_oproj(l, lw, self.qkv_buf(l), s)
+            xo, xn = (cur + 1) % 3, (cur + 2) % 3
+            call = self._fr_calls.get(("tail", l))
+            if call is None:
+                nxt = None
+                if l + 1 < L:
+                    nl = m.layers[l + 1]
+                    nxt = (nl.in_norm, nl.qkv.wp, nl.qkv.ws, self.qkv_buf(l + 1)[0], xs[xn][0])
+                call = FusedRouterLayerCall(xs[cur][0], b.oproj[0], lw.post_norm, c.rms_eps, lw.gate.wp, lw.gate.ws,
+                                            c.top_k, lw.experts, b.moe[0], self.layer_ws, x_out=xs[xo][0],
+                                            y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt)
+                self._fr_calls[("tail", l)] = call
+            call(s)
+            if on_layer is not None:
+                on_layer(l, xs[xo], b.moe)
+            if l + 1 < L:
+                cur = xn
+        return xs[xo], xs[xn]
+
     def run(self, on_layer=None):
         """Issue one step on the current stream.  on_layer(l, x, moe): an
         optional eager hook after each layer's MoE (x is the residual stream
@@ -264,22 +322,15 @@ class DecodeStep:
         self._ck(lib.mxfp4_embed_rows(m.embed.wp.data_ptr(), m.embed.ws.data_ptr(), c.vocab, H, b.ids.data_ptr(), M,
                                       b.x.data_ptr(), s), "embed_rows")
         xa, xb = b.x, b.x2          # residual stream ping-pong
-        for l, lw in enumerate(m.layers):
+        if self.qkv_tail:
+            xa, xb = self._layers_qkv_tail(on_layer, s)
+        for l, lw in enumerate(m.layers if not self.qkv_tail else ()):
             # input norm (+ the previous layer's MoE residual) and the q|k|v projection
             resid = b.moe if l > 0 else None
             self._norm_lin(xa, resid, lw.in_norm, xb if l > 0 else None, False, lw.qkv, b.qkv, s)
             if l > 0:
                 xa, xb = xb, xa
-            kvk, kvv = b.kvk[l], b.kvv[l]
-            # q/k head norm + RoPE, the step's KV rows and attention in one
-            # pass, its output straight to MXFP4 of bf16(o) for o_proj (the raw
-            # scores are not kept)
-            self._ck(lib.mxfp4_attn_decode_fused(b.qkv.data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(),
-                                                 c.rms_eps, c.rope_theta, kvk.data_ptr(), kvv.data_ptr(),
-                                                 b.dpos.data_ptr(), None, None, b.aq.data_ptr(),
-                                                 b.as_.data_ptr(), M, Hq, Hkv, D, self.max_pos, self.kv_codec,
-                                                 b.attn_ws.data_ptr(), b.attn_ws.numel(), s), "attn_decode_fused")
-            self._lin(b.aq, b.as_, lw.o, H, Hq * D, b.oproj, s)
+            self._attn_oproj(l, lw, b.qkv, s)
             if self.fused_router:
                 # x = x + bf16(o), its RMSNorm (y), the router logits and the MoE in one launch
                 key = (l, xa.data_ptr())

@@ -130,30 +130,54 @@ class FusedRouterLayerCall:
     (mxfp4_moe_decode_layer_fused_router): x bf16 (H,) and resid fp32 (H,)
     in, x_out = bf16(x + bf16(resid)), the MoE of h2 = rms_norm(x_out) * norm_w
     in `out` (fp32 (H,)), routed on the logits of the MXFP4 router
-    (router_wp, router_ws) computed in the same launch."""
+    (router_wp, router_ws) computed in the same launch.
+
+    With next_qkv = (norm_w, wp, ws, qkv_out[, x_next]) the launch also runs
+    the next layer's input residual, RMSNorm and q|k|v projection
+    (mxfp4_moe_decode_layer_fused_router_qkv): x_next = bf16(x_out +
+    bf16(out)), qkv_out fp32 (Nq,) = MXFP4(rms_norm(x_next) * norm_w) . W^T
+    for the MXFP4 W = (wp (Nq, H/2), ws (Nq, H/32)); x_next must not alias x or x_out."""
 
     def __init__(self, x, resid, norm_w, eps, router_wp, router_ws, E, experts, out, ws, norm=True, x_out=None,
-                 y_out=None, logits_out=None, ids_out=None, w_out=None):
+                 y_out=None, logits_out=None, ids_out=None, w_out=None, next_qkv=None):
         self.lib = _lib.load()
         if (ids_out is None) != (w_out is None):
             raise RuntimeError("give ids_out and w_out both or neither")
-        n = experts.n_experts
-        if tuple(router_wp.shape) != (n, experts.hidden // 2) or tuple(router_ws.shape) != (n, experts.hidden // 32):
-            raise RuntimeError(f"router weights must be ({n}, {experts.hidden // 2}) + ({n}, {experts.hidden // 32})")
+        n, H = experts.n_experts, experts.hidden
+        if tuple(router_wp.shape) != (n, H // 2) or tuple(router_ws.shape) != (n, H // 32):
+            raise RuntimeError(f"router weights must be ({n}, {H // 2}) + ({n}, {H // 32})")
         if resid.dtype != torch.float32 or x.dtype != torch.bfloat16 or norm_w.dtype != torch.bfloat16:
             raise RuntimeError("x and norm_w must be bfloat16, resid float32")
         ptr = (lambda t: t.data_ptr() if t is not None else None)
-        self.keep = (x, resid, norm_w, router_wp, router_ws, experts, out, ws, x_out, y_out, logits_out, ids_out, w_out)
-        self.args = (x.data_ptr(), resid.data_ptr(), norm_w.data_ptr(), float(eps), router_wp.data_ptr(),
-                     router_ws.data_ptr(), int(bool(norm)), ptr(x_out), ptr(y_out), ptr(logits_out), ptr(ids_out),
-                     ptr(w_out), experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
-                     experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
-                     experts.down_wp.data_ptr(), experts.down_ws.data_ptr(),
-                     n, int(E), experts.hidden, experts.inter, out.data_ptr(), ws.data_ptr(), ws.numel())
+        self.keep = (x, resid, norm_w, router_wp, router_ws, experts, out, ws, x_out, y_out, logits_out, ids_out,
+                     w_out, next_qkv)
+        head = (x.data_ptr(), resid.data_ptr(), norm_w.data_ptr(), float(eps), router_wp.data_ptr(),
+                router_ws.data_ptr(), int(bool(norm)), ptr(x_out), ptr(y_out), ptr(logits_out), ptr(ids_out),
+                ptr(w_out), experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(),
+                experts.up_wp.data_ptr(), experts.up_ws.data_ptr(),
+                experts.down_wp.data_ptr(), experts.down_ws.data_ptr(),
+                n, int(E), H, experts.inter)
+        tail = (out.data_ptr(), ws.data_ptr(), ws.numel())
+        if next_qkv is None:
+            self.fn, self.what = self.lib.mxfp4_moe_decode_layer_fused_router, "moe_decode_layer_fused_router"
+            self.args = head + tail
+        else:
+            qnw, qwp, qws, qkv_out = next_qkv[:4]
+            x_next = next_qkv[4] if len(next_qkv) > 4 else None
+            nq = qwp.shape[0]
+            if tuple(qwp.shape) != (nq, H // 2) or tuple(qws.shape) != (nq, H // 32) or qwp.dtype != torch.uint8:
+                raise RuntimeError(f"q|k|v weights must be uint8 (Nq, {H // 2}) + (Nq, {H // 32})")
+            if qkv_out.dtype != torch.float32 or qkv_out.numel() != nq or qnw.dtype != torch.bfloat16:
+                raise RuntimeError("qkv_out must be float32 (Nq,), the norm weight bfloat16")
+            if x_next is not None and x_next.data_ptr() in (x.data_ptr(), ptr(x_out)):
+                raise RuntimeError("x_next must not alias x or x_out")
+            self.fn, self.what = self.lib.mxfp4_moe_decode_layer_fused_router_qkv, "moe_decode_layer_fused_router_qkv"
+            self.args = head + (qnw.data_ptr(), qwp.data_ptr(), qws.data_ptr(), nq, qkv_out.data_ptr(),
+                                ptr(x_next)) + tail
 
     def __call__(self, stream=None):
         s = torch.cuda.current_stream().cuda_stream if stream is None else stream
-        _lib.check(self.lib.mxfp4_moe_decode_layer_fused_router(*self.args, s), "moe_decode_layer_fused_router")
+        _lib.check(self.fn(*self.args, s), self.what)
 
 
 def decode_layer_routed(x, logits, E, experts, norm=True, out=None, resid=None, ws=None, want_routing=False):

@@ -107,7 +107,7 @@ def run_cfg5(model, M, n_steps):
             torch.cuda.synchronize()
             b = st.b
             if l in CHECK:   # the GPU's intermediates of this layer, for stage-wise teacher forcing
-                stages[l] = {"qkv": np_(b.qkv), "oproj": np_(b.oproj), "x_mid": np_(xa.float()),
+                stages[l] = {"qkv": np_(st.qkv_buf(l)), "oproj": np_(b.oproj), "x_mid": np_(xa.float()),
                              "hp2": np_(b.y.float()), "glog": np_(b.glog), "moe": np_(moe)}
             xs.append(np_((xa.float() + moe.bfloat16().float()).bfloat16().float()))
 
@@ -166,3 +166,32 @@ def test_cfg5_decode_step_one_token(model):
 
 def test_cfg5_decode_step_batch8(model):
     run_cfg5(model, 8, 2)
+
+
+def test_cfg5_launch_fusions_equal_separate_launches(model):
+    """The M = 1 step with the q|k|v tail (the next layer's input norm +
+    q|k|v inside each MoE launch) equals the step with that projection as its
+    own launch, bit for bit: logits, greedy ids, every layer's KV rows and the
+    final residual stream, over two steps from the same state."""
+    m, _ = model
+    res = {}
+    for tail in (True, False):
+        st = DecodeStep(m, CFG, M=1, max_pos=MAX_POS, device=DEV, qkv_tail=tail)
+        assert st.qkv_tail == tail and st.fused_router
+        pos = MAX_POS - 2
+        st.fill_cache(pos, seed=19)
+        st.set_state([4242], pos)
+        out = []
+        for _ in range(2):
+            st.run()
+            st.check_status()
+            out.append((np_(st.b.logits).copy(), np_(st.b.ids).copy(), np_(st.x_final.view(torch.int16)).copy()))
+        kv = (np_(st.b.kvk[:, pos:pos + 2]).copy(), np_(st.b.kvv[:, pos:pos + 2]).copy())
+        res[tail] = (out, kv)
+        del st
+        torch.cuda.synchronize()
+    (ot, kt), (of, kf) = res[True], res[False]
+    for i, (a, b) in enumerate(zip(ot, of)):
+        assert all(np.array_equal(u, v) for u, v in zip(a, b)), f"step {i} differs"
+    assert np.array_equal(kt[0], kf[0]) and np.array_equal(kt[1], kf[1]), "KV rows differ"
+    log(f"  q|k|v tail step == separate-launch step (ids {ot[0][1].tolist()}, {ot[1][1].tolist()})")

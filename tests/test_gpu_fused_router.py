@@ -140,3 +140,133 @@ def test_fused_router_argument_checks(dext):
     assert "multiple of 16" in lib.mxfp4_last_error().decode()
     assert lib.mxfp4_moe_decode_layer_fused_router(*args, 32, E, 1024, MI, p, *tail) == -1
     assert "2048" in lib.mxfp4_last_error().decode()
+
+
+def _qkv_reference(lib, x_out, out, qnw, qwp, qws, nq):
+    """The next layer's input residual + norm + q|k|v as the separate
+    mxfp4_rmsnorm_lin_pq call."""
+    xn = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    qkv = torch.empty(nq, dtype=torch.float32, device=DEV)
+    _lib.check(lib.mxfp4_rmsnorm_lin_pq(x_out.data_ptr(), out.data_ptr(), qnw.data_ptr(), EPS, 1, H, xn.data_ptr(),
+                                        None, None, None, qwp.data_ptr(), qws.data_ptr(), nq, qkv.data_ptr(), None),
+               "rmsnorm_lin_pq")
+    return xn, qkv
+
+
+@pytest.mark.parametrize("nq", [5120, 1000])
+def test_fused_router_qkv_tail_matches_separate_calls(dext, nq):
+    """mxfp4_moe_decode_layer_fused_router_qkv: the MoE part equals the
+    launch without the tail, and qkv_out / x_next equal the next layer's
+    mxfp4_rmsnorm_lin_pq on (x_out, out) bit for bit.  The tail splits K in
+    four parts, as rmsnorm_lin_pq does for 4081..8192 rows, so the reference
+    projects onto 5120 rows whose first nq are the tail's.  Launches with and
+    without the tail, and plain fused-layer launches, share one workspace."""
+    lib = _lib.load()
+    n_exp = 128
+    experts = make_stack(dext, n_exp, H, MI, seed=14000 + nq)
+    rwp, rws = rand_weight(dext, n_exp, H, seed=14100 + nq, std=0.05)
+    nref = 5120
+    qwp_all, qws_all = rand_weight(dext, nref, H, seed=14200 + nq, std=0.05)
+    qwp, qws = qwp_all[:nq], qws_all[:nq]
+    g = torch.Generator(device=DEV)
+    g.manual_seed(nq)
+    ws = moe_layer.workspace(E, MI, H)
+    for it in range(4):
+        xa, o, _ = _inputs(g)
+        nw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+        qnw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+        out = torch.empty(H, dtype=torch.float32, device=DEV)
+        x_out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        qkv = torch.full((nq,), float("nan"), dtype=torch.float32, device=DEV)
+        x_next = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        ids_out = torch.empty(E, dtype=torch.int32, device=DEV)
+        w_out = torch.empty(E, dtype=torch.float32, device=DEV)
+        moe_layer.FusedRouterLayerCall(xa, o, nw, EPS, rwp, rws, E, experts, out, ws, x_out=x_out, ids_out=ids_out,
+                                       w_out=w_out, next_qkv=(qnw, qwp, qws, qkv, x_next))()
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(ws) == 0
+        # the same launch without the tail
+        out2 = torch.empty(H, dtype=torch.float32, device=DEV)
+        x_out2 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+        moe_layer.FusedRouterLayerCall(xa, o, nw, EPS, rwp, rws, E, experts, out2, ws, x_out=x_out2)()
+        xn_ref, qkv_ref = _qkv_reference(lib, x_out2, out2, qnw, qwp_all, qws_all, nref)
+        qkv_ref = qkv_ref[:nq]
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(ws) == 0
+        assert torch.equal(out, out2) and torch.equal(x_out, x_out2), "MoE part differs from the launch without tail"
+        assert torch.equal(x_next, xn_ref), "x_next differs from rmsnorm_lin_pq's residual"
+        if not torch.equal(qkv, qkv_ref):
+            a, b = np_(qkv), np_(qkv_ref)
+            bad = np.nonzero(a != b)[0]
+            fin = np.isfinite(a)
+            rel = np.abs(a[fin] - b[fin]) / (np.abs(b[fin]) + 1e-6)
+            log(f"  nq={nq} launch {it}: {bad.size} of {nq} rows differ, first {bad[:12].tolist()}, "
+                f"finite {int(fin.sum())}, median rel of finite {float(np.median(rel)) if rel.size else -1:.3e}, "
+                f"bad by wave {np.bincount((bad % 64) // 16, minlength=4).tolist()}, by lane {np.bincount(bad % 16, minlength=16).tolist()}, "
+                f"ratio a/b first {(a[bad[:6]] / b[bad[:6]]).tolist()}")
+        assert torch.equal(qkv, qkv_ref), "q|k|v differs from rmsnorm_lin_pq"
+        log(f"  nq={nq} launch {it}: out, x_next and q|k|v equal the separate calls "
+            f"(|qkv| max {float(qkv.abs().max()):.3f})")
+        # a plain launch in between keeps every launch count in step
+        moe_layer.decode_layer(x_out, ids_out, w_out, experts, ws=ws)
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(ws) == 0
+
+
+def test_fused_router_qkv_tail_graph_replays(dext):
+    """Two chained tail launches (the second's x is the first's x_next) in a
+    captured graph; every replay equals the eager run."""
+    n_exp, nq = 32, 5120
+    experts = make_stack(dext, n_exp, H, MI, seed=15000)
+    rwp, rws = rand_weight(dext, n_exp, H, seed=15100, std=0.05)
+    qwp, qws = rand_weight(dext, nq, H, seed=15200, std=0.05)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(6)
+    xa, o, nw = _inputs(g)
+    ws = moe_layer.workspace(E, MI, H)
+    out = torch.empty(H, dtype=torch.float32, device=DEV)
+    x_out = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    x_next = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    x_next2 = torch.empty(H, dtype=torch.bfloat16, device=DEV)
+    qkv = torch.empty(nq, dtype=torch.float32, device=DEV)
+    qkv2 = torch.empty(nq, dtype=torch.float32, device=DEV)
+    calls = [moe_layer.FusedRouterLayerCall(xa, o, nw, EPS, rwp, rws, E, experts, out, ws, x_out=x_out,
+                                            next_qkv=(nw, qwp, qws, qkv, x_next)),
+             moe_layer.FusedRouterLayerCall(x_next, o, nw, EPS, rwp, rws, E, experts, out, ws, x_out=x_out,
+                                            next_qkv=(nw, qwp, qws, qkv2, x_next2))]
+
+    def run():
+        for c in calls:
+            c()
+
+    run()
+    torch.cuda.synchronize()
+    eager = [t.clone() for t in (qkv, qkv2, x_next2, out)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            run()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        for t in (qkv, qkv2, x_next2, out):
+            t.zero_()
+        _ = torch.randn(1024, device=DEV).sum().item()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert all(torch.equal(a, b) for a, b in zip((qkv, qkv2, x_next2, out), eager)), f"replay {rep}"
+    assert moe_layer.layer_status(ws) == 0
+
+
+def test_fused_router_qkv_argument_checks(dext):
+    lib = _lib.load()
+    p = 256
+    args = [p, p, p, 1e-6, p, p, 1, None, None, None, None, None, p, p, p, p, p, p, 32, E, H, MI]
+    ws = moe_layer.workspace(E, MI, H)
+    tail = [p, ws.data_ptr(), ws.numel(), None]
+    assert lib.mxfp4_moe_decode_layer_fused_router_qkv(*args, p, p, p, 0, p, None, *tail) == -1
+    assert "Nq=0" in lib.mxfp4_last_error().decode()
+    assert lib.mxfp4_moe_decode_layer_fused_router_qkv(*args, p, p, p, 8193, p, None, *tail) == -1
+    assert lib.mxfp4_moe_decode_layer_fused_router_qkv(*args, None, p, p, 64, p, None, *tail) == -1
+    assert "null" in lib.mxfp4_last_error().decode()
