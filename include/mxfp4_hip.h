@@ -186,6 +186,16 @@ int mxfp4_attn_decode_fused(const float* qkv, const void* q_norm_w, const void* 
                             uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, int codec,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* mxfp4_attn_decode_fused_partials: the first pass of mxfp4_attn_decode_fused
+ * alone -- q/k norm, RoPE, the KV write and every 64-position chunk's softmax
+ * record -- leaving the records in the workspace for the merge that
+ * mxfp4_decode_layer_post_attn runs at the front of the MoE launch (no merge
+ * launch here).  Arguments as mxfp4_attn_decode_fused without outputs. */
+int mxfp4_attn_decode_fused_partials(const float* qkv, const void* q_norm_w, const void* k_norm_w, float eps,
+                                     float theta, uint8_t* kvk, uint8_t* kvv, const int32_t* dpos, int M, int Hq,
+                                     int Hkv, int D, int max_pos, int codec, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------------
  * KV write: k, v bf16 (M, Hkv, D) -> the reference's E4M3 bytes (rounding
  * half away from zero, >= 248 saturating to 0x7F) at rows dpos+m < max_pos
@@ -299,6 +309,41 @@ int mxfp4_moe_decode_layer_fused_router_qkv(const void* x, const float* resid, c
                                             const void* qkv_norm_w, const uint8_t* qkv_wp, const uint8_t* qkv_ws,
                                             int Nq, float* qkv_out, void* x_next_out, float* out,
                                             void* workspace, size_t workspace_bytes, void* stream);
+
+/* Everything of a decode layer after the attention scores, for one token
+ * (batch 1), in one launch: the merge of the attention chunk records
+ * (mxfp4_attn_decode_fused_partials' workspace; attn_decode's merge,
+ * src/ext/mxfp4_decode.cu:366-430), o_proj on the MXFP4 of bf16(o)
+ * (runtime/model_runner_v2.py:175-178, lin_pq), then
+ * mxfp4_moe_decode_layer_fused_router_qkv (residual, RMSNorm, router, MoE and,
+ * when qkv_wp is given, the next layer's input norm + q|k|v).  32 merge
+ * workgroups and H/16 o_proj workgroups hand their rows on as tagged words
+ * (bounded waits, as for h).  No single counterpart in the reference, whose
+ * step runs these as separate launches; it leaves the step two launches per
+ * layer.  The attention output (aq_out / as_out, optional) and oproj_out
+ * equal attn_decode_mx's MXFP4 rows and lin_pq's output bit for bit.
+ *   attn_workspace  the records of mxfp4_attn_decode_fused_partials (M = 1),
+ *                   attn_workspace_bytes >= mxfp4_attn_decode_workspace_size(1,
+ *                   Hq, max_pos); dpos the token's position (device)
+ *   Hq = 32 query heads of 128 (o_proj K = 4096); o_wp / o_ws the MXFP4
+ *   o_proj (H, 2048) + (H, 128); oproj_out fp32 (H), required
+ *   x, norm_w, ... out, workspace: as mxfp4_moe_decode_layer_fused_router
+ *   with resid = this launch's o_proj output; qkv_*: as
+ *   mxfp4_moe_decode_layer_fused_router_qkv, or qkv_wp NULL for no tail.
+ * 16-byte aligned (aq_out 4-byte).  A position outside [0, max_pos) gives a
+ * zero attention output.  Same workspace as mxfp4_moe_decode_layer.
+ */
+int mxfp4_decode_layer_post_attn(const void* attn_workspace, size_t attn_workspace_bytes, const int32_t* dpos,
+                                 int Hq, int max_pos, uint8_t* aq_out, uint8_t* as_out, const uint8_t* o_wp,
+                                 const uint8_t* o_ws, float* oproj_out, const void* x, const void* norm_w,
+                                 float eps, const uint8_t* router_wp, const uint8_t* router_ws, int norm,
+                                 void* x_out, void* y_out, float* logits_out, int32_t* ids_out, float* w_out,
+                                 const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+                                 const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
+                                 int n_experts, int E, int H, int Mi, const void* qkv_norm_w,
+                                 const uint8_t* qkv_wp, const uint8_t* qkv_ws, int Nq, float* qkv_out,
+                                 void* x_next_out, float* out, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /* ---------------------------------------------------------------------
  * A run of consecutive decode MoE layers in one launch (batch 1).  No single

@@ -46,6 +46,15 @@ SIGNATURES = {
                                                        _c_i, _c_i, _c_i, _c_i,
                                                        _c_p, _c_p, _c_p, _c_i, _c_p, _c_p,
                                                        _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_decode_layer_post_attn": (_c_i, [_c_p, _c_sz, _c_p, _c_i, _c_i, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                            _c_p, _c_p, ctypes.c_float, _c_p, _c_p, _c_i,
+                                            _c_p, _c_p, _c_p, _c_p, _c_p,
+                                            _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                                            _c_i, _c_i, _c_i, _c_i,
+                                            _c_p, _c_p, _c_p, _c_i, _c_p, _c_p,
+                                            _c_p, _c_p, _c_sz, _c_p]),
+    "mxfp4_attn_decode_fused_partials": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_p,
+                                                _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),
     "mxfp4_decode_stack_workspace_size": (_c_sz, [_c_i, _c_i, _c_i]),
     "mxfp4_decode_stack_reset": (_c_i, [_c_p, _c_i, _c_i, _c_i, _c_p]),
     "mxfp4_decode_stack_status": (_c_i, [_c_p, ctypes.POINTER(ctypes.c_int)]),

@@ -26,6 +26,7 @@
 // outputs must match it: rounding half away from zero, |v| >= 248 saturating
 // to 0x7F, subnormal codes read as m * 2^-6 (standard E4M3: m * 2^-9) and
 // exponent-15 codes read as 56 * (8 + m).
+#include "attn_merge.h"
 #include "head_rope.h"
 #include "mx_device.h"
 #include "mx_host.h"
@@ -36,13 +37,13 @@ namespace {
 using kv::e4m3_ref_decode;
 using kv::e4m3_ref_encode;
 
-constexpr int kD = 128;          // head dimension (the reference's kernels assume 128)
-constexpr int kChunk = 64;       // positions per score workgroup
+using am::kD;           // head dimension
+using am::kChunk;       // positions per score workgroup
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t b) { return __uint_as_float((uint32_t)b << 16); }
 
-constexpr int kPart = 132;       // floats per partial record: max, sum, 128 column sums, pad
-constexpr int kMaxChunks = 1024; // max_pos <= 65536
+using am::kPart;        // floats per partial record: max, sum, 128 column sums, pad
+using am::kMaxChunks;   // max_pos <= 65536
 constexpr int kMaxFusedM = 16;   // tokens per call of the fused entry (the decode step's M)
 
 // The fused entry's extra inputs: the fp32 q|k|v projection rows (M, (Hq +
@@ -378,135 +379,25 @@ __global__ __launch_bounds__(256) void attn_partial_kernel(const uint16_t* __res
         }
 }
 
-// Workgroup (query head h, token m), 256 threads: merges the chunk records,
-// o = sum_c exp(m_c - M) acc_c / sum_c exp(m_c - M) l_c with M = max_c m_c.
-// Up to 64 chunks (context 4096): one pass, thread (column pair, chunk phase
-// cq) loads the statistics and column sums of the chunks c = cq mod 4 at
-// once.  Longer contexts: pass 1 loads every chunk's (m_c, l_c) (a thread per
-// chunk), pass 2 sums the column records with all loads in flight.  The four
-// phases meet in LDS.  The
-// output is fp32 o and/or the MXFP4 rows (oq, os) of bf16(o) (32-blocks of
-// 16 column pairs, the quantizer's rule).
+// Workgroup (query head h, token m), 256 threads: merges the chunk records
+// (am::merge_head).  The output is fp32 o and/or the MXFP4 rows (oq, os) of
+// bf16(o) (32-blocks of 16 column pairs, the quantizer's rule).
 __global__ __launch_bounds__(256) void attn_final_kernel(const float* __restrict__ part, float* __restrict__ o,
                                                          uint8_t* __restrict__ oq, uint8_t* __restrict__ os,
                                                          const int32_t* __restrict__ dpos, int Hq, int max_pos,
                                                          int nchunk) {
-    const int h = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+    const int h = blockIdx.x, m = blockIdx.y, lane = threadIdx.x & 63;
     const int pos = *dpos + m;
     if (pos < 0 || pos >= max_pos) return;
     const int n = pos / kChunk + 1;            // chunks holding positions 0..pos
     const float* rec = part + ((int64_t)m * Hq + h) * nchunk * kPart;
-    __shared__ float cw[kMaxChunks];           // chunk max, then its weight exp(m_c - M)
-    __shared__ float red[4];
-    __shared__ float dred[4];
-    __shared__ __align__(8) float2 nred[4][64];
-    const int lane = tid & 63, wave = tid >> 6;
+    __shared__ am::MergeLds lds;
     float r0, r1;
-    if (n <= 64) {
-        // one pass: thread (column pair lane, phase wave) loads the statistics
-        // and column sums of chunks wave, wave + 4, ... all at once
-        constexpr int kF = 16;
-        float2 st[kF], cs[kF];
-#pragma unroll
-        for (int i = 0; i < kF; ++i) {
-            const int c = wave + 4 * i;
-            st[i] = make_float2(-INFINITY, 0.0f);
-            cs[i] = make_float2(0.0f, 0.0f);
-            if (c < n) {
-                st[i] = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart);
-                cs[i] = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart + 4 + 2 * lane);
-            }
-        }
-        float gm = -INFINITY;
-#pragma unroll
-        for (int i = 0; i < kF; ++i) gm = fmaxf(gm, st[i].x);
-        if (lane == 0) red[wave] = gm;
-        __syncthreads();
-        gm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        float den = 0.0f;
-        float2 num = make_float2(0.0f, 0.0f);
-#pragma unroll
-        for (int i = 0; i < kF; ++i) {
-            if (wave + 4 * i < n) {
-                const float w = expf(st[i].x - gm);
-                den = fmaf(w, st[i].y, den);
-                num.x = fmaf(w, cs[i].x, num.x);
-                num.y = fmaf(w, cs[i].y, num.y);
-            }
-        }
-        nred[wave][lane] = num;
-        if (lane == 0) dred[wave] = den;
-        __syncthreads();
-        if (wave != 0) return;
-        den = (dred[0] + dred[1]) + (dred[2] + dred[3]);
-        num.x = (nred[0][lane].x + nred[1][lane].x) + (nred[2][lane].x + nred[3][lane].x);
-        num.y = (nred[0][lane].y + nred[1][lane].y) + (nred[2][lane].y + nred[3][lane].y);
-        r0 = num.x / den;
-        r1 = num.y / den;
-    } else {
-    constexpr int kPer = kMaxChunks / 256;
-    float mc[kPer], lc[kPer];
-    float gm = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int c = i * 256 + tid;
-        mc[i] = -INFINITY;
-        lc[i] = 0.0f;
-        if (c < n) {
-            const float2 st = *reinterpret_cast<const float2*>(rec + (int64_t)c * kPart);
-            mc[i] = st.x;
-            lc[i] = st.y;
-        }
-        gm = fmaxf(gm, mc[i]);
-    }
-    gm = mx::wave_reduce_dpp<true>(gm);
-    if (lane == 0) red[wave] = gm;
-    __syncthreads();
-    gm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float den = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kPer; ++i) {
-        const int c = i * 256 + tid;
-        if (c < n) {
-            const float w = expf(mc[i] - gm);
-            cw[c] = w;
-            den = fmaf(w, lc[i], den);
-        }
-    }
-    den = mx::wave_reduce_dpp<false>(den);
-    __syncthreads();                           // red[] reads above are done
-    if (lane == 0) red[wave] = den;
-    __syncthreads();                           // cw[] and red[] complete
-    den = (red[0] + red[1]) + (red[2] + red[3]);
-    // pass 2: thread = (column pair cp = lane, phase cq = wave)
-    float2 num = make_float2(0.0f, 0.0f);
-    const float* colp = rec + 4 + 2 * lane;
-#pragma unroll 16
-    for (int c = wave; c < n; c += 4) {
-        const float2 a = *reinterpret_cast<const float2*>(colp + (int64_t)c * kPart);
-        const float w = cw[c];
-        num.x = fmaf(w, a.x, num.x);
-        num.y = fmaf(w, a.y, num.y);
-    }
-    nred[wave][lane] = num;
-    __syncthreads();
-    if (wave != 0) return;
-    num.x = (nred[0][lane].x + nred[1][lane].x) + (nred[2][lane].x + nred[3][lane].x);
-    num.y = (nred[0][lane].y + nred[1][lane].y) + (nred[2][lane].y + nred[3][lane].y);
-    r0 = num.x / den;
-    r1 = num.y / den;
-    }
+    if (!am::merge_head(rec, n, lds, r0, r1)) return;
     if (o) *reinterpret_cast<float2*>(o + ((int64_t)m * Hq + h) * kD + 2 * lane) = make_float2(r0, r1);
     if (oq) {
-        // MXFP4 of bf16(o): a 32-block is 16 lanes; the quantizer's rule
-        const float v0 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r0));
-        const float v1 = mx::bf16_to_f32(mx::f32_to_bf16_rne(r1));
-        const float am = mx::row16_reduce<true>(fmaxf(__builtin_fabsf(v0), __builtin_fabsf(v1)));
-        const uint32_t code = mx::e8m0_code(am);
-        const float inv = mx::e8m0_inv_scale(code);
-        uint32_t byte = mx::e2m1_code(v0 * inv) | (mx::e2m1_code(v1 * inv) << 4);
-        byte |= (uint32_t)mx::dpp<mx::kDppQuadNext1>((int)byte) << 8;    // lane 4j: bytes of 4j..4j+3
-        byte |= (uint32_t)mx::dpp<mx::kDppQuadNext2>((int)byte) << 16;
+        uint32_t byte, code;
+        am::quant_head_row(r0, r1, byte, code);
         const int64_t rowq = (int64_t)m * (Hq * kD / 2) + h * (kD / 2);
         if ((lane & 3) == 0) *reinterpret_cast<uint32_t*>(oq + rowq + lane) = byte;
         if ((lane & 15) == 0) os[(int64_t)m * (Hq * kD / 32) + h * (kD / 32) + lane / 16] = (uint8_t)code;
@@ -542,9 +433,9 @@ namespace {
 template <bool FUSED>
 int launch_attn(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int32_t* dpos, float* sc, float* o,
                 uint8_t* oq, uint8_t* os, int M, int Hq, int Hkv, int D, int max_pos, void* workspace,
-                size_t workspace_bytes, const QkvIn& fz, hipStream_t st) {
+                size_t workspace_bytes, const QkvIn& fz, hipStream_t st, bool merge = true) {
     MXH_REQUIRE(kvk && kvv && dpos && workspace, "attn_decode: null pointer");   // sc may be null: no scores kept
-    MXH_REQUIRE(o || oq, "attn_decode: no output (o and oq both null)");
+    MXH_REQUIRE(o || oq || !merge, "attn_decode: no output (o and oq both null)");
     MXH_REQUIRE(!oq == !os, "attn_decode: oq and os go together");
     MXH_REQUIRE(D == kD, "attn_decode: head_dim D=%d (this build supports %d, as the reference's kernels)", D, kD);
     MXH_REQUIRE(M > 0 && M <= 65535 && Hkv > 0 && Hq > 0 && Hq % Hkv == 0, "attn_decode: M=%d Hq=%d Hkv=%d", M, Hq, Hkv);
@@ -587,7 +478,7 @@ int launch_attn(const void* q, const uint8_t* kvk, const uint8_t* kvv, const int
 #undef MXH_ATTN_G
 #undef MXH_ATTN
     const int rc = mxh::launch_status("attn_decode (partials)");
-    if (rc != MXFP4_OK) return rc;
+    if (rc != MXFP4_OK || !merge) return rc;
     hipLaunchKernelGGL(attn_final_kernel, dim3(Hq, M), dim3(256), 0, st, part, o, oq, os, dpos, Hq, max_pos, nchunk);
     return mxh::launch_status("attn_decode (merge)");
 }
@@ -635,4 +526,18 @@ extern "C" int mxfp4_kv_write(const void* k, const void* v, uint8_t* kvk, uint8_
                        static_cast<const uint16_t*>(k), static_cast<const uint16_t*>(v), kvk, kvv, dpos, M, (int)row,
                        max_pos);
     return mxh::launch_status("kv_write");
+}
+
+extern "C" int mxfp4_attn_decode_fused_partials(const float* qkv, const void* q_norm_w, const void* k_norm_w,
+                                                float eps, float theta, uint8_t* kvk, uint8_t* kvv,
+                                                const int32_t* dpos, int M, int Hq, int Hkv, int D, int max_pos,
+                                                int codec, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(qkv && q_norm_w && k_norm_w, "attn_decode_fused_partials: null pointer");
+    MXH_REQUIRE(codec == 0 || codec == 1, "attn_decode_fused_partials: codec %d (0 kv_write's, 1 torch float8_e4m3fn)",
+                codec);
+    MXH_REQUIRE(M > 0 && M <= kMaxFusedM, "attn_decode_fused_partials: M=%d (1..%d)", M, kMaxFusedM);
+    const QkvIn fz{qkv, static_cast<const uint16_t*>(q_norm_w), static_cast<const uint16_t*>(k_norm_w), eps, theta,
+                   codec, kvk, kvv};
+    return launch_attn<true>(nullptr, kvk, kvv, dpos, nullptr, nullptr, nullptr, nullptr, M, Hq, Hkv, D, max_pos,
+                             workspace, workspace_bytes, fz, mxh::as_stream(stream), false);
 }

@@ -65,6 +65,7 @@
 // operand of v_mfma_scale_f32_16x16x128_f8f6f4 (A = E4M3, B = E2M1), so one
 // MFMA yields all three partial products and y = D[0] + D[1] + D[2]; the other
 // 13 rows are zero and cost nothing in an HBM-bound kernel.
+#include "attn_merge.h"
 #include "decode_common.h"
 #include "mx_host.h"
 
@@ -80,11 +81,19 @@ constexpr int kMemoBOff = 2048;       // int32 launch count of down workgroup cb
 constexpr int kMemoROff = 2560;       // int32 launch count of router workgroup r (fused router): [16]
 constexpr int kMemoQOff = 3072;       // int32 launch count of q|k|v workgroup q (fused router tail): [128]
 constexpr int kLogOff = 4096;         // fused router: (logit, tag) 64-bit words, n_experts <= 256
+constexpr int kMemoMOff = 6144;       // int32 launch count of attention-merge workgroup h (front): [64]
+constexpr int kMemoOOff = 6400;       // int32 launch count of o_proj workgroup o (front): [128]
 constexpr int kHOff = 8192;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
-                                      // then (out[c], tag) 64-bit words, c < H, for the q|k|v tail
+                                      // then (out[c], tag) 64-bit words, c < H, for the q|k|v tail,
+                                      // then the front's words: kAttnWords per head of the attention
+                                      // output, and (o_proj[c], tag), c < H
 constexpr int kMaxRouterWg = 16;      // fused router: 16 logits per workgroup
 constexpr int kMaxQkvWg = 128;        // q|k|v tail: 64 rows per workgroup, up to 8192 rows
 constexpr int kMaxH = 2048;
+constexpr int kMaxHq = 32;            // front: query heads (o_proj K = 4096)
+constexpr int kMaxOWg = 128;          // front: o_proj workgroups, 16 rows each
+constexpr int kAttnWords = 17;        // front: per head, 16 words of 4 MXFP4 bytes + 1 of the 4 scale codes
+constexpr int kWordsAfterH = 2 * kMaxH + kMaxHq * kAttnWords;   // 64-bit words after the h buffers
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -122,6 +131,20 @@ struct LayerArgs {
     float* qkv_out;           // (Nq) fp32
     uint16_t* xn_out;         // optional (H) bf16 x_next
     int nq, Nq;               // tail workgroups (ceil(Nq / 64)) and rows
+    // attention merge + o_proj front (ROUTE_FUSED with nm > 0): the launch
+    // first merges the token's decode-attention chunk records (one workgroup
+    // per query head) and runs o_proj on the MXFP4 of the result; the o_proj
+    // output then reaches the other workgroups as (value, tag) words instead
+    // of through `oproj`
+    const float* apart;       // attention chunk records of the token: head h at + h*nchunk*kPart
+    const int32_t* dpos;      // the token's position
+    int nchunk, max_pos;
+    uint8_t* aq_out;          // optional (Hq*128/2) + (Hq*128/32) MXFP4 attention output
+    uint8_t* as_out;
+    const uint8_t* owp;       // (H, 2048) + (H, 128) MXFP4 o_proj weight (K = 4096)
+    const uint8_t* ows;
+    float* oproj_out;         // optional (H) fp32 o_proj output
+    int nm, no;               // merge workgroups (Hq = 32) and o_proj workgroups (H / 16)
     int n_experts;            // experts per layer (logits routing)
     int norm;                 // renormalise the top-E weights (logits routing)
     int32_t* ids_out;         // optional (E) ids / weights written by workgroup 0 (logits routing)
@@ -179,23 +202,86 @@ union Smem {
         uint8_t xs[64];
         float red[4][16];
     } r;
+    am::MergeLds m;                                // attention-merge workgroups (front)
+    struct {                                       // o_proj workgroups (front)
+        uint8_t aq[kMaxHq * 64];                   // the attention output's MXFP4 (K = 4096)
+        uint8_t as[kMaxHq * 4];
+        float red[8][16];                          // row sums of the eight K parts
+    } o;
 };
+
+// The (out[c], tag) words the down workgroups publish for the q|k|v tail.
+__device__ __forceinline__ uint64_t* out_words(const LayerArgs& a) {
+    return reinterpret_cast<uint64_t*>(a.ws + kHOff + (size_t)2 * a.bufwords * 4);
+}
+// The front's words: the attention output (kAttnWords per head), then o_proj's.
+__device__ __forceinline__ uint64_t* attn_words(const LayerArgs& a) { return out_words(a) + kMaxH; }
+__device__ __forceinline__ uint64_t* oproj_words(const LayerArgs& a) {
+    return attn_words(a) + kMaxHq * kAttnWords;
+}
+
+// o_proj output elements 8t .. 8t+7 of thread t: from `oproj`, or with the
+// front from this launch's o_proj words -- one probe word per wave (the first
+// column of the wave's last thread), then the thread's words until all carry
+// `tag`.  Returns false when the bounded wait expired (values then zero).
+__device__ __forceinline__ bool load_oproj(const LayerArgs& a, uint32_t tag, float (&of)[8]) {
+    const int k0 = 8 * (int)threadIdx.x, wave = threadIdx.x >> 6;
+    if (a.nm == 0) {
+        const float4 o0 = *reinterpret_cast<const float4*>(a.oproj + k0);
+        const float4 o1 = *reinterpret_cast<const float4*>(a.oproj + k0 + 4);
+        of[0] = o0.x; of[1] = o0.y; of[2] = o0.z; of[3] = o0.w;
+        of[4] = o1.x; of[5] = o1.y; of[6] = o1.z; of[7] = o1.w;
+        return true;
+    }
+    const uint64_t* words = oproj_words(a);
+    int spins = 0;
+    bool ok = true;
+    while (true) {
+        const uint64_t w0 = __hip_atomic_load(words + 8 * (64 * wave + 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane((uint32_t)(w0 >> 32)) == tag) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    while (ok) {
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint64_t w = __hip_atomic_load(words + k0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            of[i] = __uint_as_float((uint32_t)w);
+            pending |= (uint32_t)(w >> 32) != tag;
+        }
+        if (!pending) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");
+    }
+    if (!ok) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) of[i] = 0.0f;
+    }
+    return ok;
+}
 
 // The post-attention residual and RMSNorm of one row for the fused router,
 // thread t holding elements 8t .. 8t+7 (H = 2048, 256 threads): v = bf16(x +
 // bf16(o)), y = bf16(bf16(v * rstd) * w) -- the arithmetic of
 // mxfp4_rmsnorm_quant / mxfp4_rmsnorm_lin_pq (runtime/model_runner.py:20-25),
 // including its order of the sum of squares, so y equals theirs bit for bit.
-// Every thread of the workgroup must call it (one barrier).
-__device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, float (&v)[8], float (&y)[8]) {
+// of: the thread's o_proj elements (load_oproj).  Every thread of the
+// workgroup must call it (one barrier).
+__device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, const float (&of)[8], float (&v)[8],
+                                               float (&y)[8]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int k0 = 8 * tid;
     const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
-    const float4 o0 = *reinterpret_cast<const float4*>(a.oproj + k0);
-    const float4 o1 = *reinterpret_cast<const float4*>(a.oproj + k0 + 4);
     const uint4 wq4 = *reinterpret_cast<const uint4*>(a.nw + k0);
     const uint32_t xw[4] = {q.x, q.y, q.z, q.w};
-    const float of[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -271,8 +357,9 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
 #pragma unroll
     for (int i = 0; i < 4; ++i) wq[i] = *reinterpret_cast<const uint4*>(wr + 16 * i);
     const uint32_t wsc = *reinterpret_cast<const uint32_t*>(a.rws + (int64_t)row * 64 + blk0);
-    float v[8], y[8];
-    fused_norm_row(a, nred, v, y);
+    float of[8], v[8], y[8];
+    if (!load_oproj(a, (uint32_t)(launch + 1), of)) set_error(a);
+    fused_norm_row(a, nred, of, v, y);
     // MXFP4 of y (bf16-exact values): block tid / 4, the block's four threads
     float am = 0.0f;
 #pragma unroll
@@ -326,9 +413,150 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
     }
 }
 
-// The (out[c], tag) words the down workgroups publish for the q|k|v tail.
-__device__ __forceinline__ uint64_t* out_words(const LayerArgs& a) {
-    return reinterpret_cast<uint64_t*>(a.ws + kHOff + (size_t)2 * a.bufwords * 4);
+// Attention-merge workgroup h (front): merges head h's chunk records of the
+// token with attn_final_kernel's arithmetic (am::merge_head) and publishes
+// the MXFP4 of bf16(o) as kAttnWords (value, tag) words: word j < 16 holds
+// the packed bytes 4j .. 4j+3 of the head's 64, word 16 its four block
+// codes.  A position outside [0, max_pos) publishes zeros (attn_final_kernel
+// writes nothing there).
+__device__ __forceinline__ void merge_wg(const LayerArgs& a, Smem& sm, int h) {
+    const int lane = threadIdx.x & 63;
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoMOff) + h;
+    const int launch = *memo;
+    const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+    const int pos = *a.dpos;
+    uint32_t bytes = 0, code = 127;
+    if (pos >= 0 && pos < a.max_pos) {
+        float r0, r1;
+        if (!am::merge_head(a.apart + (int64_t)h * a.nchunk * am::kPart, pos / am::kChunk + 1, sm.m, r0, r1))
+            return;   // waves 1..3
+        am::quant_head_row(r0, r1, bytes, code);
+    } else if (threadIdx.x >= 64) {
+        return;
+    }
+    const uint64_t tag = (uint64_t)(uint32_t)(launch + 1) << 32;
+    uint64_t* w = attn_words(a) + h * kAttnWords;
+    const bool cfg_ok = cfg == a.cfg;
+    const uint32_t codes = (uint32_t)__builtin_amdgcn_readlane((int)code, 0) |
+                           ((uint32_t)__builtin_amdgcn_readlane((int)code, 16) << 8) |
+                           ((uint32_t)__builtin_amdgcn_readlane((int)code, 32) << 16) |
+                           ((uint32_t)__builtin_amdgcn_readlane((int)code, 48) << 24);
+    if (cfg_ok) {
+        if ((lane & 3) == 0) __hip_atomic_store(w + (lane >> 2), (uint64_t)bytes | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) __hip_atomic_store(w + 16, (uint64_t)codes | tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (a.aq_out) {
+        if ((lane & 3) == 0) *reinterpret_cast<uint32_t*>(a.aq_out + h * 64 + lane) = bytes;
+        if ((lane & 15) == 0) a.as_out[h * 4 + lane / 16] = (uint8_t)code;
+    }
+    if (lane == 0) {
+        *memo = launch + 1;
+        if (!cfg_ok) set_error(a);
+    }
+}
+
+// o_proj workgroup oi (front): rows 16oi .. 16oi+15 of o_proj (K = 4096) on
+// this launch's attention output, with the arithmetic mxfp4_lin_pq uses for
+// one row at this shape (lin_small_kernel<1, 8>): K in eight parts of four
+// MFMA steps (block 16p + 4s + g at step s of part p), two parts per wave
+// here, the part sums added in part order -- so the rows equal lin_pq's bit
+// for bit.  Published as (value, tag) words, and written to oproj_out.
+__device__ __forceinline__ void oproj_wg(const LayerArgs& a, Smem& sm, int oi) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoOOff) + oi;
+    const int launch = *memo;
+    const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
+    constexpr int kRowB = kMaxHq * 64, kRowS = kMaxHq * 4;   // bytes and scale bytes of a weight row
+    const int row = 16 * oi + r;
+    const uint8_t* wr = a.owp + (int64_t)row * kRowB + g * 16;
+    uint4 wq[2][4], sc4[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int p = 2 * wave + q;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) wq[q][s] = *reinterpret_cast<const uint4*>(wr + (16 * p + 4 * s) * 16);
+        sc4[q] = *reinterpret_cast<const uint4*>(a.ows + (int64_t)row * kRowS + 16 * p);
+    }
+    // the attention output words: thread t takes words t, t + 256, t + 512;
+    // first one probe word per wave (head 31's codes, published last)
+    const uint64_t* words = attn_words(a);
+    constexpr int kW = kMaxHq * kAttnWords;
+    const uint32_t tag = (uint32_t)(launch + 1);
+    bool ok = cfg == a.cfg;
+    int spins = 0;
+    while (ok) {
+        const uint64_t w0 = __hip_atomic_load(words + kW - 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_readfirstlane((uint32_t)(w0 >> 32)) == tag) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    uint64_t wv[3];
+    while (ok) {
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int idx = min(tid + 256 * i, kW - 1);
+            wv[i] = __hip_atomic_load(words + idx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            pending |= (uint32_t)(wv[i] >> 32) != tag;
+        }
+        if (!pending) break;
+        if (++spins >= kSpinLimit) {
+            ok = false;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+        asm volatile("" ::: "memory");
+    }
+    if (__syncthreads_or(!ok)) {
+        if (tid == 0) {
+            set_error(a);
+            *memo = launch + 1;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 3; ++i) {
+        const int idx = tid + 256 * i;
+        if (idx < kW) {
+            const int h = idx / kAttnWords, j = idx - h * kAttnWords;
+            uint8_t* dst = j < 16 ? sm.o.aq + h * 64 + 4 * j : sm.o.as + h * 4;
+            *reinterpret_cast<uint32_t*>(dst) = (uint32_t)wv[i];
+        }
+    }
+    __syncthreads();
+    mx::v4f acc[2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+        const int p = 2 * wave + q;
+        acc[q] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
+        const uint32_t sw[4] = {sc4[q].x, sc4[q].y, sc4[q].z, sc4[q].w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int c = 16 * p + 4 * s + g;
+            const uint4 aq = *reinterpret_cast<const uint4*>(sm.o.aq + c * 16);
+            acc[q] = mx::mfma16_fp4(aq, wq[q][s], acc[q], (uint32_t)sm.o.as[c], (sw[s] >> (8 * g)) & 0xFFu);
+        }
+    }
+    mx::pin(acc[0]);   // the whole MFMA chain before the lane < 16 branch
+    mx::pin(acc[1]);
+    if (lane < 16) {
+        sm.o.red[2 * wave][lane] = acc[0][0];
+        sm.o.red[2 * wave + 1][lane] = acc[1][0];
+    }
+    __syncthreads();
+    if (tid < 16) {
+        float t = sm.o.red[0][tid];
+#pragma unroll
+        for (int p = 1; p < 8; ++p) t += sm.o.red[p][tid];
+        __hip_atomic_store(oproj_words(a) + 16 * oi + tid, (uint64_t)__float_as_uint(t) | ((uint64_t)tag << 32),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (a.oproj_out) a.oproj_out[16 * oi + tid] = t;
+    }
+    if (tid == 0) *memo = launch + 1;
 }
 
 // q|k|v tail workgroup qi (fused router, nq > 0): rows 64qi .. 64qi+63 of
@@ -361,17 +589,15 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
     for (int p = 0; p < 4; ++p) sc4[p] = *reinterpret_cast<const uint4*>(a.qws + (int64_t)row * (kMaxH / 32) + 16 * p);
     const int k0 = 8 * tid;
     const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
-    const float4 o0 = *reinterpret_cast<const float4*>(a.oproj + k0);
-    const float4 o1 = *reinterpret_cast<const float4*>(a.oproj + k0 + 4);
     const uint4 wn = *reinterpret_cast<const uint4*>(a.qnw + k0);
     // this launch's MoE output of columns k0 .. k0+7
     const uint64_t* yw = out_words(a) + k0;
     const uint32_t tag = (uint32_t)(launch + 1);
-    float yo[8];
+    float of[8], yo[8];
     // one probe word per wave first (the first column of the wave's last
     // thread; one request per round while the weights stream), then every
     // thread's words until all carry the tag
-    bool ok = cfg == a.cfg;
+    bool ok = cfg == a.cfg && load_oproj(a, tag, of);
     int spins = 0;
     while (ok) {
         const uint64_t w0 = __hip_atomic_load(out_words(a) + 8 * (64 * wave + 63), __ATOMIC_RELAXED,
@@ -407,7 +633,6 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
         return;
     }
     const uint32_t xw[4] = {q.x, q.y, q.z, q.w};
-    const float of[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
     float v[8];
     float ss = 0.0f;
 #pragma unroll
@@ -491,13 +716,23 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int nblk_mi = a.Mi >> 5;
     const int nA = a.E * nblk_mi;
     constexpr bool kLogitRoute = ROUTE == ROUTE_LOGITS || ROUTE == ROUTE_FUSED;
-    // fused router: workgroups [0, nr) compute the logits; the gate/up and
-    // down workgroups follow them
-    const int bid = (int)blockIdx.x - (ROUTE == ROUTE_FUSED ? a.nr : 0);
+    // fused router: workgroups [0, nm) merge the attention heads and [nm,
+    // nm + no) run o_proj (the front, nm = no = 0 without it), the next nr
+    // compute the router logits; the gate/up and down workgroups follow them
+    const int nfront = ROUTE == ROUTE_FUSED ? a.nm + a.no : 0;
+    const int bid = (int)blockIdx.x - (ROUTE == ROUTE_FUSED ? nfront + a.nr : 0);
     __shared__ float nred[4];
     if constexpr (ROUTE == ROUTE_FUSED) {
+        if ((int)blockIdx.x < a.nm) {
+            merge_wg(a, sm, (int)blockIdx.x);
+            return;
+        }
+        if ((int)blockIdx.x < nfront) {
+            oproj_wg(a, sm, (int)blockIdx.x - a.nm);
+            return;
+        }
         if (bid < 0) {
-            router_wg(a, sm, nred, (int)blockIdx.x);
+            router_wg(a, sm, nred, (int)blockIdx.x - nfront);
             return;
         }
         // q|k|v tail workgroups follow the down workgroups
@@ -517,10 +752,14 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     const int k0 = threadIdx.x * 8;
     uint4 xq = make_uint4(0, 0, 0, 0);
     float yf[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    // fused router: this launch's tag is the workgroup's own launch count + 1
+    const int* memo0 = reinterpret_cast<const int*>(a.ws) +
+                       (bid < nA ? kMemoAOff / 4 + (bid % a.E) * 32 + bid / a.E : kMemoBOff / 4 + (bid - nA));
     if constexpr (ROUTE == ROUTE_FUSED) {
         if (bid < nA) {
-            float vf[8];
-            fused_norm_row(a, nred, vf, yf);
+            float of[8], vf[8];
+            if (!load_oproj(a, (uint32_t)(*memo0 + 1), of)) set_error(a);
+            fused_norm_row(a, nred, of, vf, yf);
         }
     } else {
         if (bid < nA && k0 < a.H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
@@ -529,9 +768,6 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         mx::wave_topk<kRouteNpl>(a.logits, a.n_experts, a.E, a.norm, rid, rw);
     }
     if constexpr (ROUTE == ROUTE_FUSED) {
-        // this launch's tag: the workgroup's own launch count + 1
-        const int* memo0 = reinterpret_cast<const int*>(a.ws) +
-                           (bid < nA ? kMemoAOff / 4 + (bid % a.E) * 32 + bid / a.E : kMemoBOff / 4 + (bid - nA));
         float lv[kRouteNpl];
         if (!poll_logits<kRouteNpl>(a, (uint32_t)(*memo0 + 1), lv)) set_error(a);
         mx::wave_topk_regs<kRouteNpl>(lv, a.n_experts, a.E, a.norm, rid, rw);
@@ -674,10 +910,17 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             // likewise the q|k|v tail slots this launch has no workgroup for
             if (bid == 0) {
                 const int nq = ROUTE == ROUTE_FUSED ? a.nq : 0;
+                const int nm = ROUTE == ROUTE_FUSED ? a.nm : 0;
+                const int no = ROUTE == ROUTE_FUSED ? a.no : 0;
                 int* mq = reinterpret_cast<int*>(a.ws + kMemoQOff);
 #pragma unroll
                 for (int k = lane; k < kMaxQkvWg; k += 64)
                     if (k >= nq) mq[k] += 1;
+                if (lane >= nm) reinterpret_cast<int*>(a.ws + kMemoMOff)[lane] += 1;
+                int* mo = reinterpret_cast<int*>(a.ws + kMemoOOff);
+#pragma unroll
+                for (int k = lane; k < kMaxOWg; k += 64)
+                    if (k >= no) mo[k] += 1;
             }
         }
         return;
@@ -895,7 +1138,7 @@ __global__ void reset_workspace_kernel(uint32_t* ws, int cfg, int hwords) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < kHOff / 4) ws[i] = (i == kCfgOff / 4) ? (uint32_t)cfg : 0u;
     if (i < hwords) ws[kHOff / 4 + i] = kEmpty;
-    if (i < 2 * kMaxH) ws[kHOff / 4 + hwords + i] = 0u;   // output words: tag 0, which no launch uses
+    if (i < 2 * kWordsAfterH) ws[kHOff / 4 + hwords + i] = 0u;   // tagged words: tag 0, which no launch uses
 }
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -907,7 +1150,7 @@ int buf_words(int E, int Mi) { return (int)(align256((size_t)E * (Mi / 32) * kRe
 
 extern "C" size_t mxfp4_decode_layer_workspace_size(int E, int Mi) {
     if (E <= 0 || Mi <= 0) return 0;
-    return kHOff + (size_t)2 * buf_words(E, Mi) * 4 + (size_t)kMaxH * 8;
+    return kHOff + (size_t)2 * buf_words(E, Mi) * 4 + (size_t)kWordsAfterH * 8;
 }
 
 extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, void* stream) {
@@ -915,7 +1158,7 @@ extern "C" int mxfp4_decode_layer_reset(void* workspace, int E, int H, int Mi, v
     MXH_REQUIRE(E >= 1 && E <= kMaxE && Mi >= 32 && Mi <= 1024 && Mi % 32 == 0 && H >= 512 && H <= 2048 && H % 512 == 0,
                 "decode_layer_reset: E=%d H=%d Mi=%d out of range", E, H, Mi);
     const int hw = 2 * buf_words(E, Mi);
-    const int n = max(max(hw, kHOff / 4), 2 * kMaxH);
+    const int n = max(max(hw, kHOff / 4), 2 * kWordsAfterH);
     hipLaunchKernelGGL(reset_workspace_kernel, dim3((n + 255) / 256), dim3(256), 0, mxh::as_stream(stream),
                        static_cast<uint32_t*>(workspace), layer_cfg(E, H, Mi), hw);
     return mxh::launch_status("decode_layer_reset");
@@ -975,8 +1218,9 @@ int launch_layer(const LayerArgs& a, hipStream_t st) {
     const int nB = a.H / 16;
     const int nR = ROUTE == ROUTE_FUSED ? a.nr : 0;
     const int nQ = ROUTE == ROUTE_FUSED ? a.nq : 0;
+    const int nF = ROUTE == ROUTE_FUSED ? a.nm + a.no : 0;
     const int steps = (a.Mi / 32 + 3) / 4;
-    const dim3 grid(nR + nA + nB + nQ);
+    const dim3 grid(nF + nR + nA + nB + nQ);
     if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), grid, dim3(256), 0, st, a);
     return mxh::launch_status("moe_decode_layer");
@@ -1108,5 +1352,60 @@ extern "C" int mxfp4_moe_decode_layer_fused_router_qkv(
     a.xn_out = static_cast<uint16_t*>(x_next_out);
     a.Nq = Nq;
     a.nq = (Nq + 63) / 64;
+    return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
+}
+
+extern "C" int mxfp4_decode_layer_post_attn(
+    const void* attn_workspace, size_t attn_workspace_bytes, const int32_t* dpos, int Hq, int max_pos, uint8_t* aq_out, uint8_t* as_out,
+    const uint8_t* o_wp, const uint8_t* o_ws, float* oproj_out, const void* x, const void* norm_w, float eps,
+    const uint8_t* router_wp, const uint8_t* router_ws, int norm, void* x_out, void* y_out, float* logits_out,
+    int32_t* ids_out, float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
+    const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
+    const void* qkv_norm_w, const uint8_t* qkv_wp, const uint8_t* qkv_ws, int Nq, float* qkv_out, void* x_next_out,
+    float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    MXH_REQUIRE(attn_workspace && dpos && o_wp && o_ws && oproj_out, "decode_layer_post_attn: null pointer");
+    MXH_REQUIRE(Hq == kMaxHq, "decode_layer_post_attn: Hq=%d (the o_proj front is built for %d heads of 128)", Hq,
+                kMaxHq);
+    MXH_REQUIRE(max_pos > 0 && max_pos <= am::kChunk * am::kMaxChunks, "decode_layer_post_attn: max_pos=%d", max_pos);
+    MXH_REQUIRE(!aq_out == !as_out, "decode_layer_post_attn: aq_out and as_out go together");
+    LayerArgs a;
+    int rc = fused_router_args(a, x, oproj_out, norm_w, eps, router_wp, router_ws, norm, x_out, y_out, logits_out,
+                               ids_out, w_out, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, E, H, Mi,
+                               out, workspace, workspace_bytes);
+    if (rc != MXFP4_OK) return rc;
+    MXH_REQUIRE(H / 16 <= kMaxOWg, "decode_layer_post_attn: H=%d", H);
+    MXH_REQUIRE(attn_workspace_bytes >= mxfp4_attn_decode_workspace_size(1, Hq, max_pos),
+                "decode_layer_post_attn: attention workspace smaller than mxfp4_attn_decode_workspace_size(1, %d, %d)",
+                Hq, max_pos);
+    MXH_REQUIRE(((uintptr_t)attn_workspace & 15) == 0 && ((uintptr_t)o_wp & 15) == 0 && ((uintptr_t)o_ws & 15) == 0 &&
+                    ((uintptr_t)aq_out & 3) == 0,
+                "decode_layer_post_attn: attn_workspace, o_wp, o_ws must be 16-byte aligned, aq_out 4-byte");
+    if (qkv_wp) {
+        MXH_REQUIRE(qkv_norm_w && qkv_ws && qkv_out, "decode_layer_post_attn: null q|k|v pointer");
+        MXH_REQUIRE(Nq >= 1 && Nq <= 64 * kMaxQkvWg, "decode_layer_post_attn: Nq=%d (1..%d)", Nq, 64 * kMaxQkvWg);
+        MXH_REQUIRE(((uintptr_t)qkv_norm_w & 15) == 0 && ((uintptr_t)qkv_wp & 15) == 0 &&
+                        ((uintptr_t)qkv_ws & 15) == 0 && ((uintptr_t)x_next_out & 15) == 0,
+                    "decode_layer_post_attn: qkv_norm_w, qkv_wp, qkv_ws, x_next_out must be 16-byte aligned");
+        MXH_REQUIRE(!x_next_out || (x_next_out != x && x_next_out != x_out),
+                    "decode_layer_post_attn: x_next_out must not alias x or x_out");
+        a.qnw = static_cast<const uint16_t*>(qkv_norm_w);
+        a.qwp = qkv_wp;
+        a.qws = qkv_ws;
+        a.qkv_out = qkv_out;
+        a.xn_out = static_cast<uint16_t*>(x_next_out);
+        a.Nq = Nq;
+        a.nq = (Nq + 63) / 64;
+    }
+    a.apart = static_cast<const float*>(attn_workspace);
+    a.dpos = dpos;
+    a.max_pos = max_pos;
+    a.nchunk = (max_pos + am::kChunk - 1) / am::kChunk;
+    a.aq_out = aq_out;
+    a.as_out = as_out;
+    a.owp = o_wp;
+    a.ows = o_ws;
+    a.oproj_out = oproj_out;
+    a.nm = Hq;
+    a.no = H / 16;
     return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
 }

@@ -32,7 +32,7 @@ from dataclasses import dataclass, field
 import torch
 
 from . import _lib
-from .moe_layer import (FusedRouterLayerCall, RoutedLayerCall, StackedExperts, layer_status,
+from .moe_layer import (FusedRouterLayerCall, PostAttnLayerCall, RoutedLayerCall, StackedExperts, layer_status,
                         workspace as layer_workspace)
 
 
@@ -158,7 +158,8 @@ class DecodeStep:
     stay on the device: each step reads them and leaves the greedy next
     tokens and dpos + M for the next step."""
 
-    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True, qkv_tail=True):
+    def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True, qkv_tail=True,
+                 attn_front=True):
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
         self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
@@ -171,6 +172,10 @@ class DecodeStep:
         # q|k|v projection also run in the MoE launch
         # (mxfp4_moe_decode_layer_fused_router_qkv): another launch per layer fewer
         self.qkv_tail = self.fused_router and bool(qkv_tail)
+        # with the q|k|v tail, the attention merge and o_proj also run in the
+        # MoE launch (mxfp4_decode_layer_post_attn; 32 heads of 128): two
+        # launches per layer in all
+        self.attn_front = self.qkv_tail and bool(attn_front) and cfg.n_heads == 32 and cfg.head_dim == 128
         self._fr_calls = {}
         c = cfg
         if c.head_dim != 128:
@@ -283,16 +288,25 @@ class DecodeStep:
     def _layers_qkv_tail(self, on_layer, s):
         """The layers at M = 1 with the q|k|v tail: per layer the attention,
         o_proj and one MoE launch that also runs the router and the next
-        layer's input norm + q|k|v.  The residual stream rotates through
-        three buffers (a launch's x, x_out and x_next are distinct).
-        Returns (x_out of the last layer, a free buffer)."""
+        layer's input norm + q|k|v; with attn_front, the attention's chunk
+        pass and one launch for the rest (merge, o_proj, router, MoE, next
+        q|k|v).  The residual stream rotates through three buffers (a
+        launch's x, x_out and x_next are distinct).  Returns (x_out of the
+        last layer, a free buffer)."""
         c, b, m = self.cfg, self.b, self.model
         xs = (b.x, b.x2, b.x3)
         L = len(m.layers)
         self._norm_lin(b.x, None, m.layers[0].in_norm, None, False, m.layers[0].qkv, self.qkv_buf(0), s)
         cur = 0                      # xs[cur]: the layer's input residual stream
         for l, lw in enumerate(m.layers):
-            self._attn_oproj(l, lw, self.qkv_buf(l), s)
+            if self.attn_front:
+                self._ck(self.lib.mxfp4_attn_decode_fused_partials(
+                    self.qkv_buf(l).data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), c.rms_eps, c.rope_theta,
+                    b.kvk[l].data_ptr(), b.kvv[l].data_ptr(), b.dpos.data_ptr(), 1, c.n_heads, c.n_kv_heads,
+                    c.head_dim, self.max_pos, self.kv_codec, b.attn_ws.data_ptr(), b.attn_ws.numel(), s),
+                    "attn_decode_fused_partials")
+            else:
+                self._attn_oproj(l, lw, self.qkv_buf(l), s)
             xo, xn = (cur + 1) % 3, (cur + 2) % 3
             call = self._fr_calls.get(("tail", l))
             if call is None:
@@ -300,9 +314,15 @@ class DecodeStep:
                 if l + 1 < L:
                     nl = m.layers[l + 1]
                     nxt = (nl.in_norm, nl.qkv.wp, nl.qkv.ws, self.qkv_buf(l + 1)[0], xs[xn][0])
-                call = FusedRouterLayerCall(xs[cur][0], b.oproj[0], lw.post_norm, c.rms_eps, lw.gate.wp, lw.gate.ws,
-                                            c.top_k, lw.experts, b.moe[0], self.layer_ws, x_out=xs[xo][0],
-                                            y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt)
+                if self.attn_front:
+                    call = PostAttnLayerCall(b.attn_ws, b.dpos, self.max_pos, lw.o.wp, lw.o.ws, b.oproj[0],
+                                             xs[cur][0], lw.post_norm, c.rms_eps, lw.gate.wp, lw.gate.ws, c.top_k,
+                                             lw.experts, b.moe[0], self.layer_ws, aq_out=b.aq[0], as_out=b.as_[0],
+                                             x_out=xs[xo][0], y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt)
+                else:
+                    call = FusedRouterLayerCall(xs[cur][0], b.oproj[0], lw.post_norm, c.rms_eps, lw.gate.wp,
+                                                lw.gate.ws, c.top_k, lw.experts, b.moe[0], self.layer_ws,
+                                                x_out=xs[xo][0], y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt)
                 self._fr_calls[("tail", l)] = call
             call(s)
             if on_layer is not None:

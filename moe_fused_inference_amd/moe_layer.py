@@ -180,6 +180,53 @@ class FusedRouterLayerCall:
         _lib.check(self.fn(*self.args, s), self.what)
 
 
+class PostAttnLayerCall:
+    """Pre-bound arguments of mxfp4_decode_layer_post_attn: the merge of the
+    token's attention chunk records (attn_ws, as mxfp4_attn_decode_fused_partials
+    left it for max_pos positions, dpos the position on the device), o_proj
+    (o_wp uint8 (H, 2048), o_ws uint8 (H, 128): 32 heads of 128) into
+    oproj_out fp32 (H,), then the fused-router MoE launch of
+    FusedRouterLayerCall on (x, oproj_out), with the same optional outputs
+    and next_qkv tail; aq_out / as_out optionally receive the attention
+    output's MXFP4 row."""
+
+    def __init__(self, attn_ws, dpos, max_pos, o_wp, o_ws, oproj_out, x, norm_w, eps, router_wp, router_ws, E,
+                 experts, out, ws, norm=True, aq_out=None, as_out=None, x_out=None, y_out=None, logits_out=None,
+                 ids_out=None, w_out=None, next_qkv=None):
+        self.lib = _lib.load()
+        n, H = experts.n_experts, experts.hidden
+        hq = 32
+        if tuple(o_wp.shape) != (H, hq * 64) or tuple(o_ws.shape) != (H, hq * 4):
+            raise RuntimeError(f"o_proj weights must be ({H}, {hq * 64}) + ({H}, {hq * 4})")
+        if (aq_out is None) != (as_out is None):
+            raise RuntimeError("give aq_out and as_out both or neither")
+        if oproj_out.dtype != torch.float32 or oproj_out.numel() != H:
+            raise RuntimeError("oproj_out must be float32 (H,)")
+        ptr = (lambda t: t.data_ptr() if t is not None else None)
+        if next_qkv is None:
+            qkv = (None, None, None, 0, None, None)
+        else:
+            qnw, qwp, qws, qkv_out = next_qkv[:4]
+            x_next = next_qkv[4] if len(next_qkv) > 4 else None
+            nq = qwp.shape[0]
+            if tuple(qwp.shape) != (nq, H // 2) or tuple(qws.shape) != (nq, H // 32) or qkv_out.numel() != nq:
+                raise RuntimeError("q|k|v weights must be (Nq, H/2) + (Nq, H/32), qkv_out (Nq,)")
+            qkv = (qnw.data_ptr(), qwp.data_ptr(), qws.data_ptr(), nq, qkv_out.data_ptr(), ptr(x_next))
+        self.keep = (attn_ws, dpos, o_wp, o_ws, oproj_out, x, norm_w, router_wp, router_ws, experts, out, ws, aq_out,
+                     as_out, x_out, y_out, logits_out, ids_out, w_out, next_qkv)
+        self.args = ((attn_ws.data_ptr(), attn_ws.numel() * attn_ws.element_size(), dpos.data_ptr(), hq,
+                      int(max_pos), ptr(aq_out), ptr(as_out), o_wp.data_ptr(), o_ws.data_ptr(),
+                      oproj_out.data_ptr(), x.data_ptr(), norm_w.data_ptr(), float(eps), router_wp.data_ptr(),
+                      router_ws.data_ptr(), int(bool(norm)), ptr(x_out), ptr(y_out), ptr(logits_out), ptr(ids_out),
+                      ptr(w_out), experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(), experts.up_wp.data_ptr(),
+                      experts.up_ws.data_ptr(), experts.down_wp.data_ptr(), experts.down_ws.data_ptr(), n, int(E),
+                      H, experts.inter) + qkv + (out.data_ptr(), ws.data_ptr(), ws.numel()))
+
+    def __call__(self, stream=None):
+        s = torch.cuda.current_stream().cuda_stream if stream is None else stream
+        _lib.check(self.lib.mxfp4_decode_layer_post_attn(*self.args, s), "decode_layer_post_attn")
+
+
 def decode_layer_routed(x, logits, E, experts, norm=True, out=None, resid=None, ws=None, want_routing=False):
     """One token through the layer, routing included: softmax / top-E /
     renormalise of the fp32 router logits (n_experts,) computed in the same

@@ -270,3 +270,103 @@ def test_fused_router_qkv_argument_checks(dext):
     assert lib.mxfp4_moe_decode_layer_fused_router_qkv(*args, p, p, p, 8193, p, None, *tail) == -1
     assert lib.mxfp4_moe_decode_layer_fused_router_qkv(*args, None, p, p, 64, p, None, *tail) == -1
     assert "null" in lib.mxfp4_last_error().decode()
+
+
+@pytest.mark.parametrize("max_pos,pos", [(512, 300), (8192, 5000)])
+def test_post_attn_matches_separate_calls(dext, max_pos, pos):
+    """mxfp4_decode_layer_post_attn after mxfp4_attn_decode_fused_partials
+    against the separate launches it replaces -- mxfp4_attn_decode_fused
+    (chunk records + merge to MXFP4), mxfp4_lin_pq (o_proj) and the fused
+    router + MoE + q|k|v tail launch -- bit for bit: the attention's MXFP4
+    row, o_proj, residual, routing, MoE output, next q|k|v, x_next and the KV
+    rows written.  Context 5000 takes the merge's two-pass path (more than
+    64 chunks).  Three positions in a row on shared workspaces, with a plain
+    fused-layer launch in between."""
+    lib = _lib.load()
+    Hq, Hkv, D, n_exp, nq = 32, 4, 128, 128, 5120
+    experts = make_stack(dext, n_exp, H, MI, seed=16000 + pos)
+    rwp, rws = rand_weight(dext, n_exp, H, seed=16100, std=0.05)
+    owp, ows = rand_weight(dext, H, Hq * D, seed=16200, std=0.03)
+    qwp, qws = rand_weight(dext, nq, H, seed=16300, std=0.05)
+    g = torch.Generator(device=DEV)
+    g.manual_seed(pos)
+    qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    qnw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+    r = torch.randint(0, 256, (max_pos, Hkv, D), generator=g, device=DEV, dtype=torch.int32)
+    cache0 = ((r & 0x80) | (r & 0x3F)).to(torch.uint8)     # |v| < 2, no NaN code
+    kv = {k: (cache0.clone(), cache0.flip(0).contiguous()) for k in ("sep", "fused")}
+    nb = lib.mxfp4_attn_decode_workspace_size(1, Hq, max_pos)
+    aws = {k: torch.empty((nb + 15) // 16 * 16, dtype=torch.uint8, device=DEV) for k in kv}
+    lws = {k: moe_layer.workspace(E, MI, H) for k in kv}
+    dpos = torch.zeros(1, dtype=torch.int32, device=DEV)
+    s = torch.cuda.current_stream().cuda_stream
+
+    def outs():
+        return dict(aq=torch.empty(Hq * D // 2, dtype=torch.uint8, device=DEV),
+                    as_=torch.empty(Hq * D // 32, dtype=torch.uint8, device=DEV),
+                    oproj=torch.empty(H, dtype=torch.float32, device=DEV),
+                    out=torch.empty(H, dtype=torch.float32, device=DEV),
+                    x_out=torch.empty(H, dtype=torch.bfloat16, device=DEV),
+                    ids=torch.empty(E, dtype=torch.int32, device=DEV),
+                    w=torch.empty(E, dtype=torch.float32, device=DEV),
+                    qkv=torch.empty(nq, dtype=torch.float32, device=DEV),
+                    x_next=torch.empty(H, dtype=torch.bfloat16, device=DEV))
+
+    for it, p in enumerate((pos, pos + 1, pos + 2)):
+        dpos.fill_(p)
+        qkv_in = (torch.randn(Hq * D + 2 * Hkv * D, generator=g, device=DEV) * 2.0).contiguous()
+        xa = torch.randn(H, generator=g, device=DEV).bfloat16()
+        nw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
+        res = {}
+        for mode in ("sep", "fused"):
+            o = outs()
+            kvk, kvv = kv[mode]
+            common = (qkv_in.data_ptr(), qn.data_ptr(), kn.data_ptr(), EPS, 1e6, kvk.data_ptr(), kvv.data_ptr(),
+                      dpos.data_ptr())
+            if mode == "sep":
+                _lib.check(lib.mxfp4_attn_decode_fused(*common, None, None, o["aq"].data_ptr(), o["as_"].data_ptr(), 1,
+                                                       Hq, Hkv, D, max_pos, 0, aws[mode].data_ptr(), aws[mode].numel(),
+                                                       s), "attn_decode_fused")
+                _lib.check(lib.mxfp4_lin_pq(o["aq"].data_ptr(), o["as_"].data_ptr(), owp.data_ptr(), ows.data_ptr(),
+                                            o["oproj"].data_ptr(), 1, H, Hq * D, Hq * D, s), "lin_pq")
+                moe_layer.FusedRouterLayerCall(xa, o["oproj"], nw, EPS, rwp, rws, E, experts, o["out"], lws[mode],
+                                               x_out=o["x_out"], ids_out=o["ids"], w_out=o["w"],
+                                               next_qkv=(qnw, qwp, qws, o["qkv"], o["x_next"]))()
+            else:
+                _lib.check(lib.mxfp4_attn_decode_fused_partials(*common, 1, Hq, Hkv, D, max_pos, 0,
+                                                                aws[mode].data_ptr(), aws[mode].numel(), s),
+                           "attn_decode_fused_partials")
+                moe_layer.PostAttnLayerCall(aws[mode], dpos, max_pos, owp, ows, o["oproj"], xa, nw, EPS, rwp, rws, E,
+                                            experts, o["out"], lws[mode], aq_out=o["aq"], as_out=o["as_"],
+                                            x_out=o["x_out"], ids_out=o["ids"], w_out=o["w"],
+                                            next_qkv=(qnw, qwp, qws, o["qkv"], o["x_next"]))()
+            torch.cuda.synchronize()
+            assert moe_layer.layer_status(lws[mode]) == 0, mode
+            res[mode] = o
+        for k in res["sep"]:
+            assert torch.equal(res["sep"][k], res["fused"][k]), f"position {p}: {k} differs from the separate launches"
+        for a, b in zip(kv["sep"], kv["fused"]):
+            assert torch.equal(a, b), f"position {p}: KV cache rows differ"
+        log(f"  max_pos={max_pos} position {p}: attention row, o_proj, MoE, routing, next q|k|v equal "
+            f"(|oproj| max {float(res['fused']['oproj'].abs().max()):.3f})")
+        # a plain launch on the fused workspace keeps the launch counts in step
+        moe_layer.decode_layer(res["fused"]["x_out"], res["fused"]["ids"], res["fused"]["w"], experts, ws=lws["fused"])
+        torch.cuda.synchronize()
+        assert moe_layer.layer_status(lws["fused"]) == 0
+
+
+def test_post_attn_argument_checks(dext):
+    lib = _lib.load()
+    p = 256
+    ws = moe_layer.workspace(E, MI, H)
+    nb = lib.mxfp4_attn_decode_workspace_size(1, 32, 512)
+    head = [p, nb, p]
+    mid = [p, p, p, p, p, 1e-6, p, p, 1, None, None, None, None, None, p, p, p, p, p, p, 128, E, H, MI,
+           None, None, None, 0, None, None, p, ws.data_ptr(), ws.numel(), None]
+    assert lib.mxfp4_decode_layer_post_attn(*head, 16, 512, None, None, *mid) == -1
+    assert "Hq=16" in lib.mxfp4_last_error().decode()
+    assert lib.mxfp4_decode_layer_post_attn(p, nb - 4, p, 32, 512, None, None, *mid) == -1
+    assert "attention workspace" in lib.mxfp4_last_error().decode()
+    assert lib.mxfp4_decode_layer_post_attn(*head, 32, 512, p, None, *mid) == -1
+    assert "aq_out and as_out" in lib.mxfp4_last_error().decode()
