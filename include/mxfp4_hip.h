@@ -330,6 +330,14 @@ int mxfp4_moe_decode_layer_fused_router_qkv(const void* x, const float* resid, c
  *   x, norm_w, ... out, workspace: as mxfp4_moe_decode_layer_fused_router
  *   with resid = this launch's o_proj output; qkv_*: as
  *   mxfp4_moe_decode_layer_fused_router_qkv, or qkv_wp NULL for no tail.
+ *   next_attn_workspace (with the tail; NULL for none): the NEXT layer's
+ *   attention chunk pass also runs in this launch, as
+ *   mxfp4_attn_decode_fused_partials(qkv_out, q_norm_next, k_norm_next, eps,
+ *   theta, kvk_next, kvv_next, dpos, M = 1, Hq, Hkv, 128, max_pos, codec,
+ *   next_attn_workspace) would: it writes the next layer's KV rows and
+ *   chunk records for the next launch's merge, so a decode step is one
+ *   launch per layer.  Hq = 8 Hkv, Nq = (Hq + 2 Hkv) * 128, max_pos * Hkv
+ *   <= 32768; next_attn_workspace must differ from attn_workspace.
  * 16-byte aligned (aq_out 4-byte).  A position outside [0, max_pos) gives a
  * zero attention output.  Same workspace as mxfp4_moe_decode_layer.
  */
@@ -342,8 +350,10 @@ int mxfp4_decode_layer_post_attn(const void* attn_workspace, size_t attn_workspa
                                  const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws,
                                  int n_experts, int E, int H, int Mi, const void* qkv_norm_w,
                                  const uint8_t* qkv_wp, const uint8_t* qkv_ws, int Nq, float* qkv_out,
-                                 void* x_next_out, float* out, void* workspace, size_t workspace_bytes,
-                                 void* stream);
+                                 void* x_next_out, void* next_attn_workspace, size_t next_attn_workspace_bytes,
+                                 uint8_t* kvk_next, uint8_t* kvv_next, const void* q_norm_next,
+                                 const void* k_norm_next, int Hkv, float theta, int codec, float* out,
+                                 void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------
  * A run of consecutive decode MoE layers in one launch (batch 1).  No single

@@ -52,6 +52,7 @@ SIGNATURES = {
                                             _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
                                             _c_i, _c_i, _c_i, _c_i,
                                             _c_p, _c_p, _c_p, _c_i, _c_p, _c_p,
+                                            _c_p, _c_sz, _c_p, _c_p, _c_p, _c_p, _c_i, ctypes.c_float, _c_i,
                                             _c_p, _c_p, _c_sz, _c_p]),
     "mxfp4_attn_decode_fused_partials": (_c_i, [_c_p, _c_p, _c_p, ctypes.c_float, ctypes.c_float, _c_p, _c_p,
                                                 _c_p, _c_i, _c_i, _c_i, _c_i, _c_i, _c_i, _c_p, _c_sz, _c_p]),

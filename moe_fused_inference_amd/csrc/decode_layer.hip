@@ -66,6 +66,7 @@
 // MFMA yields all three partial products and y = D[0] + D[1] + D[2]; the other
 // 13 rows are zero and cost nothing in an HBM-bound kernel.
 #include "attn_merge.h"
+#include "attn_partial.h"
 #include "decode_common.h"
 #include "mx_host.h"
 
@@ -83,17 +84,20 @@ constexpr int kMemoQOff = 3072;       // int32 launch count of q|k|v workgroup q
 constexpr int kLogOff = 4096;         // fused router: (logit, tag) 64-bit words, n_experts <= 256
 constexpr int kMemoMOff = 6144;       // int32 launch count of attention-merge workgroup h (front): [64]
 constexpr int kMemoOOff = 6400;       // int32 launch count of o_proj workgroup o (front): [128]
-constexpr int kHOff = 8192;           // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
+constexpr int kMemoTOff = 8192;       // int32 launch count of attention chunk workgroup t (next layer): [512]
+constexpr int kHOff = 16384;          // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
                                       // then (out[c], tag) 64-bit words, c < H, for the q|k|v tail,
                                       // then the front's words: kAttnWords per head of the attention
-                                      // output, and (o_proj[c], tag), c < H
+                                      // output, and (o_proj[c], tag), c < H; then (q|k|v[r], tag)
+                                      // for the next layer's attention, r < 8192
 constexpr int kMaxRouterWg = 16;      // fused router: 16 logits per workgroup
 constexpr int kMaxQkvWg = 128;        // q|k|v tail: 64 rows per workgroup, up to 8192 rows
 constexpr int kMaxH = 2048;
 constexpr int kMaxHq = 32;            // front: query heads (o_proj K = 4096)
 constexpr int kMaxOWg = 128;          // front: o_proj workgroups, 16 rows each
 constexpr int kAttnWords = 17;        // front: per head, 16 words of 4 MXFP4 bytes + 1 of the 4 scale codes
-constexpr int kWordsAfterH = 2 * kMaxH + kMaxHq * kAttnWords;   // 64-bit words after the h buffers
+constexpr int kMaxAttnWg = 512;       // next layer's attention: chunks x kv heads (max_pos 8192 at 4 kv heads)
+constexpr int kWordsAfterH = 2 * kMaxH + kMaxHq * kAttnWords + 64 * kMaxQkvWg;   // 64-bit words after h
 
 struct LayerArgs {
     const uint16_t* x;        // (H) bf16
@@ -145,6 +149,18 @@ struct LayerArgs {
     const uint8_t* ows;
     float* oproj_out;         // optional (H) fp32 o_proj output
     int nm, no;               // merge workgroups (Hq = 32) and o_proj workgroups (H / 16)
+    // the next layer's attention chunk pass (with the q|k|v tail, nat > 0):
+    // nat = nchunk * Hkv workgroups after the tail take q and the new k / v
+    // rows from the tail's (value, tag) words and write the next layer's KV
+    // rows and chunk records (apart_n), which the next launch merges
+    float* apart_n;
+    uint8_t* kvk_n;
+    uint8_t* kvv_n;
+    const uint16_t* qn_n;     // next layer's q / k head RMSNorm weights (128) bf16
+    const uint16_t* kn_n;
+    float theta;
+    int codec;
+    int nat, hkv;
     int n_experts;            // experts per layer (logits routing)
     int norm;                 // renormalise the top-E weights (logits routing)
     int32_t* ids_out;         // optional (E) ids / weights written by workgroup 0 (logits routing)
@@ -203,6 +219,7 @@ union Smem {
         float red[4][16];
     } r;
     am::MergeLds m;                                // attention-merge workgroups (front)
+    ap::AttnLds<1, true> t;                        // next layer's attention chunk workgroups
     struct {                                       // o_proj workgroups (front)
         uint8_t aq[kMaxHq * 64];                   // the attention output's MXFP4 (K = 4096)
         uint8_t as[kMaxHq * 4];
@@ -219,6 +236,7 @@ __device__ __forceinline__ uint64_t* attn_words(const LayerArgs& a) { return out
 __device__ __forceinline__ uint64_t* oproj_words(const LayerArgs& a) {
     return attn_words(a) + kMaxHq * kAttnWords;
 }
+__device__ __forceinline__ uint64_t* qkv_words(const LayerArgs& a) { return oproj_words(a) + kMaxH; }
 
 // o_proj output elements 8t .. 8t+7 of thread t: from `oproj`, or with the
 // front from this launch's o_proj words -- one probe word per wave (the first
@@ -559,6 +577,93 @@ __device__ __forceinline__ void oproj_wg(const LayerArgs& a, Smem& sm, int oi) {
     if (tid == 0) *memo = launch + 1;
 }
 
+// q|k|v values for the next layer's attention chunk pass from the tail's
+// (value, tag) words (ap::attn_partial_body's source): one probe word per
+// wave, then the rows until every word carries the tag.  Rows repeated in
+// the wave's list (clamped rows of absent tokens: at M = 1 the q rows of the
+// second token slot and all k / v tasks) are loaded once.  On expiry the
+// error flag is set and the values are zero.
+struct TaggedQkv {
+    static constexpr bool kWaits = true;
+    const uint64_t* words;
+    uint32_t tag;
+    int* err;
+    template <int N>
+    __device__ __forceinline__ static bool load_rows(const uint64_t* words, uint32_t tag, const int64_t (&o)[N],
+                                                     float (&va)[N], float (&vb)[N]) {
+        const int lane = threadIdx.x & 63;
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            int dup = -1;
+#pragma unroll
+            for (int k = 0; k < i; ++k) dup = (dup < 0 && o[k] == o[i]) ? k : dup;
+            if (dup < 0) {
+                const uint64_t wa = __hip_atomic_load(words + o[i] + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t wb = __hip_atomic_load(words + o[i] + lane + 64, __ATOMIC_RELAXED,
+                                                      __HIP_MEMORY_SCOPE_AGENT);
+                va[i] = __uint_as_float((uint32_t)wa);
+                vb[i] = __uint_as_float((uint32_t)wb);
+                pending |= (uint32_t)(wa >> 32) != tag || (uint32_t)(wb >> 32) != tag;
+            } else {
+                va[i] = va[dup];
+                vb[i] = vb[dup];
+            }
+        }
+        return pending;
+    }
+    template <int QR, int NR>
+    __device__ __forceinline__ bool fetch(const int64_t (&qo)[QR], const int64_t (&ko)[NR], float (&qa)[QR],
+                                          float (&qb)[QR], float (&ka)[NR], float (&kb)[NR]) const {
+        int spins = 0;
+        bool ok = true;
+        while (true) {
+            const uint64_t w = __hip_atomic_load(words + ko[NR - 1] + 127, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (__builtin_amdgcn_readfirstlane((uint32_t)(w >> 32)) == tag) break;
+            if (++spins >= kSpinLimit) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+        }
+        while (ok) {
+            bool pending = load_rows<QR>(words, tag, qo, qa, qb);
+            pending |= load_rows<NR>(words, tag, ko, ka, kb);
+            if (__builtin_amdgcn_ballot_w64(pending) == 0) break;
+            if (++spins >= kSpinLimit) {
+                ok = false;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+            asm volatile("" ::: "memory");
+        }
+        if (!ok) {
+#pragma unroll
+            for (int i = 0; i < QR; ++i) qa[i] = qb[i] = 0.0f;
+#pragma unroll
+            for (int j = 0; j < NR; ++j) ka[j] = kb[j] = 0.0f;
+            __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return ok;
+    }
+};
+
+// Attention chunk workgroup ti (next layer, after the q|k|v tail): chunk ti
+// % nchunk of kv head ti / nchunk, attn_partial_kernel's work for one token
+// (ap::attn_partial_body, 8 query heads per kv head) with q and the new k /
+// v rows from this launch's q|k|v words.  Its K / V cache loads are issued
+// at dispatch, while the MoE runs.
+__device__ __forceinline__ void attn_wg(const LayerArgs& a, Smem& sm, int ti) {
+    int* memo = reinterpret_cast<int*>(a.ws + kMemoTOff) + ti;
+    const int launch = *memo;
+    const TaggedQkv src{qkv_words(a), (uint32_t)(launch + 1), reinterpret_cast<int*>(a.ws + kErrOff)};
+    const ap::QkvIn fz{nullptr, a.qn_n, a.kn_n, a.eps, a.theta, a.codec, a.kvk_n, a.kvv_n};
+    ap::attn_partial_body<8, 1, true>(sm.t, src, ti % a.nchunk, ti / a.nchunk, 0, nullptr, a.kvk_n, a.kvv_n, nullptr,
+                                      a.apart_n, a.dpos, 1, 8 * a.hkv, a.hkv, a.max_pos, a.nchunk,
+                                      1.0f / sqrtf((float)am::kD), fz);
+    if (threadIdx.x == 0) *memo = launch + 1;
+}
+
 // q|k|v tail workgroup qi (fused router, nq > 0): rows 64qi .. 64qi+63 of
 // the next layer's q|k|v projection, wave w rows 64qi + 16w .. +15.  The
 // weights are loaded first and stream while the MoE runs; the workgroup then
@@ -691,7 +796,12 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
     t += acc[1][0];
     t += acc[2][0];
     t += acc[3][0];
-    if (lane < 16 && row_i < a.Nq) a.qkv_out[row_i] = t;
+    if (lane < 16 && row_i < a.Nq) {
+        a.qkv_out[row_i] = t;
+        if (a.nat > 0)   // for the next layer's attention workgroups of this launch
+            __hip_atomic_store(qkv_words(a) + row_i, (uint64_t)__float_as_uint(t) | ((uint64_t)tag << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
     if (tid == 0) {
         *memo = launch + 1;
         if (cfg != a.cfg) set_error(a);
@@ -735,7 +845,12 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             router_wg(a, sm, nred, (int)blockIdx.x - nfront);
             return;
         }
-        // q|k|v tail workgroups follow the down workgroups
+        // q|k|v tail workgroups follow the down workgroups, the next layer's
+        // attention chunk workgroups follow them
+        if (bid >= nA + (a.H >> 4) + a.nq) {
+            attn_wg(a, sm, bid - nA - (a.H >> 4) - a.nq);
+            return;
+        }
         if (bid >= nA + (a.H >> 4)) {
             qkv_wg(a, sm, nred, bid - nA - (a.H >> 4));
             return;
@@ -907,21 +1022,23 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 if (ROUTE != ROUTE_FUSED && bid == 0)
                     for (int k = 0; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
             }
-            // likewise the q|k|v tail slots this launch has no workgroup for
-            if (bid == 0) {
-                const int nq = ROUTE == ROUTE_FUSED ? a.nq : 0;
-                const int nm = ROUTE == ROUTE_FUSED ? a.nm : 0;
-                const int no = ROUTE == ROUTE_FUSED ? a.no : 0;
-                int* mq = reinterpret_cast<int*>(a.ws + kMemoQOff);
+        }
+        // likewise the slots of the q|k|v tail, the front and the next
+        // layer's attention this launch has no workgroup for (workgroup 0,
+        // all threads: one memory round trip)
+        if (bid == 0) {
+            const int t = threadIdx.x;
+            const int nq = ROUTE == ROUTE_FUSED ? a.nq : 0;
+            const int nm = ROUTE == ROUTE_FUSED ? a.nm : 0;
+            const int no = ROUTE == ROUTE_FUSED ? a.no : 0;
+            const int nat = ROUTE == ROUTE_FUSED ? a.nat : 0;
+            if (t < kMaxQkvWg && t >= nq) reinterpret_cast<int*>(a.ws + kMemoQOff)[t] += 1;
+            if (t < 64 && t >= nm) reinterpret_cast<int*>(a.ws + kMemoMOff)[t] += 1;
+            if (t < kMaxOWg && t >= no) reinterpret_cast<int*>(a.ws + kMemoOOff)[t] += 1;
+            int* mt = reinterpret_cast<int*>(a.ws + kMemoTOff);
 #pragma unroll
-                for (int k = lane; k < kMaxQkvWg; k += 64)
-                    if (k >= nq) mq[k] += 1;
-                if (lane >= nm) reinterpret_cast<int*>(a.ws + kMemoMOff)[lane] += 1;
-                int* mo = reinterpret_cast<int*>(a.ws + kMemoOOff);
-#pragma unroll
-                for (int k = lane; k < kMaxOWg; k += 64)
-                    if (k >= no) mo[k] += 1;
-            }
+            for (int k = t; k < kMaxAttnWg; k += 256)
+                if (k >= nat) mt[k] += 1;
         }
         return;
     }
@@ -1219,8 +1336,9 @@ int launch_layer(const LayerArgs& a, hipStream_t st) {
     const int nR = ROUTE == ROUTE_FUSED ? a.nr : 0;
     const int nQ = ROUTE == ROUTE_FUSED ? a.nq : 0;
     const int nF = ROUTE == ROUTE_FUSED ? a.nm + a.no : 0;
+    const int nT = ROUTE == ROUTE_FUSED ? a.nat : 0;
     const int steps = (a.Mi / 32 + 3) / 4;
-    const dim3 grid(nF + nR + nA + nB + nQ);
+    const dim3 grid(nF + nR + nA + nB + nQ + nT);
     if (steps <= 6) hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 6>), grid, dim3(256), 0, st, a);
     else hipLaunchKernelGGL((decode_layer_kernel<ROUTE, 8>), grid, dim3(256), 0, st, a);
     return mxh::launch_status("moe_decode_layer");
@@ -1362,7 +1480,9 @@ extern "C" int mxfp4_decode_layer_post_attn(
     int32_t* ids_out, float* w_out, const uint8_t* gate_wp, const uint8_t* gate_ws, const uint8_t* up_wp,
     const uint8_t* up_ws, const uint8_t* down_wp, const uint8_t* down_ws, int n_experts, int E, int H, int Mi,
     const void* qkv_norm_w, const uint8_t* qkv_wp, const uint8_t* qkv_ws, int Nq, float* qkv_out, void* x_next_out,
-    float* out, void* workspace, size_t workspace_bytes, void* stream) {
+    void* next_attn_workspace, size_t next_attn_workspace_bytes, uint8_t* kvk_next, uint8_t* kvv_next,
+    const void* q_norm_next, const void* k_norm_next, int Hkv, float theta, int codec, float* out, void* workspace,
+    size_t workspace_bytes, void* stream) {
     MXH_REQUIRE(attn_workspace && dpos && o_wp && o_ws && oproj_out, "decode_layer_post_attn: null pointer");
     MXH_REQUIRE(Hq == kMaxHq, "decode_layer_post_attn: Hq=%d (the o_proj front is built for %d heads of 128)", Hq,
                 kMaxHq);
@@ -1407,5 +1527,29 @@ extern "C" int mxfp4_decode_layer_post_attn(
     a.oproj_out = oproj_out;
     a.nm = Hq;
     a.no = H / 16;
+    if (next_attn_workspace) {
+        MXH_REQUIRE(qkv_wp, "decode_layer_post_attn: the next layer's attention needs the q|k|v tail");
+        MXH_REQUIRE(kvk_next && kvv_next && q_norm_next && k_norm_next, "decode_layer_post_attn: null next-attention pointer");
+        MXH_REQUIRE(Hkv >= 1 && Hq == 8 * Hkv && Nq == (Hq + 2 * Hkv) * am::kD,
+                    "decode_layer_post_attn: Hkv=%d, Nq=%d (8 query heads per kv head, Nq = (Hq + 2 Hkv) * 128)", Hkv,
+                    Nq);
+        MXH_REQUIRE(codec == 0 || codec == 1, "decode_layer_post_attn: codec %d", codec);
+        MXH_REQUIRE(next_attn_workspace_bytes >= mxfp4_attn_decode_workspace_size(1, Hq, max_pos) &&
+                        ((uintptr_t)next_attn_workspace & 15) == 0 && next_attn_workspace != attn_workspace,
+                    "decode_layer_post_attn: next attention workspace (16-byte aligned, "
+                    "mxfp4_attn_decode_workspace_size bytes, not attn_workspace)");
+        MXH_REQUIRE(((uintptr_t)kvk_next & 15) == 0 && ((uintptr_t)kvv_next & 3) == 0,
+                    "decode_layer_post_attn: kv cache rows must be aligned");
+        MXH_REQUIRE(a.nchunk * Hkv <= kMaxAttnWg, "decode_layer_post_attn: max_pos=%d x Hkv=%d too large", max_pos, Hkv);
+        a.apart_n = static_cast<float*>(next_attn_workspace);
+        a.kvk_n = kvk_next;
+        a.kvv_n = kvv_next;
+        a.qn_n = static_cast<const uint16_t*>(q_norm_next);
+        a.kn_n = static_cast<const uint16_t*>(k_norm_next);
+        a.theta = theta;
+        a.codec = codec;
+        a.hkv = Hkv;
+        a.nat = a.nchunk * Hkv;
+    }
     return launch_layer<ROUTE_FUSED>(a, mxh::as_stream(stream));
 }

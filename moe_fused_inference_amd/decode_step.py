@@ -159,7 +159,7 @@ class DecodeStep:
     tokens and dpos + M for the next step."""
 
     def __init__(self, model, cfg, M=1, max_pos=4096, device="cuda", fused_router=True, qkv_tail=True,
-                 attn_front=True):
+                 attn_front=True, attn_next=True):
         self.lib = _lib.load()
         self.model, self.cfg, self.M, self.max_pos = model, cfg, int(M), int(max_pos)
         self.kv_codec = 0 if self.M == 1 else 1   # kv_write's codec / torch float8_e4m3fn
@@ -176,6 +176,10 @@ class DecodeStep:
         # MoE launch (mxfp4_decode_layer_post_attn; 32 heads of 128): two
         # launches per layer in all
         self.attn_front = self.qkv_tail and bool(attn_front) and cfg.n_heads == 32 and cfg.head_dim == 128
+        # and with the front, the next layer's attention chunk pass too: one
+        # launch per layer (8 query heads per kv head, max_pos * kv heads <= 32768)
+        self.attn_next = (self.attn_front and bool(attn_next) and cfg.n_heads == 8 * cfg.n_kv_heads
+                          and ((max_pos + 63) // 64) * cfg.n_kv_heads <= 512)
         self._fr_calls = {}
         c = cfg
         if c.head_dim != 128:
@@ -209,6 +213,7 @@ class DecodeStep:
         buf("arg_ws", ((nb + 255) // 256 * 256,), u8)   # zero-filled once; each call leaves it so
         nb = self.lib.mxfp4_attn_decode_workspace_size(M, Hq, self.max_pos)
         buf("attn_ws", ((nb + 15) // 16 * 16,), u8)
+        buf("attn_ws2", ((nb + 15) // 16 * 16,) if M == 1 else (16,), u8)   # odd layers' chunk records (attn_next)
         # KV cache of every layer: (L, max_pos, Hkv, D) E4M3 bytes
         buf("kvk", (c.n_layers, self.max_pos, Hkv, D), u8)
         buf("kvv", (c.n_layers, self.max_pos, Hkv, D), u8)
@@ -271,6 +276,13 @@ class DecodeStep:
         by layer l-1's MoE launch, so odd and even layers alternate buffers."""
         return self.b.qkv2 if (self.qkv_tail and l % 2) else self.b.qkv
 
+    def attn_ws_of(self, l):
+        """The attention workspace holding layer l's chunk records: with the
+        next layer's attention in each layer launch, odd and even layers
+        alternate buffers (a launch merges one layer's records while it
+        writes the next layer's)."""
+        return self.b.attn_ws2 if (self.attn_next and l % 2) else self.b.attn_ws
+
     def _attn_oproj(self, l, lw, qkv, s):
         """q/k head norm + RoPE, the step's KV rows and attention in one pass,
         its output straight to MXFP4 of bf16(o) (the raw scores are not kept),
@@ -299,13 +311,14 @@ class DecodeStep:
         self._norm_lin(b.x, None, m.layers[0].in_norm, None, False, m.layers[0].qkv, self.qkv_buf(0), s)
         cur = 0                      # xs[cur]: the layer's input residual stream
         for l, lw in enumerate(m.layers):
-            if self.attn_front:
+            if self.attn_front and (l == 0 or not self.attn_next):
+                aws = self.attn_ws_of(l)
                 self._ck(self.lib.mxfp4_attn_decode_fused_partials(
                     self.qkv_buf(l).data_ptr(), lw.q_norm.data_ptr(), lw.k_norm.data_ptr(), c.rms_eps, c.rope_theta,
                     b.kvk[l].data_ptr(), b.kvv[l].data_ptr(), b.dpos.data_ptr(), 1, c.n_heads, c.n_kv_heads,
-                    c.head_dim, self.max_pos, self.kv_codec, b.attn_ws.data_ptr(), b.attn_ws.numel(), s),
+                    c.head_dim, self.max_pos, self.kv_codec, aws.data_ptr(), aws.numel(), s),
                     "attn_decode_fused_partials")
-            else:
+            elif not self.attn_front:
                 self._attn_oproj(l, lw, self.qkv_buf(l), s)
             xo, xn = (cur + 1) % 3, (cur + 2) % 3
             call = self._fr_calls.get(("tail", l))
@@ -315,10 +328,16 @@ class DecodeStep:
                     nl = m.layers[l + 1]
                     nxt = (nl.in_norm, nl.qkv.wp, nl.qkv.ws, self.qkv_buf(l + 1)[0], xs[xn][0])
                 if self.attn_front:
-                    call = PostAttnLayerCall(b.attn_ws, b.dpos, self.max_pos, lw.o.wp, lw.o.ws, b.oproj[0],
+                    nat = None
+                    if self.attn_next and l + 1 < L:
+                        nl = m.layers[l + 1]
+                        nat = (self.attn_ws_of(l + 1), b.kvk[l + 1], b.kvv[l + 1], nl.q_norm, nl.k_norm, c.n_kv_heads,
+                               c.rope_theta, self.kv_codec)
+                    call = PostAttnLayerCall(self.attn_ws_of(l), b.dpos, self.max_pos, lw.o.wp, lw.o.ws, b.oproj[0],
                                              xs[cur][0], lw.post_norm, c.rms_eps, lw.gate.wp, lw.gate.ws, c.top_k,
                                              lw.experts, b.moe[0], self.layer_ws, aq_out=b.aq[0], as_out=b.as_[0],
-                                             x_out=xs[xo][0], y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt)
+                                             x_out=xs[xo][0], y_out=b.y[0], logits_out=b.glog[0], next_qkv=nxt,
+                                             next_attn=nat)
                 else:
                     call = FusedRouterLayerCall(xs[cur][0], b.oproj[0], lw.post_norm, c.rms_eps, lw.gate.wp,
                                                 lw.gate.ws, c.top_k, lw.experts, b.moe[0], self.layer_ws,

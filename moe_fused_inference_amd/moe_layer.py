@@ -188,11 +188,14 @@ class PostAttnLayerCall:
     oproj_out fp32 (H,), then the fused-router MoE launch of
     FusedRouterLayerCall on (x, oproj_out), with the same optional outputs
     and next_qkv tail; aq_out / as_out optionally receive the attention
-    output's MXFP4 row."""
+    output's MXFP4 row.  next_attn = (attn_ws_next, kvk_next, kvv_next,
+    q_norm_next, k_norm_next, Hkv, theta, codec), with next_qkv: the next
+    layer's attention chunk pass in the same launch, on next_qkv's output,
+    leaving its records in attn_ws_next (a buffer other than attn_ws)."""
 
     def __init__(self, attn_ws, dpos, max_pos, o_wp, o_ws, oproj_out, x, norm_w, eps, router_wp, router_ws, E,
                  experts, out, ws, norm=True, aq_out=None, as_out=None, x_out=None, y_out=None, logits_out=None,
-                 ids_out=None, w_out=None, next_qkv=None):
+                 ids_out=None, w_out=None, next_qkv=None, next_attn=None):
         self.lib = _lib.load()
         n, H = experts.n_experts, experts.hidden
         hq = 32
@@ -212,15 +215,21 @@ class PostAttnLayerCall:
             if tuple(qwp.shape) != (nq, H // 2) or tuple(qws.shape) != (nq, H // 32) or qkv_out.numel() != nq:
                 raise RuntimeError("q|k|v weights must be (Nq, H/2) + (Nq, H/32), qkv_out (Nq,)")
             qkv = (qnw.data_ptr(), qwp.data_ptr(), qws.data_ptr(), nq, qkv_out.data_ptr(), ptr(x_next))
+        if next_attn is None:
+            nat = (None, 0, None, None, None, None, 0, 0.0, 0)
+        else:
+            aws_n, kvk_n, kvv_n, qn_n, kn_n, hkv, theta, codec = next_attn
+            nat = (aws_n.data_ptr(), aws_n.numel() * aws_n.element_size(), kvk_n.data_ptr(), kvv_n.data_ptr(),
+                   qn_n.data_ptr(), kn_n.data_ptr(), int(hkv), float(theta), int(codec))
         self.keep = (attn_ws, dpos, o_wp, o_ws, oproj_out, x, norm_w, router_wp, router_ws, experts, out, ws, aq_out,
-                     as_out, x_out, y_out, logits_out, ids_out, w_out, next_qkv)
+                     as_out, x_out, y_out, logits_out, ids_out, w_out, next_qkv, next_attn)
         self.args = ((attn_ws.data_ptr(), attn_ws.numel() * attn_ws.element_size(), dpos.data_ptr(), hq,
                       int(max_pos), ptr(aq_out), ptr(as_out), o_wp.data_ptr(), o_ws.data_ptr(),
                       oproj_out.data_ptr(), x.data_ptr(), norm_w.data_ptr(), float(eps), router_wp.data_ptr(),
                       router_ws.data_ptr(), int(bool(norm)), ptr(x_out), ptr(y_out), ptr(logits_out), ptr(ids_out),
                       ptr(w_out), experts.gate_wp.data_ptr(), experts.gate_ws.data_ptr(), experts.up_wp.data_ptr(),
                       experts.up_ws.data_ptr(), experts.down_wp.data_ptr(), experts.down_ws.data_ptr(), n, int(E),
-                      H, experts.inter) + qkv + (out.data_ptr(), ws.data_ptr(), ws.numel()))
+                      H, experts.inter) + qkv + nat + (out.data_ptr(), ws.data_ptr(), ws.numel()))
 
     def __call__(self, stream=None):
         s = torch.cuda.current_stream().cuda_stream if stream is None else stream

@@ -169,17 +169,18 @@ def test_cfg5_decode_step_batch8(model):
 
 
 def test_cfg5_launch_fusions_equal_separate_launches(model):
-    """The M = 1 step with two launches per layer (attention chunk pass; then
-    merge + o_proj + router + MoE + the next layer's input norm and q|k|v in
-    one launch), with three (q|k|v tail only) and with four (the q|k|v
-    projection as its own launch) are equal bit for bit: logits, greedy ids,
-    every layer's KV rows and the final residual stream, over two steps from
-    the same state."""
+    """The M = 1 step with one launch per layer (merge + o_proj + router + MoE
+    + the next layer's input norm, q|k|v and attention chunk pass), with two
+    (the chunk pass as its own launch), with three (q|k|v tail only) and with
+    four (the q|k|v projection as its own launch) are equal bit for bit:
+    logits, greedy ids, every layer's KV rows and the final residual stream,
+    over two steps from the same state."""
     m, _ = model
     res = {}
-    for tail, front in ((True, True), (True, False), (False, False)):
-        st = DecodeStep(m, CFG, M=1, max_pos=MAX_POS, device=DEV, qkv_tail=tail, attn_front=front)
-        assert st.qkv_tail == tail and st.attn_front == front and st.fused_router
+    modes = ((True, True, True), (True, True, False), (True, False, False), (False, False, False))
+    for tail, front, nxt in modes:
+        st = DecodeStep(m, CFG, M=1, max_pos=MAX_POS, device=DEV, qkv_tail=tail, attn_front=front, attn_next=nxt)
+        assert st.qkv_tail == tail and st.attn_front == front and st.attn_next == nxt and st.fused_router
         pos = MAX_POS - 2
         st.fill_cache(pos, seed=19)
         st.set_state([4242], pos)
@@ -189,13 +190,14 @@ def test_cfg5_launch_fusions_equal_separate_launches(model):
             st.check_status()
             out.append((np_(st.b.logits).copy(), np_(st.b.ids).copy(), np_(st.x_final.view(torch.int16)).copy()))
         kv = (np_(st.b.kvk[:, pos:pos + 2]).copy(), np_(st.b.kvv[:, pos:pos + 2]).copy())
-        res[(tail, front)] = (out, kv)
+        res[(tail, front, nxt)] = (out, kv)
         del st
         torch.cuda.synchronize()
-    (o0, k0) = res[(True, True)]
-    for key in ((True, False), (False, False)):
+    (o0, k0) = res[modes[0]]
+    for key in modes[1:]:
         o1, k1 = res[key]
         for i, (a, b) in enumerate(zip(o0, o1)):
             assert all(np.array_equal(u, v) for u, v in zip(a, b)), f"step {i} differs from {key}"
         assert np.array_equal(k0[0], k1[0]) and np.array_equal(k0[1], k1[1]), f"KV rows differ from {key}"
-    log(f"  two-launch layer step == three- and four-launch steps (ids {o0[0][1].tolist()}, {o0[1][1].tolist()})")
+    log(f"  one-launch layer step == two-, three- and four-launch steps (ids {o0[0][1].tolist()}, "
+        f"{o0[1][1].tolist()})")

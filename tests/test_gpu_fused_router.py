@@ -276,12 +276,14 @@ def test_fused_router_qkv_argument_checks(dext):
 def test_post_attn_matches_separate_calls(dext, max_pos, pos):
     """mxfp4_decode_layer_post_attn after mxfp4_attn_decode_fused_partials
     against the separate launches it replaces -- mxfp4_attn_decode_fused
-    (chunk records + merge to MXFP4), mxfp4_lin_pq (o_proj) and the fused
-    router + MoE + q|k|v tail launch -- bit for bit: the attention's MXFP4
-    row, o_proj, residual, routing, MoE output, next q|k|v, x_next and the KV
-    rows written.  Context 5000 takes the merge's two-pass path (more than
-    64 chunks).  Three positions in a row on shared workspaces, with a plain
-    fused-layer launch in between."""
+    (chunk records + merge to MXFP4), mxfp4_lin_pq (o_proj), the fused
+    router + MoE + q|k|v tail launch and the next layer's
+    mxfp4_attn_decode_fused_partials -- bit for bit: the attention's MXFP4
+    row, o_proj, residual, routing, MoE output, next q|k|v, x_next, the KV
+    rows written in both layers and the next layer's chunk records.  Context
+    5000 takes the merge's two-pass path (more than 64 chunks).  Three
+    positions in a row on shared workspaces, with a plain fused-layer launch
+    in between."""
     lib = _lib.load()
     Hq, Hkv, D, n_exp, nq = 32, 4, 128, 128, 5120
     experts = make_stack(dext, n_exp, H, MI, seed=16000 + pos)
@@ -292,12 +294,16 @@ def test_post_attn_matches_separate_calls(dext, max_pos, pos):
     g.manual_seed(pos)
     qn = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
     kn = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    qn2 = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
+    kn2 = (1.0 + 0.1 * torch.randn(D, generator=g, device=DEV)).bfloat16()
     qnw = (1.0 + 0.1 * torch.randn(H, generator=g, device=DEV)).bfloat16()
     r = torch.randint(0, 256, (max_pos, Hkv, D), generator=g, device=DEV, dtype=torch.int32)
     cache0 = ((r & 0x80) | (r & 0x3F)).to(torch.uint8)     # |v| < 2, no NaN code
     kv = {k: (cache0.clone(), cache0.flip(0).contiguous()) for k in ("sep", "fused")}
+    kv2 = {k: (cache0.flip(1).contiguous(), cache0.flip(2).contiguous()) for k in kv}   # the next layer's
     nb = lib.mxfp4_attn_decode_workspace_size(1, Hq, max_pos)
     aws = {k: torch.empty((nb + 15) // 16 * 16, dtype=torch.uint8, device=DEV) for k in kv}
+    aws2 = {k: torch.zeros((nb + 15) // 16 * 16, dtype=torch.uint8, device=DEV) for k in kv}
     lws = {k: moe_layer.workspace(E, MI, H) for k in kv}
     dpos = torch.zeros(1, dtype=torch.int32, device=DEV)
     s = torch.cuda.current_stream().cuda_stream
@@ -333,6 +339,10 @@ def test_post_attn_matches_separate_calls(dext, max_pos, pos):
                 moe_layer.FusedRouterLayerCall(xa, o["oproj"], nw, EPS, rwp, rws, E, experts, o["out"], lws[mode],
                                                x_out=o["x_out"], ids_out=o["ids"], w_out=o["w"],
                                                next_qkv=(qnw, qwp, qws, o["qkv"], o["x_next"]))()
+                _lib.check(lib.mxfp4_attn_decode_fused_partials(
+                    o["qkv"].data_ptr(), qn2.data_ptr(), kn2.data_ptr(), EPS, 1e6, kv2[mode][0].data_ptr(),
+                    kv2[mode][1].data_ptr(), dpos.data_ptr(), 1, Hq, Hkv, D, max_pos, 0, aws2[mode].data_ptr(),
+                    aws2[mode].numel(), s), "attn_decode_fused_partials")
             else:
                 _lib.check(lib.mxfp4_attn_decode_fused_partials(*common, 1, Hq, Hkv, D, max_pos, 0,
                                                                 aws[mode].data_ptr(), aws[mode].numel(), s),
@@ -340,14 +350,23 @@ def test_post_attn_matches_separate_calls(dext, max_pos, pos):
                 moe_layer.PostAttnLayerCall(aws[mode], dpos, max_pos, owp, ows, o["oproj"], xa, nw, EPS, rwp, rws, E,
                                             experts, o["out"], lws[mode], aq_out=o["aq"], as_out=o["as_"],
                                             x_out=o["x_out"], ids_out=o["ids"], w_out=o["w"],
-                                            next_qkv=(qnw, qwp, qws, o["qkv"], o["x_next"]))()
+                                            next_qkv=(qnw, qwp, qws, o["qkv"], o["x_next"]),
+                                            next_attn=(aws2[mode], kv2[mode][0], kv2[mode][1], qn2, kn2, Hkv, 1e6,
+                                                       0))()
             torch.cuda.synchronize()
             assert moe_layer.layer_status(lws[mode]) == 0, mode
             res[mode] = o
         for k in res["sep"]:
             assert torch.equal(res["sep"][k], res["fused"][k]), f"position {p}: {k} differs from the separate launches"
-        for a, b in zip(kv["sep"], kv["fused"]):
+        for a, b in zip(kv["sep"] + kv2["sep"], kv["fused"] + kv2["fused"]):
             assert torch.equal(a, b), f"position {p}: KV cache rows differ"
+        # the next layer's chunk records (max, sum and the 128 column sums of
+        # every chunk up to the position; the record's two pad floats are not written)
+        nchunk = (max_pos + 63) // 64
+        rec = {k: aws2[k][:Hq * nchunk * 132 * 4].view(torch.float32).view(Hq, nchunk, 132)[:, :p // 64 + 1]
+               for k in kv}
+        for sl in (slice(0, 2), slice(4, 132)):
+            assert torch.equal(rec["sep"][..., sl], rec["fused"][..., sl]), f"position {p}: next layer's records differ"
         log(f"  max_pos={max_pos} position {p}: attention row, o_proj, MoE, routing, next q|k|v equal "
             f"(|oproj| max {float(res['fused']['oproj'].abs().max()):.3f})")
         # a plain launch on the fused workspace keeps the launch counts in step
@@ -363,10 +382,17 @@ def test_post_attn_argument_checks(dext):
     nb = lib.mxfp4_attn_decode_workspace_size(1, 32, 512)
     head = [p, nb, p]
     mid = [p, p, p, p, p, 1e-6, p, p, 1, None, None, None, None, None, p, p, p, p, p, p, 128, E, H, MI,
-           None, None, None, 0, None, None, p, ws.data_ptr(), ws.numel(), None]
+           None, None, None, 0, None, None, None, 0, None, None, None, None, 0, 0.0, 0, p, ws.data_ptr(), ws.numel(),
+           None]
     assert lib.mxfp4_decode_layer_post_attn(*head, 16, 512, None, None, *mid) == -1
     assert "Hq=16" in lib.mxfp4_last_error().decode()
     assert lib.mxfp4_decode_layer_post_attn(p, nb - 4, p, 32, 512, None, None, *mid) == -1
     assert "attention workspace" in lib.mxfp4_last_error().decode()
     assert lib.mxfp4_decode_layer_post_attn(*head, 32, 512, p, None, *mid) == -1
     assert "aq_out and as_out" in lib.mxfp4_last_error().decode()
+    # the next layer's attention needs the q|k|v tail
+    nxt = list(mid)
+    nxt[30] = p
+    nxt[31] = nb
+    assert lib.mxfp4_decode_layer_post_attn(*head, 32, 512, None, None, *nxt) == -1
+    assert "q|k|v tail" in lib.mxfp4_last_error().decode()
