@@ -291,14 +291,19 @@ __device__ __forceinline__ bool load_oproj(const LayerArgs& a, uint32_t tag, flo
 // bf16(o)), y = bf16(bf16(v * rstd) * w) -- the arithmetic of
 // mxfp4_rmsnorm_quant / mxfp4_rmsnorm_lin_pq (runtime/model_runner.py:20-25),
 // including its order of the sum of squares, so y equals theirs bit for bit.
-// of: the thread's o_proj elements (load_oproj).  Every thread of the
-// workgroup must call it (one barrier).
-__device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, const float (&of)[8], float (&v)[8],
-                                               float (&y)[8]) {
+// q, wq4: the thread's residual and norm weight elements (NormIn, loaded
+// before the o_proj wait); of: its o_proj elements (load_oproj).  Every
+// thread of the workgroup must call it (one barrier).
+struct NormIn {
+    uint4 q, wq4;
+    __device__ __forceinline__ explicit NormIn(const LayerArgs& a)
+        : q(*reinterpret_cast<const uint4*>(a.xres + 8 * threadIdx.x)),
+          wq4(*reinterpret_cast<const uint4*>(a.nw + 8 * threadIdx.x)) {}
+};
+__device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, const NormIn& in, const float (&of)[8],
+                                               float (&v)[8], float (&y)[8]) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int k0 = 8 * tid;
-    const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
-    const uint4 wq4 = *reinterpret_cast<const uint4*>(a.nw + k0);
+    const uint4 q = in.q, wq4 = in.wq4;
     const uint32_t xw[4] = {q.x, q.y, q.z, q.w};
     float ss = 0.0f;
 #pragma unroll
@@ -375,9 +380,10 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
 #pragma unroll
     for (int i = 0; i < 4; ++i) wq[i] = *reinterpret_cast<const uint4*>(wr + 16 * i);
     const uint32_t wsc = *reinterpret_cast<const uint32_t*>(a.rws + (int64_t)row * 64 + blk0);
+    const NormIn nin(a);
     float of[8], v[8], y[8];
     if (!load_oproj(a, (uint32_t)(launch + 1), of)) set_error(a);
-    fused_norm_row(a, nred, of, v, y);
+    fused_norm_row(a, nred, nin, of, v, y);
     // MXFP4 of y (bf16-exact values): block tid / 4, the block's four threads
     float am = 0.0f;
 #pragma unroll
@@ -872,9 +878,10 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                        (bid < nA ? kMemoAOff / 4 + (bid % a.E) * 32 + bid / a.E : kMemoBOff / 4 + (bid - nA));
     if constexpr (ROUTE == ROUTE_FUSED) {
         if (bid < nA) {
+            const NormIn nin(a);
             float of[8], vf[8];
             if (!load_oproj(a, (uint32_t)(*memo0 + 1), of)) set_error(a);
-            fused_norm_row(a, nred, of, vf, yf);
+            fused_norm_row(a, nred, nin, of, vf, yf);
         }
     } else {
         if (bid < nA && k0 < a.H) xq = *reinterpret_cast<const uint4*>(a.x + k0);
