@@ -201,3 +201,46 @@ def test_cfg5_launch_fusions_equal_separate_launches(model):
         assert np.array_equal(k0[0], k1[0]) and np.array_equal(k0[1], k1[1]), f"KV rows differ from {key}"
     log(f"  one-launch layer step == two-, three- and four-launch steps (ids {o0[0][1].tolist()}, "
         f"{o0[1][1].tolist()})")
+
+
+def test_cfg5_graph_replays_equal_eager_steps(model):
+    """The one-launch-per-layer M = 1 step captured in a HIP graph: three
+    replays (with unrelated eager work between them) give the logits, greedy
+    ids, KV rows and residual stream of three eager steps from the same
+    state, bit for bit, and the layer launches' error flag stays clear."""
+    m, _ = model
+    runs = {}
+    for mode in ("eager", "graph"):
+        st = DecodeStep(m, CFG, M=1, max_pos=MAX_POS, device=DEV)
+        assert st.attn_next
+        pos = MAX_POS - 5
+        st.fill_cache(pos, seed=29)
+        st.set_state([777], pos)
+        torch.cuda.synchronize()
+        seq = []
+        if mode == "eager":
+            for _ in range(4):
+                st.run()
+                torch.cuda.synchronize()
+                seq.append((np_(st.b.logits).copy(), np_(st.b.ids).copy(), np_(st.x_final.view(torch.int16)).copy()))
+        else:
+            graph = st.capture()          # step 1 runs eagerly while capturing
+            torch.cuda.synchronize()
+            seq.append((np_(st.b.logits).copy(), np_(st.b.ids).copy(), np_(st.x_final.view(torch.int16)).copy()))
+            for _ in range(3):
+                _ = torch.randn(4096, device=DEV).sum().item()
+                graph.replay()
+                torch.cuda.synchronize()
+                seq.append((np_(st.b.logits).copy(), np_(st.b.ids).copy(),
+                            np_(st.x_final.view(torch.int16)).copy()))
+        st.check_status()
+        runs[mode] = (seq, np_(st.b.kvk[:, pos:pos + 4]).copy(), np_(st.b.kvv[:, pos:pos + 4]).copy(),
+                      int(np_(st.b.dpos)[0]))
+        del st
+        torch.cuda.synchronize()
+    (se, ke, ve, de), (sg, kg, vg, dg) = runs["eager"], runs["graph"]
+    assert de == dg == MAX_POS - 1
+    for i, (a, b) in enumerate(zip(se, sg)):
+        assert all(np.array_equal(u, v) for u, v in zip(a, b)), f"step {i}: graph replay differs from eager"
+    assert np.array_equal(ke, kg) and np.array_equal(ve, vg), "KV rows differ"
+    log(f"  graph replays == eager steps (ids {[int(s[1][0]) for s in se]})")
