@@ -170,6 +170,23 @@ __device__ __forceinline__ void attn_partial_body(AttnLds<RT, FUSED>& L, const Q
                     vraw[c][kt][t] = vc[(int64_t)(s0 + min(kt * 32 + lq * 8 + t, rowmax)) * rs + c * 16];
     }
     const int base = *dpos;
+    // with a waiting q|k|v source: K / V as bf16 MFMA operands, decoded ahead
+    uint4 kdec[QSRC::kWaits ? 4 : 1], vdec[QSRC::kWaits ? 2 : 1][2];
+    auto decode_v = [&](int kt, int c) {
+        const uint32_t* v = vraw[c][kt];
+        return make_uint4(pack_bf16(kv_lut(lut, v[0]), kv_lut(lut, v[1])), pack_bf16(kv_lut(lut, v[2]), kv_lut(lut, v[3])),
+                          pack_bf16(kv_lut(lut, v[4]), kv_lut(lut, v[5])), pack_bf16(kv_lut(lut, v[6]), kv_lut(lut, v[7])));
+    };
+    auto decode_all = [&]() {
+        if constexpr (QSRC::kWaits) {
+#pragma unroll
+            for (int kt = 0; kt < 4; ++kt) kdec[kt] = kv8_bf16(lut, kraw[kt]);
+#pragma unroll
+            for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) vdec[kt][c] = decode_v(kt, c);
+        }
+    };
     if (!FUSED) {
         for (int i = tid; i < R * 16; i += 256) {
             const int r = i >> 4, c = i & 15;
@@ -218,7 +235,13 @@ __device__ __forceinline__ void attn_partial_body(AttnLds<RT, FUSED>& L, const Q
                 if (own || newrow) rcs[jm][lane] = hr::rope_cs(fz.theta, lane, base + jm);
             }
         };
-        if constexpr (QSRC::kWaits) rope_tables();
+        if constexpr (QSRC::kWaits) {
+            // the wait for q is long: decode the cache bytes to bf16 and build
+            // the RoPE tables before it, off the critical path
+            __syncthreads();   // lut
+            decode_all();
+            rope_tables();
+        }
         src.template fetch<QR, NR>(qo, ko, qa, qb, ka, kb);
         if constexpr (!QSRC::kWaits) rope_tables();
 #pragma unroll
@@ -305,17 +328,27 @@ __device__ __forceinline__ void attn_partial_body(AttnLds<RT, FUSED>& L, const Q
         const int kr = s0 + wave * 16 + l16;
         if (kr >= n_lo && kr < n_hi) {
 #pragma unroll
-            for (int kt = 0; kt < 4; ++kt) kraw[kt] = *reinterpret_cast<const uint2*>(&knew[kr - s0][kt * 32 + lq * 8]);
+            for (int kt = 0; kt < 4; ++kt) {
+                kraw[kt] = *reinterpret_cast<const uint2*>(&knew[kr - s0][kt * 32 + lq * 8]);
+                if constexpr (QSRC::kWaits) kdec[kt] = kv8_bf16(lut, kraw[kt]);   // decoded ahead: again
+            }
         }
 #pragma unroll
         for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int kt = 0; kt < 2; ++kt)
+            for (int kt = 0; kt < 2; ++kt) {
+                bool changed = false;
 #pragma unroll
                 for (int t = 0; t < 8; ++t) {
                     const int vr = s0 + kt * 32 + lq * 8 + t;
-                    if (vr >= n_lo && vr < n_hi) vraw[c][kt][t] = vnew[vr - s0][wave * 32 + l16 + c * 16];
+                    if (vr >= n_lo && vr < n_hi) {
+                        vraw[c][kt][t] = vnew[vr - s0][wave * 32 + l16 + c * 16];
+                        changed = true;
+                    }
                 }
+                if constexpr (QSRC::kWaits)
+                    if (changed) vdec[kt][c] = decode_v(kt, c);
+            }
     }
     // ---- 2. scores, wave = positions 16*wave + l16
     mx::v4f sacc[RT];
@@ -323,7 +356,9 @@ __device__ __forceinline__ void attn_partial_body(AttnLds<RT, FUSED>& L, const Q
     for (int rt = 0; rt < RT; ++rt) sacc[rt] = mx::v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-        const uint4 kb = kv8_bf16(lut, kraw[kt]);
+        uint4 kb;
+        if constexpr (QSRC::kWaits) kb = kdec[kt];
+        else kb = kv8_bf16(lut, kraw[kt]);
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt)
             sacc[rt] = mfma_bf16(*reinterpret_cast<const uint4*>(&qs[rt * 16 + l16][kt * 32 + lq * 8]), kb, sacc[rt]);
@@ -370,9 +405,8 @@ __device__ __forceinline__ void attn_partial_body(AttnLds<RT, FUSED>& L, const Q
         uint4 vb[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const uint32_t* v = vraw[c][kt];
-            vb[c] = make_uint4(pack_bf16(kv_lut(lut, v[0]), kv_lut(lut, v[1])), pack_bf16(kv_lut(lut, v[2]), kv_lut(lut, v[3])),
-                               pack_bf16(kv_lut(lut, v[4]), kv_lut(lut, v[5])), pack_bf16(kv_lut(lut, v[6]), kv_lut(lut, v[7])));
+            if constexpr (QSRC::kWaits) vb[c] = vdec[kt][c];
+            else vb[c] = decode_v(kt, c);
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
