@@ -312,8 +312,7 @@ __device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, 
         v[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(xi + mx::bf16_to_f32(mx::f32_to_bf16_rne(of[i]))));
         ss = fmaf(v[i], v[i], ss);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss = mx::wave_sum_butterfly(ss);   // the xor-32..1 butterfly of rmsnorm_lin_pq
     if (lane == 0) nred[wave] = ss;
     __syncthreads();
     const float var = ((nred[0] + nred[1]) + (nred[2] + nred[3])) / (float)2048;
@@ -753,8 +752,7 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
         v[i] = mx::bf16_to_f32(mx::f32_to_bf16_rne(xp + mx::bf16_to_f32(mx::f32_to_bf16_rne(yo[i]))));
         ss = fmaf(v[i], v[i], ss);
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    ss = mx::wave_sum_butterfly(ss);   // the xor-32..1 butterfly of rmsnorm_lin_pq
     if (lane == 0) nred[wave] = ss;
     __syncthreads();
     const float var = ((nred[0] + nred[1]) + (nred[2] + nred[3])) / (float)kMaxH;

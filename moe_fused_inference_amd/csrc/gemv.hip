@@ -477,8 +477,7 @@ __global__ __launch_bounds__(64 * R * S) void norm_lin_kernel(NormLinArgs a) {
             // the sum over the 256 threads in mxfp4_rmsnorm_quant's order
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-#pragma unroll
-                for (int o = 32; o >= 1; o >>= 1) ss[j] += __shfl_xor(ss[j], o);
+                ss[j] = mx::wave_sum_butterfly(ss[j]);
                 if (lane == 0) red[j][wave] = ss[j];
             }
         }

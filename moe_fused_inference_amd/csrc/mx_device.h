@@ -261,6 +261,31 @@ constexpr int kDppQuadNext2 = 0xEE;       // quad_perm [2,3,2,3]: lane q*4 reads
 constexpr int kDppRowHalfMirror = 0x141;  // lane i of 8 reads 7 - i
 constexpr int kDppRowMirror = 0x140;      // lane i of 16 reads 15 - i
 
+// The wave's sum by the butterfly xor 32, 16, 8, 4, 2, 1 (each lane adds
+// its partner's partial sum), in every lane: the bits of
+//     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+// with the lane exchanges kept in the VALU -- the gfx950 permlane swaps for
+// xor 32 and 16 (lanes of VDST's upper half / odd rows trade with VSRC's
+// lower half / even rows), a row rotation by 8, quad xor 3 then the half-row
+// mirror (lane i of 8 reads (7 - i) ^ 3 = i ^ 4), quad xor 2 and 1 -- instead
+// of six shuffles through the LDS path.
+__device__ __forceinline__ float wave_sum_butterfly(float v) {
+    const int lane = threadIdx.x & 63;
+    {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v += __uint_as_float(lane < 32 ? r[1] : r[0]);
+    }
+    {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+        v += __uint_as_float(((lane >> 4) & 1) ? r[0] : r[1]);
+    }
+    v += dpp<0x128>(v);                             // row_ror 8: lane i of 16 reads i ^ 8
+    v += dpp<kDppRowHalfMirror>(dpp<0x1B>(v));      // quad_perm [3,2,1,0], then the half-row mirror
+    v += dpp<kDppQuadXor2>(v);
+    v += dpp<kDppQuadXor1>(v);
+    return v;
+}
+
 // Reduction over each row of 16 lanes, the row's total in every lane of it.
 // Quad xor 1, quad xor 2, half-row mirror, row mirror: after the quad steps
 // every lane of a quad holds the same value, so the mirrors pair each quad

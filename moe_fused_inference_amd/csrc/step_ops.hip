@@ -66,8 +66,7 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const uint8_t* __restri
 // Sum over the 256 threads of a workgroup (4 waves): DPP/shuffle inside the
 // wave, then LDS across waves.  Deterministic order.
 __device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    v = mx::wave_sum_butterfly(v);
     const int wave = threadIdx.x >> 6;
     __syncthreads();   // red may still be read by a previous call
     if ((threadIdx.x & 63) == 0) red[wave] = v;
