@@ -642,20 +642,48 @@ def copy_reference(torch, nbytes=1 << 30, reps=4):
 
 
 STACK_SRC = os.path.join(ROOT, "moe_fused_inference_amd", "csrc", "decode_stack.hip")
+INCLUDE_DIRS = (os.path.join(ROOT, "moe_fused_inference_amd", "csrc"), os.path.join(ROOT, "include"))
+
+
+def source_files(path):
+    """`path` and every quoted header it includes, transitively (the files the
+    kernel's object is compiled from), in a fixed order."""
+    import re
+    seen, order, todo = set(), [], [path]
+    while todo:
+        f = todo.pop(0)
+        if f in seen:
+            continue
+        seen.add(f)
+        order.append(f)
+        with open(f) as fh:
+            for name in re.findall(r'^\s*#\s*include\s+"([^"]+)"', fh.read(), re.M):
+                for d in INCLUDE_DIRS:
+                    cand = os.path.join(d, name)
+                    if os.path.exists(cand):
+                        todo.append(cand)
+                        break
+    return order
 
 
 def source_sha256(path):
+    """SHA-256 over the kernel source and all the headers it includes (name and
+    bytes of each), so an edit to any of them marks a measurement stale."""
     import hashlib
-    with open(path, "rb") as f:
-        return hashlib.sha256(f.read()).hexdigest()
+    h = hashlib.sha256()
+    for f in source_files(path):
+        h.update(os.path.relpath(f, ROOT).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()
 
 
 def read_traffic():
     """HBM bytes per launch of the headline kernel (decode_stack_kernel, one
     launch = 48 layers) from the committed counter summary (key: value
     lines), and a note.  The summary records the SHA-256 of the kernel source
-    it measured; if that is not the current source, the figure is stale and
-    (None, note) is returned."""
+    and the headers it includes as measured; if that is not the current
+    source, the figure is stale and (None, note) is returned."""
     path = os.path.join(ROOT, "profiles", "decode_stack_traffic.txt")
     if not os.path.exists(path):
         return None, "no counter summary in profiles/"
@@ -666,7 +694,7 @@ def read_traffic():
                 k, v = line.split(":", 1)
                 kv[k.strip()] = v.strip()
     if kv.get("source_sha256") != source_sha256(STACK_SRC):
-        return None, "counter summary measured another version of decode_stack.hip (stale): not reported"
+        return None, "counter summary measured another version of decode_stack.hip or its headers (stale): not reported"
     if "hbm_bytes_per_launch" not in kv:
         return None, "counter summary has no hbm_bytes_per_launch"
     return int(float(kv["hbm_bytes_per_launch"])), ("FETCH_SIZE + WRITE_SIZE per launch of this decode_stack.hip "

@@ -52,3 +52,25 @@ def assert_close(y, ref, cos_min=COS_OP, rel_max=REL_OP, what=""):
 
 def dequant(q, s, k=None):
     return fmt.dequant_rows(np_(q), np_(s), k)
+
+
+def pool_layer(dext, n_exp, H, Mi, seed, chunk=16):
+    """One MoE layer of n_exp experts with seeded bf16 N(0, 0.02) weights,
+    quantized on the GPU by the bit-exact quantizer, stacked per projection as
+    config 2 holds them: gate/up (n_exp, Mi, H/2) + (n_exp, Mi, H/32), down
+    (n_exp, H, Mi/2) + (n_exp, H, Mi/32).  Experts are drawn `chunk` at a time."""
+    from moe_fused_inference_amd import moe_layer
+    g = torch.Generator(device=DEV)
+    g.manual_seed(seed)
+    t = {}
+    for nm, (n, k) in (("gate", (Mi, H)), ("up", (Mi, H)), ("down", (H, Mi))):
+        wps, wss = [], []
+        for e0 in range(0, n_exp, chunk):
+            c = min(chunk, n_exp - e0)
+            w = (torch.randn((c * n, k), generator=g, device=DEV) * 0.02).bfloat16()
+            q, s = dext.prequant(w)
+            wps.append(q.view(c, n, k // 2))
+            wss.append(s.view(c, n, k // 32))
+        t[nm + "_wp"] = torch.cat(wps).contiguous()
+        t[nm + "_ws"] = torch.cat(wss).contiguous()
+    return moe_layer.StackedExperts(**t)
