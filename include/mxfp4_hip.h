@@ -520,7 +520,12 @@ int mxfp4_route_tables(const int32_t* ids, int M, int k, const uint8_t* gate_wp,
  *   ids, w   int32 / fp32 (M, E) expert ids and routing weights
  *            (mxfp4_route_topk output); ids outside [0, n_experts)
  *            contribute nothing
- *   y        fp32 (M, H) MoE output
+ *   y        fp32 (M, H) MoE output, overwritten: the gate/up launch clears
+ *            it and the down launch adds two partial sums per element with
+ *            device-scope fp32 atomics (a fixed pair, so the result is
+ *            deterministic).  y must be ordinary device memory (not host-
+ *            mapped or fine-grained) and nothing may read or write it
+ *            between the entry's two launches.
  *   ws       mxfp4_moe_decode_batch_workspace_size(M, E, Mi) bytes, 16-byte
  *            aligned (the per-slot MXFP4 h; nothing persists)
  * Limits: 1 <= M <= 16, 1 <= E <= 8, H a multiple of 128, Mi of 32.  The
@@ -580,6 +585,12 @@ int mxfp4_moe_prefill(const void* x, const int64_t* topi, const uint16_t* scores
 int mxfp4_moe_prefill_tab(const void* x, const int64_t* topi, const uint16_t* scores,
                           const int64_t* expert_tab, int n_experts, int T, int topk, int H, int Mi,
                           void* out, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Test hook, no counterpart in the reference: for each of n_waves groups of
+ * 64 floats, every lane's wave sum as the RMSNorm kernels reduce it
+ * (permlane swaps + DPP, out_butterfly) and by the __shfl_xor butterfly
+ * (out_xor), so the GPU tests can pin the two as bit-identical. */
+int mxfp4_selftest_wave_sum(const float* in, float* out_butterfly, float* out_xor, int n_waves, void* stream);
 
 #ifdef __cplusplus
 }

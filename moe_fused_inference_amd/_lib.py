@@ -18,6 +18,7 @@ _c_sz = ctypes.c_size_t
 # name -> (restype, argtypes); keep in step with include/mxfp4_hip.h
 SIGNATURES = {
     "mxfp4_abi_version": (_c_i, []),
+    "mxfp4_selftest_wave_sum": (_c_i, [_c_p, _c_p, _c_p, _c_i, _c_p]),
     "mxfp4_last_error": (ctypes.c_char_p, []),
     "mxfp4_prequant": (_c_i, [_c_p, _c_i64, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p]),
     "mxfp4_quantize_rows": (_c_i, [_c_p, _c_i, _c_i, _c_i64, _c_i, _c_i, _c_i, _c_p, _c_p, _c_p]),
