@@ -24,9 +24,12 @@
 //   back each wave's MFMAs while the memory pipeline accepted them).  Every
 //   wave issues the same number of copies per step, so a step's arrival is a
 //   fixed vmcnt.
-// * Measured limit (MI355X): the K loop is bound by LDS bandwidth, about
-//   110 B/clk per CU: a step moves 68 KB into LDS and reads 192 KB of
-//   operands out of it, against ~1 us of MFMA work.
+// * Measured limit (MI355X, 4096 x 4096 x 2048, timing copies that drop one
+//   part): a 256-wide K step takes ~2.0 us, and each of its three parts
+//   alone takes 1.5-1.6 us -- the L2 -> LDS copies (68 KB per CU, ~42 GB/s
+//   per CU when all 256 CUs copy), the LDS operand reads with the MFMAs, and
+//   the MFMAs alone at the power-limited ~1.8 GHz clock (1.14 us) -- so the
+//   step is bound by all three at once, not by LDS bank conflicts (none).
 // * Scales: BK/32 bytes per row per step, loaded the same way (4 bytes per
 //   lane) and permuted once per step (v_perm_b32) so that op_sel = ks selects
 //   the byte of K-substep ks.
