@@ -920,11 +920,13 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const uint8_t* uw = a.up_wp + (int64_t)e * a.wp_stride_gu;
         const uint8_t* us = a.up_ws + (int64_t)e * a.ws_stride_gu;
 
-        // weights: 4 row groups (gate lo/hi, up lo/hi) x sa K-steps; lane
-        // group g owns blocks bpw*wave + sa*g .. +sa-1 of its row (contiguous)
+        // weights: 4 row groups (gate lo/hi, up lo/hi) x sa K-steps; step i
+        // takes blocks q0 + 4i .. q0 + 4i + 3 of the wave's K quarter (q0 =
+        // bpw*wave), lane group g block q0 + 4i + g: the four lanes of a row
+        // read 64 contiguous bytes per load (the order of decode_stack.hip)
         uint4 bq[4][4];
-        uint32_t bsc4[4];
-        const int blk0 = bpw * wave + sa * g;
+        uint32_t bsd[4][4];   // scale dwords of blocks q0 + 4i .. (byte g of dword i)
+        const int q0 = bpw * wave;
 #pragma unroll
         for (int G = 0; G < 4; ++G) {
             const int row = j0 + 16 * (G & 1) + r;
@@ -932,15 +934,19 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             const uint8_t* srow = ((G < 2) ? gs : us) + (int64_t)row * hb;
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int blk = min(blk0 + i, hb - 1);
+                const int blk = q0 + 4 * min(i, sa - 1) + g;
                 bq[G][i] = ld_sel(reinterpret_cast<const uint4*>(wrow + blk * 16), i < sa, make_uint4(0, 0, 0, 0));
             }
-            // scale bytes blk0..blk0+sa-1 (sa <= 4) from the two dwords around
-            // them; bytes past sa belong to zero data and are ignored
-            const int d0 = blk0 & ~3;
-            const uint32_t lo = *reinterpret_cast<const uint32_t*>(srow + d0);
-            const uint32_t hi = *reinterpret_cast<const uint32_t*>(srow + min(d0 + 4, hb - 4));
-            bsc4[G] = (uint32_t)((((uint64_t)hi << 32) | lo) >> (8 * (blk0 & 3)));
+            if (sa == 4) {   // the quarter's 16 scale bytes in one load (H = 2048)
+                const uint4 v = *reinterpret_cast<const uint4*>(srow + q0);
+                bsd[G][0] = v.x;
+                bsd[G][1] = v.y;
+                bsd[G][2] = v.z;
+                bsd[G][3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bsd[G][i] = *reinterpret_cast<const uint32_t*>(srow + q0 + 4 * min(i, sa - 1));
+            }
         }
 
         // x -> three E4M3 terms in LDS (whole row; 8 values per thread)
@@ -964,22 +970,24 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         if (threadIdx.x < 2) sm.a.zero[threadIdx.x] = make_uint4(0, 0, 0, 0);
         __syncthreads();
 
-        // MFMA: step i covers blocks {bpw*wave + sa*gb + i : gb = 0..3}.
-        // Operands first, then the MFMAs.  A zero operand is read from the
-        // zero region (an address select), not selected after the read: a
-        // value select compiles to branches that serialise the LDS reads.
+        // MFMA: step i covers blocks {q0 + 4i + gb : gb = 0..3}; A lane group g
+        // holds K [16g, +16) and [64 + 16g, +16) of the step, i.e. halves
+        // (g & 1) of blocks 4i + (g >> 1) and 4i + 2 + (g >> 1), with block
+        // 4i + g's scale.  Operands first, then the MFMAs.  A zero operand is
+        // read from the zero region (an address select), not selected after the
+        // read: a value select compiles to branches that serialise the LDS reads.
         mx::v8i av[4];
         uint32_t asc[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int base = bpw * wave + min(i, sa - 1);
+            const int base = q0 + 4 * min(i, sa - 1);
             const bool ok = r < kTerms && i < sa;
-            const uint4* plo = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (g >> 1)) * 32 + 16 * (g & 1)])
+            const uint4* plo = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + (g >> 1)) * 32 + 16 * (g & 1)])
                                   : &sm.a.zero[0];
-            const uint4* phi = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + sa * (2 + (g >> 1))) * 32 + 16 * (g & 1)])
+            const uint4* phi = ok ? reinterpret_cast<const uint4*>(&sm.a.x8[rr][(base + 2 + (g >> 1)) * 32 + 16 * (g & 1)])
                                   : &sm.a.zero[1];
             av[i] = cat8(*plo, *phi);
-            const uint32_t c = sm.a.xsc[rr][base + sa * g];
+            const uint32_t c = sm.a.xsc[rr][base + g];
             asc[i] = ok ? c : 127u;
         }
         mx::v4f acc[4];
@@ -989,7 +997,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int G = 0; G < 4; ++G)
-                acc[G] = mx::mfma16_fp8a_fp4b(av[i], bq[G][i], acc[G], asc[i], (bsc4[G] >> (8 * i)) & 0xFFu);
+                acc[G] = mx::mfma16_fp8a_fp4b(av[i], bq[G][i], acc[G], asc[i], (bsd[G][i] >> (8 * g)) & 0xFFu);
 #pragma unroll
         for (int G = 0; G < 4; ++G) mx::pin(acc[G]);   // complete the chain before the lane < 16 branch
         // rows 0..2 of D (the three terms) are elements 0..2 of lanes 0..15
@@ -1057,8 +1065,9 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
     int* memo = reinterpret_cast<int*>(a.ws + kMemoBOff) + cb;
     const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
     const int launch = *memo;
-    // wave handles slots 2*wave, 2*wave+1; lane group g owns blocks
-    // g*steps .. g*steps+steps-1 of its row
+    // wave handles slots 2*wave, 2*wave+1; step i takes blocks 4i .. 4i + 3
+    // of the Mi row, lane group g block 4i + g (64 contiguous bytes per row
+    // and load; the order of decode_stack.hip)
     int slot[2], eid[2];
     float wgt[2];
 #pragma unroll
@@ -1070,7 +1079,7 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         wgt[q] = kLogitRoute ? __shfl(rw, sl) : ROUTE == ROUTE_DEV_IDS ? a.w_dev[sl] : pick_w(a, sl);
     }
     uint4 bq[2][MS];
-    uint32_t bsw[2][3];   // dwords holding the scale bytes of blocks g*steps..
+    uint32_t bsc[2][MS];   // the scale byte of block 4i + g
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
         const bool live = slot[q] < a.E;
@@ -1078,25 +1087,19 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         const uint8_t* srow = a.down_ws + (int64_t)eid[q] * a.ws_stride_dn + (int64_t)(c0 + r) * kb;
 #pragma unroll
         for (int i = 0; i < MS; ++i) {
-            const int blk = g * steps + i;
+            const int blk = 4 * i + g;
             bq[q][i] = ld_sel(reinterpret_cast<const uint4*>(wrow + min(blk, kb - 1) * 16),
                               live && i < steps && blk < kb, make_uint4(0, 0, 0, 0));
         }
-        const int sb0 = (g * steps) & ~3;  // blocks [g*steps, +steps) lie in 12 bytes from here
         if ((kb & 3) == 0) {
 #pragma unroll
-            for (int d = 0; d < 3; ++d)  // raw dwords; blocks past the row are masked by zero data
-                bsw[q][d] = *reinterpret_cast<const uint32_t*>(srow + min(sb0 + 4 * d, kb - 4));
+            for (int i = 0; i < MS; ++i)  // dword i holds blocks 4i .. 4i + 3; past the row: zero data
+                bsc[q][i] = (*reinterpret_cast<const uint32_t*>(srow + 4 * min(i, (kb >> 2) - 1)) >> (8 * g)) & 0xFFu;
         } else {  // rows not a dword multiple: byte loads, never past the row
 #pragma unroll
-            for (int d = 0; d < 3; ++d) {
-                uint32_t v = 0;
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    const int off = sb0 + 4 * d + b;
-                    v |= ((live && off < kb) ? (uint32_t)srow[off] : 127u) << (8 * b);
-                }
-                bsw[q][d] = v;
+            for (int i = 0; i < MS; ++i) {
+                const int off = 4 * i + g;
+                bsc[q][i] = (live && off < kb) ? (uint32_t)srow[off] : 127u;
             }
         }
     }
@@ -1182,7 +1185,6 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
 
     float part = 0.0f;  // this lane's (lane < 16) partial combine over its slots
     if (!abort) {
-        const int sb0 = (g * steps) & ~3;
         bool live[2];
         const uint8_t* h8[2];
         const uint32_t* hsq[2];
@@ -1198,17 +1200,14 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
         // step (independent accumulators).  Zero operands come from the zero
         // region: an address select, no branch between the LDS reads.
         mx::v8i av[2][MS];
-        uint32_t asc[2][MS], bsc[2][MS];
+        uint32_t asc[2][MS];
 #pragma unroll
         for (int i = 0; i < MS; ++i) {
-            // step i: B lane group gb holds block gb*steps + i
-            const int blo = (g >> 1) * steps + i;
-            const int bhi = (2 + (g >> 1)) * steps + i;
-            const int bown = g * steps + i;
+            // step i: B lane group gb holds block 4i + gb (see the gate/up operands)
+            const int blo = 4 * i + (g >> 1);
+            const int bhi = 4 * i + 2 + (g >> 1);
+            const int bown = 4 * i + g;
             const bool rok = r < kTerms && i < steps;
-            // weight scale byte of block g*steps+i from the aligned dwords
-            // (blocks past the row carry zero data, so any scale is fine)
-            const int bi = g * steps + i - sb0;           // 0..10
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 const bool ok = rok && live[q];
@@ -1219,8 +1218,6 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                 const uint32_t* pc = (ok && bown < kb) ? &hsq[q][bown] : &sm.b.code127[0];
                 av[q][i] = cat8(*plo, *phi);
                 asc[q][i] = (*pc >> (8 * rr)) & 0xFFu;
-                const uint32_t wd = bi < 4 ? bsw[q][0] : (bi < 8 ? bsw[q][1] : bsw[q][2]);
-                bsc[q][i] = (wd >> (8 * (bi & 3))) & 0xFFu;
             }
         }
         mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};

@@ -338,15 +338,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
     const int kb = Mi >> 5;                    // 32-blocks along Mi
     const int steps = (kb + 3) >> 2;           // down K steps
 
-    // ---- gate/up weights: K quarter cw (blocks bpw*cw ..) of tiles jj + 16m.
-    // Offsets of tiles past the last are out of the descriptor's range: their
-    // loads return zeros without touching memory.
+    // ---- gate/up weights: K quarter cw (blocks q0 = bpw*cw ..) of tiles jj + 16m.
+    // MFMA step i takes blocks q0 + 4i .. q0 + 4i + 3, lane group g block
+    // q0 + 4i + g: the four lanes of a row read 64 contiguous bytes per load
+    // (with lane group g on blocks q0 + sa*g + i, 16-byte pieces 64 bytes
+    // apart, a set's per-layer burst took twice as long).  Offsets of tiles
+    // past the last are out of the descriptor's range: their loads return
+    // zeros without touching memory.
     constexpr uint32_t kNone = 0x80000000u;
     const int bpw = hb >> 2;
     const int sa = bpw >> 2;
-    const int blk0 = bpw * cw + sa * g;
+    const int q0 = bpw * cw;
     uint4 bq[NT][4];
-    uint32_t bslo[NT], bshi[NT];
+    uint32_t bs[NT][4];   // scale dwords of blocks q0 + 4i .. q0 + 4i + 3 (byte g of dword i)
     uint32_t woff[NT], soff[NT];
     bool tup[NT];
 #pragma unroll
@@ -355,10 +359,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         const bool ok = t < ntile;
         tup[m] = t >= (ntile >> 1);
         const int row = 16 * (tup[m] ? t - (ntile >> 1) : t) + r;
-        woff[m] = ok ? (uint32_t)(row * (H >> 1) + blk0 * 16) : kNone;
-        soff[m] = ok ? (uint32_t)(row * hb + (blk0 & ~3)) : kNone;
+        woff[m] = ok ? (uint32_t)(row * (H >> 1) + (q0 + g) * 16) : kNone;
+        soff[m] = ok ? (uint32_t)(row * hb + q0) : kNone;
     }
-    const uint32_t shi = (uint32_t)(min((blk0 & ~3) + 4, hb - 4) - (blk0 & ~3));
     // valid = false: a zero-extent descriptor, so the loads return zeros
     // without touching memory
     auto load_gu = [&](int l, bool valid) {
@@ -372,17 +375,27 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         for (int m = 0; m < NT; ++m) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw[tup[m]], woff[m] + 16 * min(i, sa - 1), 0, 0);
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw[tup[m]], woff[m] + 64 * min(i, sa - 1), 0, 0);
                 bq[m][i] = make_uint4(v.x, v.y, v.z, v.w);
             }
-            bslo[m] = __builtin_amdgcn_raw_buffer_load_b32(rs[tup[m]], soff[m], 0, 0);
-            bshi[m] = __builtin_amdgcn_raw_buffer_load_b32(rs[tup[m]], soff[m] + shi, 0, 0);
+            if (sa == 4) {   // the quarter's 16 scale bytes in one load (H = 2048)
+                const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs[tup[m]], soff[m], 0, 0);
+                bs[m][0] = v.x;
+                bs[m][1] = v.y;
+                bs[m][2] = v.z;
+                bs[m][3] = v.w;
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    bs[m][i] = __builtin_amdgcn_raw_buffer_load_b32(rs[tup[m]], soff[m] + 4 * min(i, sa - 1), 0, 0);
+            }
         }
     };
     // ---- down weights: column tiles cw and cw + 4 (16 columns each) of the
-    // workgroup's columns
-    const int sb0 = (g * steps) & ~3;
-    const int ilast = min(steps, kb - g * steps) - 1;   // last in-row step of this lane group (may be < 0)
+    // workgroup's columns.  Step i takes blocks 4i .. 4i + 3 of the Mi row,
+    // lane group g block 4i + g (64 contiguous bytes per row and load);
+    // blocks past the row reload its last block (finite data, valid scale)
+    // against zero activations.
     bool dok[2];
     uint32_t woffd[2], soffd[2];
 #pragma unroll
@@ -390,11 +403,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         const int ct = cw + 4 * k;
         dok[k] = ct < nct;
         const int drow = c0d + 16 * ct + r;
-        woffd[k] = dok[k] ? (uint32_t)(drow * (Mi >> 1) + g * steps * 16) : kNone;
+        woffd[k] = dok[k] ? (uint32_t)(drow * (Mi >> 1)) : kNone;
         soffd[k] = dok[k] ? (uint32_t)(drow * kb) : kNone;
     }
     uint4 dq[2][MS];
-    uint32_t dsw[2][3];
+    uint32_t dsc[2][MS];   // scale byte of block 4i + g (KB4: its dword, byte g)
     auto load_dn = [&](int l, bool valid) {
         const int e = route_id(l);
         const __amdgpu_buffer_rsrc_t rw = rsrc(route_ptr(l, 2) + (int64_t)e * a.wp_stride_dn, valid ? H * (Mi >> 1) : 0);
@@ -403,23 +416,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         for (int k = 0; k < 2; ++k) {
 #pragma unroll
             for (int i = 0; i < MS; ++i) {
-                const v4u q = __builtin_amdgcn_raw_buffer_load_b128(rw, woffd[k] + 16 * max(0, min(i, ilast)), 0, 0);
+                const v4u q = __builtin_amdgcn_raw_buffer_load_b128(rw, woffd[k] + 16 * min(4 * i + g, kb - 1), 0, 0);
                 dq[k][i] = make_uint4(q.x, q.y, q.z, q.w);
             }
-            if (KB4) {
 #pragma unroll
-                for (int d = 0; d < 3; ++d)
-                    dsw[k][d] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + min(sb0 + 4 * d, kb - 4), 0, 0);
-            } else {
-#pragma unroll
-                for (int d = 0; d < 3; ++d) {
-                    uint32_t w = 0;
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
-                        w |= (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(rs, soffd[k] + min(sb0 + 4 * d + q, kb - 1), 0, 0)
-                             << (8 * q);
-                    dsw[k][d] = w;
-                }
+            for (int i = 0; i < MS; ++i) {
+                if (KB4) dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + 4 * min(i, (kb >> 2) - 1), 0, 0);
+                else dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b8(rs, soffd[k] + min(4 * i + g, kb - 1), 0, 0);
             }
         }
     };
@@ -506,24 +509,26 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             uint32_t asc[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int base = bpw * cw + min(i, sa - 1);
+                // step i, blocks q0 + 4i + gb: A lane group g holds K [16g, +16) and [64 + 16g, +16) of
+                // the step, i.e. halves (g & 1) of blocks 4i + (g >> 1) and 4i + 2 + (g >> 1); its scale is
+                // block 4i + g's
+                const int base = q0 + 4 * min(i, sa - 1);
                 const bool ok = r < kTerms && i < sa;
-                const uint4* plo = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + sa * (g >> 1)) * kRecBytes + 32 * rr + 16 * (g & 1))
+                const uint4* plo = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + (g >> 1)) * kRecBytes + 32 * rr + 16 * (g & 1))
                                       : &sm.zero[0];
-                const uint4* phi = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + sa * (2 + (g >> 1))) * kRecBytes + 32 * rr + 16 * (g & 1))
+                const uint4* phi = ok ? reinterpret_cast<const uint4*>(sm.xr + (base + 2 + (g >> 1)) * kRecBytes + 32 * rr + 16 * (g & 1))
                                       : &sm.zero[1];
                 av[i] = cat8(*plo, *phi);
-                const uint32_t c = sm.xr[(base + sa * g) * kRecBytes + 96 + rr];
+                const uint32_t c = sm.xr[(base + g) * kRecBytes + 96 + rr];
                 asc[i] = ok ? c : 127u;
             }
             mx::v4f acc[NT];
 #pragma unroll
             for (int m = 0; m < NT; ++m) {
                 acc[m] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
-                const uint64_t sc8 = (((uint64_t)bshi[m] << 32) | bslo[m]) >> (8 * (blk0 & 3));
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    acc[m] = mx::mfma16_fp8a_fp4b(av[i], bq[m][i], acc[m], asc[i], (uint32_t)(sc8 >> (8 * i)) & 0xFFu);
+                    acc[m] = mx::mfma16_fp8a_fp4b(av[i], bq[m][i], acc[m], asc[i], (bs[m][i] >> (8 * g)) & 0xFFu);
             }
 #pragma unroll
             for (int m = 0; m < NT; ++m) mx::pin(acc[m]);
@@ -589,9 +594,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
             for (int i = 0; i < MS; ++i) {
-                const int blo = (g >> 1) * steps + i;
-                const int bhi = (2 + (g >> 1)) * steps + i;
-                const int bown = g * steps + i;
+                // step i, blocks 4i + gb (see the gate/up operands)
+                const int blo = 4 * i + (g >> 1);
+                const int bhi = 4 * i + 2 + (g >> 1);
+                const int bown = 4 * i + g;
                 const bool rok = r < kTerms && i < steps;
                 const uint4* plo = (rok && blo < kb) ? reinterpret_cast<const uint4*>(h8 + blo * kRecBytes + 16 * (g & 1))
                                                      : &sm.zero[0];
@@ -601,11 +607,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                                                        : reinterpret_cast<const uint8_t*>(&sm.code127[0]);
                 const mx::v8i av = cat8(*plo, *phi);
                 const uint32_t asc = *pc;
-                const int bi = g * steps + i - sb0;
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
-                    const uint32_t wd = bi < 4 ? dsw[k][0] : (bi < 8 ? dsw[k][1] : dsw[k][2]);
-                    acc[k] = mx::mfma16_fp8a_fp4b(av, dq[k][i], acc[k], asc, (wd >> (8 * (bi & 3))) & 0xFFu);
+                    const uint32_t bsc = KB4 ? (dsc[k][i] >> (8 * g)) & 0xFFu : dsc[k][i] & 0xFFu;
+                    acc[k] = mx::mfma16_fp8a_fp4b(av, dq[k][i], acc[k], asc, bsc);
                 }
             }
 #pragma unroll
