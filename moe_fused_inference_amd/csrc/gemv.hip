@@ -31,13 +31,22 @@ namespace {
 constexpr int kMaxT = MXFP4_MAX_TABLE;
 constexpr int kSeg = 4;  // MFMA K-steps (512 K) per prefetch segment
 
+// A host table also carries its grouping, worked out on the host (the
+// pointers are there already): info[t] = n | (f << 8), n entries share entry
+// t's weights when t is the first of them (n = 0 otherwise), listed at
+// mem[f ..].  The kernel then starts on its weights after one scalar load
+// instead of a scan of the table (a dependent memory round trip).
 struct HostTable {
+    static constexpr bool kGrouped = true;
     const uint8_t* wp[kMaxT];
     const uint8_t* ws[kMaxT];
+    uint32_t info[kMaxT];
+    uint8_t mem[kMaxT];
     __device__ __forceinline__ const uint8_t* w(int i) const { return wp[i]; }
     __device__ __forceinline__ const uint8_t* s(int i) const { return ws[i]; }
 };
 struct DevTable {
+    static constexpr bool kGrouped = false;
     const int64_t* wp;
     const int64_t* ws;
     __device__ __forceinline__ const uint8_t* w(int i) const { return reinterpret_cast<const uint8_t*>(wp[i]); }
@@ -168,7 +177,16 @@ __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, Gemv
     const uint8_t* ws = tab.s(t);
 
     // ---- grouping: the first entry with this weight owns all of its rows
-    if (threadIdx.x < 64) {
+    if constexpr (Tab::kGrouped) {
+        const uint32_t info = tab.info[t];
+        const int n = (int)(info & 0xFFu);
+        if (n == 0) return;   // a later entry of a group: its owner serves it
+        if ((int)threadIdx.x < n) s_rows[threadIdx.x] = n == 1 ? t : tab.mem[(info >> 8) + threadIdx.x];
+        if (threadIdx.x == 0) {
+            s_first = 1;
+            s_cnt = n;
+        }
+    } else if (threadIdx.x < 64) {
         bool dup = false;
         for (int j = lane; j < t; j += 64) dup |= (tab.w(j) == wp) && (tab.s(j) == ws);
         const bool any = __ballot(dup) != 0ull;
@@ -230,11 +248,23 @@ __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, Gemv
             const int k0 = (u - rr * upr) * 8;
             const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
             const float* grow = a.gu + (int64_t)em.src * 2 * a.K;
+            if ((a.K & 7) == 0 && k0 + 8 <= a.K && (((uintptr_t)a.gu) & 15) == 0) {
+                // 16-byte loads: g and u of the thread's 8 values (rows of 2K floats, K % 8 == 0)
+                const float4 g0 = *reinterpret_cast<const float4*>(grow + k0);
+                const float4 g1 = *reinterpret_cast<const float4*>(grow + k0 + 4);
+                const float4 u0 = *reinterpret_cast<const float4*>(grow + a.K + k0);
+                const float4 u1 = *reinterpret_cast<const float4*>(grow + a.K + k0 + 4);
+                pg[0] = g0.x; pg[1] = g0.y; pg[2] = g0.z; pg[3] = g0.w;
+                pg[4] = g1.x; pg[5] = g1.y; pg[6] = g1.z; pg[7] = g1.w;
+                pu[0] = u0.x; pu[1] = u0.y; pu[2] = u0.z; pu[3] = u0.w;
+                pu[4] = u1.x; pu[5] = u1.y; pu[6] = u1.z; pu[7] = u1.w;
+            } else {
 #pragma unroll
-            for (int i = 0; i < 8; ++i) {   // clamped: every load issued before any is used
-                const int k = min(k0 + i, a.K - 1);
-                pg[i] = grow[k];
-                pu[i] = grow[a.K + k];
+                for (int i = 0; i < 8; ++i) {   // clamped: every load issued before any is used
+                    const int k = min(k0 + i, a.K - 1);
+                    pg[i] = grow[k];
+                    pu[i] = grow[a.K + k];
+                }
             }
         }
         if (sb < se) load_seg<AMODE>(s0buf, cx, 0);   // the weights stream while h is built
@@ -613,6 +643,21 @@ int run_host_table(const uint8_t* const* wp_tab, const uint8_t* const* ws_tab, i
         }
         for (int i = 0; i < n; ++i)
             MXH_REQUIRE(tab.wp[i] && tab.ws[i], "pointer table entry %d is null", c0 + i);
+        // grouping: entries with equal (weight, scale) pointers, in table order
+        int nm = 0;
+        for (int i = 0; i < kMaxT; ++i) {
+            tab.info[i] = 0;
+            tab.mem[i] = 0;
+        }
+        for (int i = 0; i < n; ++i) {
+            bool seen = false;
+            for (int j = 0; j < i && !seen; ++j) seen = tab.wp[j] == tab.wp[i] && tab.ws[j] == tab.ws[i];
+            if (seen) continue;
+            const int f = nm;
+            for (int j = i; j < n; ++j)
+                if (tab.wp[j] == tab.wp[i] && tab.ws[j] == tab.ws[i]) tab.mem[nm++] = (uint8_t)j;
+            tab.info[i] = (uint32_t)(nm - f) | ((uint32_t)f << 8);
+        }
         a.T = n;
         a.t0 = c0;
         const int rc = launch_gemv(tab, a, amode, st);
