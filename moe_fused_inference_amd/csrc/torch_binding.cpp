@@ -47,16 +47,35 @@ uint8_t* u8m(const torch::Tensor& t) { return static_cast<uint8_t*>(t.data_ptr()
 float* f32(const torch::Tensor& t) { return static_cast<float*>(t.data_ptr()); }
 
 // Host pointer table of cuda uint8 tensors (the checks of
-// src/ext/mxfp4_decode_binding.cpp:44-60).
-std::vector<const uint8_t*> ptr_table(const std::vector<torch::Tensor>& ts) {
-    require(!ts.empty(), "empty pointer table");
-    std::vector<const uint8_t*> p;
-    p.reserve(ts.size());
-    for (const auto& t : ts) {
+// src/ext/mxfp4_decode_binding.cpp:44-60), read straight from the Python
+// list (or tuple): no std::vector<Tensor> of reference-counted copies, and the
+// pointer array is a per-thread buffer reused from call to call (slot 0 = the
+// packed data table, 1 = the scale table).  cols0 = size(1) of the first entry.
+struct PtrTable {
+    const uint8_t* const* p;
+    int64_t cols0;
+};
+
+PtrTable ptr_table(const py::handle& seq, int slot, int64_t expect, const char* count_msg) {
+    PyObject* fast = PySequence_Fast(seq.ptr(), "pointer table must be a list of tensors");
+    if (fast == nullptr) throw py::error_already_set();
+    const py::object keep = py::reinterpret_steal<py::object>(fast);
+    const Py_ssize_t n = PySequence_Fast_GET_SIZE(fast);
+    require((int64_t)n == expect, count_msg);
+    require(n > 0, "empty pointer table");
+    thread_local std::vector<const uint8_t*> buf[2];
+    std::vector<const uint8_t*>& p = buf[slot];
+    p.resize((size_t)n);
+    PyObject** items = PySequence_Fast_ITEMS(fast);
+    int64_t cols0 = 0;
+    for (Py_ssize_t i = 0; i < n; ++i) {
+        require(THPVariable_Check(items[i]), "ptr table entries must be cuda uint8");
+        const at::Tensor& t = THPVariable_Unpack(items[i]);
         require(t.is_cuda() && t.scalar_type() == torch::kUInt8, "ptr table entries must be cuda uint8");
-        p.push_back(u8(t));
+        if (i == 0) cols0 = t.dim() >= 2 ? t.size(1) : 0;
+        p[(size_t)i] = static_cast<const uint8_t*>(t.data_ptr());
     }
-    return p;
+    return {p.data(), cols0};
 }
 
 int dtype_code(c10::ScalarType s) {
@@ -120,32 +139,31 @@ torch::Tensor lin_pq(torch::Tensor xq, torch::Tensor xsc, torch::Tensor wp, torc
 }
 
 // Grouped gate+up over a token-major table of 2E*M weights -> f32 (M*E, 2N).
-torch::Tensor moe_gateup(torch::Tensor xq, torch::Tensor xsc, const std::vector<torch::Tensor>& wps,
-                         const std::vector<torch::Tensor>& wscs, int64_t E_, int64_t M_, int64_t N_,
-                         int64_t K_) {
+torch::Tensor moe_gateup(torch::Tensor xq, torch::Tensor xsc, const py::object& wps, const py::object& wscs,
+                         int64_t E_, int64_t M_, int64_t N_, int64_t K_) {
     const int E = (int)E_, M = (int)M_, N = (int)N_, K = (int)K_;
-    require((int64_t)wps.size() == 2 * E_ * M_, "wps must be 2E*M");
-    require((int64_t)wscs.size() == 2 * E_ * M_, "wscs must be 2E*M");
-    const int Kp = (int)wps[0].size(1) * 2;
-    const auto tw = ptr_table(wps), ts = ptr_table(wscs);
+    require((int64_t)py::len(wps) == 2 * E_ * M_, "wps must be 2E*M");
+    require((int64_t)py::len(wscs) == 2 * E_ * M_, "wscs must be 2E*M");
+    const PtrTable tw = ptr_table(wps, 0, 2 * E_ * M_, "wps must be 2E*M");
+    const PtrTable ts = ptr_table(wscs, 1, 2 * E_ * M_, "wscs must be 2E*M");
+    const int Kp = (int)tw.cols0 * 2;
     auto gu = torch::empty({(int64_t)M * E, 2 * N}, xq.options().dtype(torch::kFloat32));
-    check(mxfp4_moe_gateup(u8(xq), u8(xsc), tw.data(), ts.data(), f32(gu), E, M, N, K, Kp, stream_of(xq)),
-          "moe_gateup");
+    check(mxfp4_moe_gateup(u8(xq), u8(xsc), tw.p, ts.p, f32(gu), E, M, N, K, Kp, stream_of(xq)), "moe_gateup");
     return gu;
 }
 
 // Fused silu(gate)*up -> MXFP4 -> down over E*M weights -> f32 (M*E, N).
-torch::Tensor moe_down(torch::Tensor gu, const std::vector<torch::Tensor>& wps,
-                       const std::vector<torch::Tensor>& wscs, int64_t E_, int64_t M_, int64_t N_,
-                       int64_t K_) {
+torch::Tensor moe_down(torch::Tensor gu, const py::object& wps, const py::object& wscs, int64_t E_, int64_t M_,
+                       int64_t N_, int64_t K_) {
     const int E = (int)E_, M = (int)M_, N = (int)N_, K = (int)K_;
-    require((int64_t)wps.size() == E_ * M_, "wps must be E*M");
-    const int Kp = (int)wps[0].size(1) * 2;
+    require((int64_t)py::len(wps) == E_ * M_, "wps must be E*M");
     require(gu.size(0) == (int64_t)M * E && gu.size(1) == 2 * (int64_t)K, "gu (M*E,2K)");
-    const auto tw = ptr_table(wps), ts = ptr_table(wscs);
+    const PtrTable tw = ptr_table(wps, 0, E_ * M_, "wps must be E*M");
+    const PtrTable ts = ptr_table(wscs, 1, E_ * M_, "wscs must be E*M");
+    const int Kp = (int)tw.cols0 * 2;
     gu = gu.contiguous();
     auto yd = torch::empty({(int64_t)M * E, N}, gu.options());
-    check(mxfp4_moe_down(f32(gu), tw.data(), ts.data(), f32(yd), E, M, N, K, Kp, stream_of(gu)), "moe_down");
+    check(mxfp4_moe_down(f32(gu), tw.p, ts.p, f32(yd), E, M, N, K, Kp, stream_of(gu)), "moe_down");
     return yd;
 }
 
