@@ -444,9 +444,14 @@ def bench_step(torch, layers, M, steps=128):
                     "MoE blocks replayed alone / the step"}
 
 
-def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
-    """Config 4: M=9 tokens, Zipf(1.1)-biased routing over 128 experts, grouped
-    drop-in path (moe_gateup + moe_down + moe_combine)."""
+def bench_spec_verify(torch, dext, layers, beta, seed, reps=5):
+    """Config 4: M=9 tokens, Zipf(1.1)-biased routing over 128 experts, through
+    the grouped drop-in path (moe_gateup + moe_down + moe_combine) and through
+    mxfp4_moe_decode_batch.  The headline figures run the verify step's MoE
+    over all resident layers in turn (one graph of len(layers) calls, the same
+    routing in every layer), so each call streams its experts from HBM as a
+    verify step through the model does; `*_one_layer` repeats one layer, whose
+    41 experts (103 MB) then sit in the 256 MB memory-side cache."""
     import numpy as np
     M = 9
     rng = np.random.default_rng(seed)
@@ -463,51 +468,69 @@ def bench_spec_verify(torch, dext, lay, beta, seed, reps=20):
     g.manual_seed(seed)
     x = torch.randn((M, H), generator=g, device="cuda").bfloat16()
     xq, xs = dext.prequant(x)
-    gw, gs, dw, ds = [], [], [], []
-    for m in range(M):
-        row = ids[m * TOPK:(m + 1) * TOPK]
-        gw += [lay.gate_wp[e] for e in row] + [lay.up_wp[e] for e in row]
-        gs += [lay.gate_ws[e] for e in row] + [lay.up_ws[e] for e in row]
-        dw += [lay.down_wp[e] for e in row]
-        ds += [lay.down_ws[e] for e in row]
 
-    def fn():
+    def tables(lay):
+        gw, gs, dw, ds = [], [], [], []
+        for m in range(M):
+            row = ids[m * TOPK:(m + 1) * TOPK]
+            gw += [lay.gate_wp[e] for e in row] + [lay.up_wp[e] for e in row]
+            gs += [lay.gate_ws[e] for e in row] + [lay.up_ws[e] for e in row]
+            dw += [lay.down_wp[e] for e in row]
+            ds += [lay.down_ws[e] for e in row]
+        return gw, gs, dw, ds
+
+    tabs = [tables(lay) for lay in layers]
+
+    def dropin(i):
+        gw, gs, dw, ds = tabs[i]
         gu = dext.moe_gateup(xq, xs, gw, gs, TOPK, M, MI, H)
         yd = dext.moe_down(gu, dw, ds, TOPK, M, H, MI)
         return dext.moe_combine(yd, tv, M)
 
-    fn()
-    torch.cuda.synchronize()
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        fn()
-        torch.cuda.synchronize()
-        with torch.cuda.graph(graph, stream=side):
-            fn()
-    ms = time_graph(torch, graph, reps, 3)
-    byts = distinct * EXPERT_BYTES
-    # the same step through mxfp4_moe_decode_batch (two launches, each routed expert read once)
     from moe_fused_inference_amd.moe_layer import decode_batch
+    from moe_fused_inference_amd import _lib
     ids32 = ti.to(torch.int32).cuda().contiguous()
     yb = torch.empty((M, H), dtype=torch.float32, device="cuda")
-    from moe_fused_inference_amd import _lib
     wsb = torch.empty(_lib.load().mxfp4_moe_decode_batch_workspace_size(M, TOPK, MI), dtype=torch.uint8, device="cuda")
-    decode_batch(xq, xs, ids32, tv, lay, out=yb, ws=wsb)
-    ref = fn()
+
+    def batched(i):
+        decode_batch(xq, xs, ids32, tv, layers[i], out=yb, ws=wsb)
+
+    # the batched path against the drop-in chain (summation order only)
+    ref = dropin(0)
+    batched(0)
     torch.cuda.synchronize()
     rel = float((yb - ref).abs().max() / ref.abs().max())
     if rel > 1e-5:
         raise RuntimeError(f"spec verify: batched MoE differs from the drop-in chain (max rel {rel:.3g})")
-    gb = torch.cuda.CUDAGraph()
-    with torch.cuda.stream(side):
-        with torch.cuda.graph(gb, stream=side):
-            decode_batch(xq, xs, ids32, tv, lay, out=yb, ws=wsb)
-    ms_b = time_graph(torch, gb, reps, 3)
-    return {"beta": beta, "distinct_experts": distinct, "us": round(ms * 1e3, 2),
-            "gbs": round(byts / (ms * 1e-3) / 1e9, 1), "bytes": byts,
-            "batched_us": round(ms_b * 1e3, 2), "batched_gbs": round(byts / (ms_b * 1e-3) / 1e9, 1)}
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+
+    def capture(fn, idx):
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            for i in idx:
+                fn(i)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                for i in idx:
+                    fn(i)
+        return graph
+
+    n = len(layers)
+    res = {"beta": beta, "distinct_experts": distinct}
+    byts = distinct * EXPERT_BYTES
+    for name, fn in (("", dropin), ("batched_", batched)):
+        ms_all = time_graph(torch, capture(fn, list(range(n))), reps, 2) / n
+        ms_one = time_graph(torch, capture(fn, [1] * 8), 4 * reps, 3) / 8
+        res[name + "us"] = round(ms_all * 1e3, 2)
+        res[name + "gbs"] = round(byts / (ms_all * 1e-3) / 1e9, 1)
+        res[name + "us_one_layer"] = round(ms_one * 1e3, 2)
+    res["bytes"] = byts
+    res["note"] = (f"us / gbs: the step's MoE over all {n} resident layers in turn (HBM); us_one_layer: one layer "
+                   "repeated (its experts then sit in the memory-side cache)")
+    return res
 
 
 def bench_prefill_moe(torch, lext, lay, T=2048, reps=10, loop_reps=2):
@@ -718,7 +741,7 @@ def only_extra(args, torch, dext, lext, layers, routes, x0):
     elif args.only == "step":
         log(f"decode step (config 5): {[bench_step(torch, layers, M) for M in args.step_m]}")
     elif args.only == "spec":
-        log(f"spec verify: {[bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
+        log(f"spec verify: {[bench_spec_verify(torch, dext, layers, b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]}")
 
 
 # ----------------------------------------------------------------------------- main
@@ -848,7 +871,7 @@ def main():
             log(f"gemm {M}x{N}x{K}: {pre[f'{M}x{N}x{K}']}")
         pre["timing"] = "20 calls through the fp4_ext mirror captured in one HIP graph; us = replay time / 20"
         extra["prefill_gemm"] = pre
-        sv = [bench_spec_verify(torch, dext, layers[1], b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]
+        sv = [bench_spec_verify(torch, dext, layers, b, 40 + i) for i, b in enumerate((0.5, 1.0, 1.5))]
         extra["spec_verify_m9"] = sv
         log(f"spec verify: {sv}")
         pf = bench_prefill_moe(torch, lext, layers[2])

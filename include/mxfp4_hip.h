@@ -527,7 +527,8 @@ int mxfp4_route_tables(const int32_t* ids, int M, int k, const uint8_t* gate_wp,
  *            mapped or fine-grained) and nothing may read or write it
  *            between the entry's two launches.
  *   ws       mxfp4_moe_decode_batch_workspace_size(M, E, Mi) bytes, 16-byte
- *            aligned (the per-slot MXFP4 h; nothing persists)
+ *            aligned (the per-slot MXFP4 h and the owner table the gate/up
+ *            launch hands to the down launch; nothing persists)
  * Limits: 1 <= M <= 16, 1 <= E <= 8, H a multiple of 128, Mi of 32.  The
  * sums match the drop-in chain up to fp32 summation order.
  */
@@ -538,7 +539,7 @@ int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, const int32_t* 
                            int M, int E, int H, int Mi, float* y, void* ws, size_t ws_bytes, void* stream);
 
 /* mxfp4_moe_decode_batch_noalloc: mxfp4_moe_decode_batch with its h staged
- * in a fixed scratch array of the library (139,264 bytes per GPU, held until
+ * in a fixed scratch array of the library (141,568 bytes per GPU, held until
  * the process ends) instead of a caller workspace.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops).  It calls no allocator.  Limits as

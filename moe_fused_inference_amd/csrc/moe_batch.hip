@@ -28,11 +28,17 @@
 //                        order).  (150 VGPRs: 3 waves per SIMD, so 12 waves
 //                        fit one CU.)  No gu / yd round trip through HBM and
 //                        no separate combine launch.
+//   batch_down_lds_kernel  the same down workgroups and arithmetic with every
+//                        slot's h row copied into LDS once per workgroup, the
+//                        owners read from a table the gate/up launch writes,
+//                        and two owners' weight rows in flight per wave (the
+//                        launcher's choice whenever the h rows fit in LDS).
 //
 // The results match the drop-in chain up to fp32 summation order (the
 // combine adds a token's experts grouped by wave instead of in slot order).
 #include <mutex>
 
+#include "lds_dma.h"
 #include "mx_device.h"
 #include "mx_host.h"
 
@@ -59,7 +65,14 @@ struct BatchArgs {
     uint8_t* hq;         // (S, Mi/2) MXFP4 h per slot
     uint8_t* hs;         // (S, Mi/32)
     float* y;            // (M, H) fp32 MoE output
+    uint8_t* meta;       // per slot: owner flag (S bytes), member count (S), member slots (S x 16)
 };
+
+// Workspace: h rows, h scales, then the owner table the gate/up launch writes
+// for the down launch, 16-byte aligned.
+__host__ __device__ constexpr size_t align16(size_t v) { return (v + 15) & ~(size_t)15; }
+__host__ __device__ constexpr size_t meta_offset(int S, int Mi) { return align16((size_t)S * (Mi / 2) + (size_t)S * (Mi / 32)); }
+__host__ __device__ constexpr size_t meta_bytes(int S) { return (size_t)S * (2 + kMaxTok); }
 
 // One prefetch segment: weight (B) and activation (A) 16-byte blocks and
 // their scale bytes for kSegB MFMA K-steps.
@@ -161,9 +174,19 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
         }
     }
     __syncthreads();
+    const bool valid_e = e >= 0 && e < a.n_experts;   // other ids contribute h = 0
+    // the owner table of the down launch: slot s owns a valid expert (first
+    // slot naming it), its member count and member slots (token order)
+    if (rb == 0 && wave == 0) {
+        const int S_ = a.M * a.E;
+        if (lane == 0) {
+            a.meta[s] = (uint8_t)(s_own && valid_e ? 1 : 0);
+            a.meta[S_ + s] = (uint8_t)(s_own ? s_cnt : 0);
+        }
+        if (s_own && lane < s_cnt) a.meta[2 * S_ + s * kMaxTok + lane] = (uint8_t)s_slot[lane];
+    }
     if (!s_own) return;
     const int cnt = s_cnt;
-    const bool valid_e = e >= 0 && e < a.n_experts;   // other ids contribute h = 0
     const int l16 = lane & 15, q = lane >> 4;
     const int H = a.H, Mi = a.Mi;
     const int proj = wave >> 1;
@@ -291,12 +314,164 @@ __global__ __launch_bounds__(64 * kDownWaves) void batch_down_kernel(BatchArgs a
     }
 }
 
-// Scratch of mxfp4_moe_decode_batch_noalloc: the per-slot MXFP4 h of up to
-// kMaxSlots slots at Mi <= kNoAllocMaxMi, 139,264 bytes.  One copy per GPU,
-// held until the process ends; host code addresses it only through the
-// pointer hipGetSymbolAddress returns for the current device.
+// The down launch with the h rows in LDS (when they fit): every slot's MXFP4
+// h row and scales are copied into LDS once per workgroup (LDS DMA), the
+// owners come from the table the gate/up launch wrote (no first-occurrence
+// pass), and a wave issues the down rows of up to two of its owners before
+// it waits, so both owners' weights are in flight at once.  Same workgroups,
+// same arithmetic and the same y additions as batch_down_kernel, so the
+// results are identical.
+constexpr int kOwnPerRound = 2;   // owners whose weights a wave has in flight at once
+
+struct DownLds {
+    int hrow;        // LDS bytes per h row (Mi/2 + 16: rows land in different bank groups)
+    int hs_off;      // h scales: S x Mi/32 bytes
+    int bs_off;      // B scales: per wave and owner in flight, 16 rows x Mi/32 bytes
+    int bytes;
+};
+
+__host__ __device__ inline DownLds down_lds_layout(int S, int Mi) {
+    DownLds d;
+    d.hrow = Mi / 2 + 16;
+    d.hs_off = (int)align16((size_t)S * d.hrow);
+    d.bs_off = d.hs_off + (int)align16((size_t)S * (Mi / 32));
+    d.bytes = d.bs_off + kDownWaves * kOwnPerRound * 16 * (Mi / 32);
+    return d;
+}
+
+// k-th set bit (k from 0) of the 128-bit mask (lo, hi); -1 if there is none
+__device__ __forceinline__ int nth_set(uint64_t lo, uint64_t hi, int k) {
+    const int nlo = __popcll(lo);
+    uint64_t m = k < nlo ? lo : hi;
+    int kk = k < nlo ? k : k - nlo;
+    if (kk >= __popcll(m)) return -1;
+    for (int i = 0; i < kk; ++i) m &= m - 1;
+    return (k < nlo ? 0 : 64) + (int)__ffsll((long long)m) - 1;
+}
+
+// MS: K steps bound; OPR <= kOwnPerRound: owners per round (1 at MS = 16, where
+// two owners' rows would not fit the registers of 3 waves per SIMD).
+template <int MS, int OPR>
+__global__ __launch_bounds__(64 * kDownWaves) void batch_down_lds_kernel(BatchArgs a) {
+    extern __shared__ __align__(16) uint8_t dyn[];
+    __shared__ float s_w[kMaxSlots];
+    __shared__ int s_mem[kDownWaves][OPR][kMaxTok];
+    __shared__ float ypart[kDownWaves][kMaxTok][17];
+    const int cb = blockIdx.x >> 1, half = blockIdx.x & 1;
+    const int S = a.M * a.E;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, q = lane >> 4;
+    const int H = a.H, Mi = a.Mi;
+    const int kb = Mi / 32, steps = (kb + 3) / 4;
+    const DownLds L = down_lds_layout(S, Mi);
+    const uint32_t lds0 = mx::lds_addr(dyn);
+    // ---- owners (slot order) from the gate/up launch's table: every wave holds the mask.
+    // These loads are waited for before any LDS copy is issued: the compiler's waits do
+    // not count the copies (inline asm), so a wait issued after them would wait for them.
+    const uint8_t* own = a.meta;
+    const uint8_t* mcnt = a.meta + S;
+    const uint8_t* mslots = a.meta + 2 * S;
+    const bool o0 = lane < S && own[lane] != 0, o1 = 64 + lane < S && own[64 + lane] != 0;
+    const uint64_t mlo = __ballot(o0), mhi = __ballot(o1);
+    const int nown = __popcll(mlo) + __popcll(mhi);
+    if (tid < S) s_w[tid] = a.w[tid];
+    for (int i = tid; i < kDownWaves * kMaxTok * 17; i += 64 * kDownWaves) (&ypart[0][0][0])[i] = 0.0f;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    // ---- copies of every slot's h row and the h scales into LDS
+    {
+        const mx::v4u rh = mx::buf_rsrc(a.hq, (int64_t)S * (Mi / 2));
+        for (int sl = wave; sl < S; sl += kDownWaves)
+            if (lane < Mi / 32) mx::dma16(16u * lane, rh, (uint32_t)(sl * (Mi / 2)), lds0 + sl * L.hrow);
+        const mx::v4u rhs = mx::buf_rsrc(a.hs, (int64_t)S * kb);
+        for (int c = wave; c * 1024 < S * kb; c += kDownWaves)
+            if (c * 1024 + 16 * lane < S * kb) mx::dma16(16u * lane, rhs, (uint32_t)(c * 1024), lds0 + L.hs_off + c * 1024);
+    }
+    bool first = true;
+    // wave w of half h: owners 2 w + h, 2 (w + kDownWaves) + h, ... in rounds of OPR
+    for (int k0 = 2 * wave + half; first || k0 < nown; k0 += 2 * kDownWaves * OPR) {
+        int oslot[OPR], oe[OPR], ocnt[OPR], mv[OPR];
+        uint4 bq[OPR][MS];
+#pragma unroll
+        for (int o = 0; o < OPR; ++o) {
+            const int k = k0 + 2 * kDownWaves * o;
+            oslot[o] = k < nown ? nth_set(mlo, mhi, k) : -1;
+            const int sl = oslot[o] < 0 ? 0 : oslot[o];
+            const int e = oslot[o] < 0 ? 0 : a.ids[sl];
+            oe[o] = e;
+            ocnt[o] = oslot[o] < 0 ? 0 : (int)mcnt[sl];
+            mv[o] = lane < ocnt[o] ? (int)mslots[sl * kMaxTok + lane] : 0;   // written to LDS after the wait
+            // the owner's down rows for the 16 columns (zero-extent for no owner) and their scales
+            const uint8_t* wrow = a.dwp + ((int64_t)e * H + cb * 16) * (Mi / 2);
+            const __amdgpu_buffer_rsrc_t rw =
+                __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(wrow), (short)0, oslot[o] < 0 ? 0 : 16 * (Mi / 2), 0x00020000);
+#pragma unroll
+            for (int st = 0; st < MS; ++st) {
+                const mx::v4u v = __builtin_amdgcn_raw_buffer_load_b128(rw, (uint32_t)(l16 * (Mi / 2) + 16 * min(4 * st + q, kb - 1)), 0, 0);
+                bq[o][st] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+            const mx::v4u rs = mx::buf_rsrc(a.dws + ((int64_t)e * H + cb * 16) * kb, oslot[o] < 0 ? 0 : 16 * kb);
+            if (lane < kb) mx::dma16(16u * lane, rs, 0u, lds0 + L.bs_off + (wave * kOwnPerRound + o) * 16 * kb);
+        }
+        // everything this wave issued has landed; the first round also waits for every
+        // wave's h copies (and the LDS clears above) at the barrier
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int o = 0; o < OPR; ++o)
+            if (lane < kMaxTok) s_mem[wave][o][lane] = mv[o];
+        if (first) __syncthreads();   // also orders the s_mem writes (wave-local) before their reads
+        else asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        first = false;
+#pragma unroll
+        for (int o = 0; o < OPR; ++o) {
+            if (oslot[o] < 0) continue;
+            const int cnt = ocnt[o];
+            const bool aok = l16 < cnt;
+            const int mslot = aok ? s_mem[wave][o][l16] : 0;
+            const uint8_t* ha = dyn + mslot * L.hrow;
+            const uint8_t* hsa = dyn + L.hs_off + mslot * kb;
+            const uint8_t* bsa = dyn + L.bs_off + (wave * kOwnPerRound + o) * 16 * kb + l16 * kb;
+            mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < MS; ++st) {
+                if (st < steps) {
+                    const int c = 4 * st + q;
+                    const bool ok = c < kb;
+                    const uint4 av = (aok && ok) ? *reinterpret_cast<const uint4*>(ha + 16 * c) : make_uint4(0, 0, 0, 0);
+                    const uint32_t sa = (aok && ok) ? (uint32_t)hsa[c] : 127u;
+                    const uint32_t sb = ok ? (uint32_t)bsa[c] : 127u;
+                    acc = mx::mfma16_fp4(av, bq[o][st], acc, sa, sb);
+                }
+            }
+            // D[4q + i][l16]: member 4q + i, column l16; weighted into its token's sum
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 4 * q + i;
+                if (r < cnt) {
+                    const int sl = s_mem[wave][o][r];
+                    ypart[wave][sl / a.E][l16] = fmaf(s_w[sl], acc[i], ypart[wave][sl / a.E][l16]);
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0): s_mem / ypart of this round done
+        __builtin_amdgcn_wave_barrier();
+    }
+    __syncthreads();
+    for (int i = tid; i < a.M * 16; i += 64 * kDownWaves) {
+        const int m = i >> 4, c = i & 15;
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kDownWaves; ++w) v += ypart[w][m][c];
+        __hip_atomic_fetch_add(a.y + (int64_t)m * H + cb * 16 + c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// Scratch of mxfp4_moe_decode_batch_noalloc: the per-slot MXFP4 h and the
+// owner table of up to kMaxSlots slots at Mi <= kNoAllocMaxMi, 141,568 bytes.
+// One copy per GPU, held until the process ends; host code addresses it only
+// through the pointer hipGetSymbolAddress returns for the current device.
 constexpr int kNoAllocMaxMi = 2048;
-constexpr size_t kScratchBytes = (size_t)kMaxSlots * (kNoAllocMaxMi / 2 + kNoAllocMaxMi / 32);
+constexpr size_t kScratchBytes = meta_offset(kMaxSlots, kNoAllocMaxMi) + meta_bytes(kMaxSlots);
 static __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxDevices = 64;
@@ -338,12 +513,33 @@ int check_batch_args(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, c
     return MXFP4_OK;
 }
 
-// The two launches, h staged in w8 (S*(Mi/2) + S*(Mi/32) bytes, 16-byte aligned).
+// The down kernel with h in LDS when it fits (Mi <= 2048: a slot's h row is
+// one LDS copy of <= 64 lanes; at most kDownLdsMax bytes of dynamic LDS).
+constexpr int kDownLdsMax = 128 * 1024;
+
+template <int MS, int OPR>
+int launch_down_lds(const BatchArgs& a, int lds_bytes, hipStream_t st) {
+    static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&batch_down_lds_kernel<MS, OPR>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize, kDownLdsMax);
+    if (attr != hipSuccess) {
+        mxh::set_error("moe_decode_batch (down): hipFuncSetAttribute: %s", hipGetErrorString(attr));
+        return (int)attr;
+    }
+    hipLaunchKernelGGL((batch_down_lds_kernel<MS, OPR>), dim3(2 * (a.H / 16)), dim3(64 * kDownWaves), lds_bytes, st, a);
+    return mxh::launch_status("moe_decode_batch (down)");
+}
+
+// The two launches; w8 holds h (S*(Mi/2) + S*(Mi/32) bytes) and the owner
+// table at meta_offset(S, Mi), 16-byte aligned.
 int launch_batch(const BatchArgs& a, hipStream_t st) {
     const int S = a.M * a.E;
     hipLaunchKernelGGL(batch_gateup_kernel, dim3(a.Mi / 32, S), dim3(256), 0, st, a);
     const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
     if (rc != MXFP4_OK) return rc;
+    const DownLds L = down_lds_layout(S, a.Mi);
+    const int steps = (a.Mi / 32 + 3) / 4;
+    if (a.Mi <= 2048 && L.bytes <= kDownLdsMax)
+        return steps <= 6 ? launch_down_lds<6, 2>(a, L.bytes, st) : launch_down_lds<16, 1>(a, L.bytes, st);
     hipLaunchKernelGGL(batch_down_kernel, dim3(2 * (a.H / 16)), dim3(64 * kDownWaves), 0, st, a);
     return mxh::launch_status("moe_decode_batch (down)");
 }
@@ -352,8 +548,7 @@ int launch_batch(const BatchArgs& a, hipStream_t st) {
 
 extern "C" size_t mxfp4_moe_decode_batch_workspace_size(int M, int E, int Mi) {
     if (M <= 0 || E <= 0 || Mi <= 0) return 0;
-    const size_t S = (size_t)M * E;
-    return S * (size_t)(Mi / 2) + S * (size_t)(Mi / 32);
+    return meta_offset(M * E, Mi) + meta_bytes(M * E);
 }
 
 extern "C" int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, const int32_t* ids, const float* w,
@@ -372,7 +567,7 @@ extern "C" int mxfp4_moe_decode_batch(const uint8_t* xq, const uint8_t* xs, cons
     const int S = M * E;
     uint8_t* w8 = static_cast<uint8_t*>(ws);
     const BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
-                      w8, w8 + (size_t)S * (Mi / 2), y};
+                      w8, w8 + (size_t)S * (Mi / 2), y, w8 + meta_offset(S, Mi)};
     return launch_batch(a, mxh::as_stream(stream));
 }
 
@@ -392,11 +587,12 @@ extern "C" int mxfp4_moe_decode_batch_noalloc(const uint8_t* xq, const uint8_t* 
     void* sp = nullptr;
     const int rs = scratch_on_current_device(&sp);
     if (rs != MXFP4_OK) return rs;
-    // Every h row the down kernel reads is written by the gate/up kernel of the
-    // same call, so nothing in the scratch has to start at zero.
+    // Every h row and owner-table entry the down kernel reads is written by the
+    // gate/up kernel of the same call, so nothing in the scratch has to start
+    // at zero.
     const int S = M * E;
     uint8_t* w8 = static_cast<uint8_t*>(sp);
     const BatchArgs a{xq, xs, ids, w, gate_wp, gate_ws, up_wp, up_ws, down_wp, down_ws, n_experts, M, E, H, Mi,
-                      w8, w8 + (size_t)S * (Mi / 2), y};
+                      w8, w8 + (size_t)S * (Mi / 2), y, w8 + meta_offset(S, Mi)};
     return launch_batch(a, mxh::as_stream(stream));
 }
