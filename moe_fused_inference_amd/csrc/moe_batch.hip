@@ -140,6 +140,18 @@ __device__ __forceinline__ bool first_occurrence(const int* s_ids, int S, int j,
     return own;
 }
 
+// STAGED (H <= 2048): the member tokens' activation rows and every scale byte
+// are copied into LDS (LDS DMA) and each wave has all of its K steps of
+// weight rows in flight at once; otherwise two 4-step segments of A and B go
+// through registers (kloop).  Both run the same MFMA chain, so h is the same.
+constexpr int kGuMaxSteps = 16;   // K steps (H/128) of the staged path
+
+__host__ __device__ constexpr int gu_arow(int H) { return H / 2 + 16; }   // LDS bytes per A row
+__host__ __device__ constexpr int gu_sa_off(int H) { return kMaxTok * gu_arow(H); }
+__host__ __device__ constexpr int gu_sb_off(int H) { return gu_sa_off(H) + (int)align16((size_t)kMaxTok * (H / 32)); }
+__host__ __device__ constexpr int gu_lds_bytes(int H) { return gu_sb_off(H) + 4 * 16 * (H / 32); }
+
+template <bool STAGED>
 __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
     __shared__ int s_slot[kMaxTok];
     __shared__ int s_cnt, s_own;
@@ -195,11 +207,60 @@ __global__ __launch_bounds__(256) void batch_gateup_kernel(BatchArgs a) {
     const uint8_t* wrow = (proj ? a.uwp : a.gwp) + (ee * Mi + row) * (int64_t)(H / 2);
     const uint8_t* srow = (proj ? a.uws : a.gws) + (ee * Mi + row) * (int64_t)(H / 32);
     const bool aok = valid_e && l16 < cnt;
-    const int tok = aok ? s_slot[l16] / a.E : 0;
-    const uint8_t* arow = a.xq + (int64_t)tok * (H / 2);
-    const uint8_t* asrow = a.xs + (int64_t)tok * (H / 32);
     const int nch = H / 32;
-    mx::v4f acc = kloop(wrow, srow, arow, asrow, aok, q, (nch + 3) / 4, nch);
+    mx::v4f acc;
+    if constexpr (STAGED) {
+        extern __shared__ __align__(16) uint8_t dyn[];
+        const int steps = nch / 4;
+        const uint32_t lds0 = mx::lds_addr(dyn);
+        // member rows of x (wave w: members w, w + 4, ...) at t * gu_arow(H)
+        const mx::v4u rx = mx::buf_rsrc(a.xq, (int64_t)a.M * (H / 2));
+        for (int t = wave; t < cnt; t += 4) {
+            const int tk = s_slot[t] / a.E;
+            for (int c = 0; c * 1024 < H / 2; ++c)
+                if (c * 1024 + 16 * lane < H / 2)
+                    mx::dma16(16u * lane, rx, (uint32_t)(tk * (H / 2) + c * 1024), lds0 + t * gu_arow(H) + c * 1024);
+        }
+        // their scales, H/32 bytes per member at t * H/32: 4 bytes a lane, 64 / (H/128) members a copy
+        const int lpr = H / 128, rpc = 64 / lpr;
+        const mx::v4u rxs = mx::buf_rsrc(a.xs, (int64_t)a.M * nch);
+        for (int t0 = wave * rpc; t0 < cnt; t0 += 4 * rpc) {
+            const int t = t0 + lane / lpr;
+            if (t < cnt)
+                mx::dma4((uint32_t)((s_slot[t] / a.E) * nch + 4 * (lane % lpr)), rxs, 0u, lds0 + gu_sa_off(H) + t0 * nch);
+        }
+        // this wave's 16 weight rows' scales (16 x H/32 contiguous bytes)
+        const mx::v4u rbs = mx::buf_rsrc(srow - (int64_t)l16 * nch, 16 * nch);
+        for (int c = 0; c * 1024 < 16 * nch; ++c)
+            if (c * 1024 + 16 * lane < 16 * nch)
+                mx::dma16(16u * lane, rbs, (uint32_t)(c * 1024), lds0 + gu_sb_off(H) + wave * 16 * nch + c * 1024);
+        // every K step of the wave's weight rows in flight
+        uint4 bq[kGuMaxSteps];
+#pragma unroll
+        for (int st = 0; st < kGuMaxSteps; ++st)
+            if (st < steps) bq[st] = *reinterpret_cast<const uint4*>(wrow + 16 * (4 * st + q));
+        // all of it has landed (the copies of every wave, at the barrier)
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const uint8_t* al = dyn + l16 * gu_arow(H);
+        const uint8_t* asl = dyn + gu_sa_off(H) + l16 * nch;
+        const uint8_t* bsl = dyn + gu_sb_off(H) + wave * 16 * nch + l16 * nch;
+        acc = (mx::v4f){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < kGuMaxSteps; ++st) {
+            if (st < steps) {
+                const int c = 4 * st + q;
+                const uint4 av = aok ? *reinterpret_cast<const uint4*>(al + 16 * c) : make_uint4(0, 0, 0, 0);
+                const uint32_t sa = aok ? (uint32_t)asl[c] : 127u;
+                acc = mx::mfma16_fp4(av, bq[st], acc, sa, (uint32_t)bsl[c]);
+            }
+        }
+    } else {
+        const int tok = aok ? s_slot[l16] / a.E : 0;
+        const uint8_t* arow = a.xq + (int64_t)tok * (H / 2);
+        const uint8_t* asrow = a.xs + (int64_t)tok * (H / 32);
+        acc = kloop(wrow, srow, arow, asrow, aok, q, (nch + 3) / 4, nch);
+    }
     mx::pin(acc);
     // D[4q + i][l16]: token 4q + i of the group, weight row l16 of the tile
 #pragma unroll
@@ -533,7 +594,10 @@ int launch_down_lds(const BatchArgs& a, int lds_bytes, hipStream_t st) {
 // table at meta_offset(S, Mi), 16-byte aligned.
 int launch_batch(const BatchArgs& a, hipStream_t st) {
     const int S = a.M * a.E;
-    hipLaunchKernelGGL(batch_gateup_kernel, dim3(a.Mi / 32, S), dim3(256), 0, st, a);
+    if (a.H <= 128 * kGuMaxSteps)
+        hipLaunchKernelGGL(batch_gateup_kernel<true>, dim3(a.Mi / 32, S), dim3(256), gu_lds_bytes(a.H), st, a);
+    else
+        hipLaunchKernelGGL(batch_gateup_kernel<false>, dim3(a.Mi / 32, S), dim3(256), 0, st, a);
     const int rc = mxh::launch_status("moe_decode_batch (gate/up)");
     if (rc != MXFP4_OK) return rc;
     const DownLds L = down_lds_layout(S, a.Mi);
