@@ -69,6 +69,7 @@ struct GemvArgs {
     const float* gu;    // A_SILU: (rows, 2K)
     float* out;
     int64_t ld_out;
+    int ncb;   // A_SILU: 64-column blocks per workgroup (one h tile build for all of them); 0 = 1
 };
 
 struct EntryMap {
@@ -161,7 +162,8 @@ __device__ __forceinline__ mx::v4f compute_seg(const SegBuf& sb, const SegCtx& c
 // (one wave per tile and part; the S partial sums meet in LDS in part order).
 // NW = 1 spreads a small-N launch over more workgroups and S > 1 puts a
 // row tile's bytes in flight at once (A_FP4 only), so more CUs stream at once.
-template <class Tab, int AMODE, int NW, int S>
+// MB (A_SILU, one K segment per part): a.ncb column blocks per workgroup.
+template <class Tab, int AMODE, int NW, int S, bool MB = false>
 __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, GemvArgs a) {
     extern __shared__ __align__(16) uint8_t s_dyn[];  // A_SILU: 16 rows of quantized h
     __shared__ int s_rows[kMaxT];
@@ -213,7 +215,11 @@ __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, Gemv
     const int steps = (nch + 3) >> 2;     // MFMA K-steps; lane group g takes blocks g, g + 4, ...
     const int r = lane & 15;
     const int g = lane >> 4;
-    const int n0 = blockIdx.x * (16 * NW) + wave * 16;
+    // column blocks of 16 * NW weight rows: a workgroup takes ncb of them
+    // (A_SILU with one K segment per part only, otherwise 1)
+    const int ncb = MB ? a.ncb : 1;
+    auto blk_n0 = [&](int cbk) { return (blockIdx.x * ncb + cbk) * (16 * NW) + wave * 16; };
+    const int n0 = blk_n0(0);
     const int nrow = min(n0 + r, a.N - 1);
     const uint8_t* wrow = wp + (int64_t)nrow * (a.Kp >> 1);
     const uint8_t* srow = ws + (int64_t)nrow * nch;
@@ -302,40 +308,67 @@ __global__ __launch_bounds__(64 * NW * S) void grouped_gemv_kernel(Tab tab, Gemv
             __syncthreads();
         }
 
-        mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
-        if (sb < se) {
-            for (int s0 = 0; s0 < cx.steps; s0 += 2 * kSeg) {
-                if (s0 + kSeg < cx.steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
-                acc = compute_seg<AMODE>(s0buf, cx, s0, acc);
-                if (s0 + kSeg >= cx.steps) break;
-                if (s0 + 2 * kSeg < cx.steps) load_seg<AMODE>(s0buf, cx, s0 + 2 * kSeg);
-                acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
+        // the S partial sums in part order (parts 1.. hand theirs to part 0),
+        // then D[4*(l/16)+i][l%16] (token row, weight row) of column block cbk
+        auto finish = [&](mx::v4f acc, int cbk) {
+            mx::pin(acc);
+            if constexpr (S > 1) {
+                if (part > 0) s_red[part - 1][wave][lane] = acc;
+                __syncthreads();
+                if (part == 0) {
+#pragma unroll
+                    for (int p = 1; p < S; ++p) {
+                        const mx::v4f o = s_red[p - 1][wave][lane];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) acc[i] += o[i];
+                    }
+                }
             }
-        }
-        mx::pin(acc);
-        if constexpr (S > 1) {
-            // partial sums in part order (parts 1.. hand theirs to part 0)
-            if (part > 0) s_red[part - 1][wave][lane] = acc;
-            __syncthreads();
+            const int col = blk_n0(cbk) + r;
             if (part == 0) {
 #pragma unroll
-                for (int p = 1; p < S; ++p) {
-                    const mx::v4f o = s_red[p - 1][wave][lane];
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) acc[i] += o[i];
+                for (int i = 0; i < 4; ++i) {
+                    const int rr = 4 * g + i;
+                    if (rt + rr < cnt && col < a.N) {
+                        const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
+                        a.out[(int64_t)em.dst * a.ld_out + em.col + col] = acc[i];
+                    }
                 }
             }
-        }
-        // D[4*(l/16)+i][l%16]: token row, weight row
-        const int col = n0 + r;
-        if (part == 0) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int rr = 4 * g + i;
-                if (rt + rr < cnt && col < a.N) {
-                    const EntryMap em = map_entry(a, a.t0 + s_rows[rt + rr]);
-                    a.out[(int64_t)em.dst * a.ld_out + em.col + col] = acc[i];
+            if constexpr (S > 1) __syncthreads();   // s_red is reused by the next block
+        };
+        if constexpr (!MB) {
+            mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+            if (sb < se) {
+                for (int s0 = 0; s0 < cx.steps; s0 += 2 * kSeg) {
+                    if (s0 + kSeg < cx.steps) load_seg<AMODE>(s1buf, cx, s0 + kSeg);
+                    acc = compute_seg<AMODE>(s0buf, cx, s0, acc);
+                    if (s0 + kSeg >= cx.steps) break;
+                    if (s0 + 2 * kSeg < cx.steps) load_seg<AMODE>(s0buf, cx, s0 + 2 * kSeg);
+                    acc = compute_seg<AMODE>(s1buf, cx, s0 + kSeg, acc);
                 }
+            }
+            finish(acc, 0);
+        } else {
+            // one K segment per part: block cbk's weights sit in s0buf (even cbk)
+            // or s1buf (odd), and the next block's are issued before the MFMAs
+            auto blk_ctx = [&](int cbk) {
+                const int nr = min(blk_n0(cbk) + r, a.N - 1);
+                SegCtx c = cx;
+                c.wrow = wp + (int64_t)nr * (a.Kp >> 1) + boff * 16;
+                c.srow = ws + (int64_t)nr * nch + boff;
+                return c;
+            };
+            for (int cbk = 0; cbk < ncb; cbk += 2) {
+                if (cbk + 1 < ncb && sb < se) load_seg<AMODE>(s1buf, blk_ctx(cbk + 1), 0);
+                mx::v4f acc = {0.f, 0.f, 0.f, 0.f};
+                if (sb < se) acc = compute_seg<AMODE>(s0buf, cx, 0, acc);
+                finish(acc, cbk);
+                if (cbk + 1 >= ncb) break;
+                if (cbk + 2 < ncb && sb < se) load_seg<AMODE>(s0buf, blk_ctx(cbk + 2), 0);
+                acc = mx::v4f{0.f, 0.f, 0.f, 0.f};
+                if (sb < se) acc = compute_seg<AMODE>(s1buf, cx, 0, acc);
+                finish(acc, cbk + 1);
             }
         }
         if (AMODE == A_SILU || S > 1) __syncthreads();  // LDS reused by the next row tile
@@ -621,9 +654,21 @@ int launch_gemv(const Tab& tab, const GemvArgs& a, int amode, hipStream_t st) {
         dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)a.T);
         if (amode == A_FP4)
             hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_FP4, 4, 1>), grid, dim3(256), 0, st, tab, a);
-        else if (steps >= 2)
-            hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 2>), grid, dim3(512), silu_lds_bytes(a.Kp),
-                               st, tab, a);
+        else if (steps >= 2) {
+            // several column blocks per workgroup (h built once for them) when each
+            // K part is one segment: fewer, fuller rounds of workgroups
+            const int ncb = a.ncb > 1 && (steps + 1) / 2 <= kSeg ? a.ncb : 1;
+            if (ncb > 1) {
+                GemvArgs b = a;
+                b.ncb = ncb;
+                dim3 g2((unsigned)((a.N + 64 * ncb - 1) / (64 * ncb)), (unsigned)a.T);
+                hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 2, true>), g2, dim3(512),
+                                   silu_lds_bytes(a.Kp), st, tab, b);
+            } else {
+                hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 2>), grid, dim3(512), silu_lds_bytes(a.Kp),
+                                   st, tab, a);
+            }
+        }
         else
             hipLaunchKernelGGL((grouped_gemv_kernel<Tab, A_SILU, 4, 1>), grid, dim3(256), silu_lds_bytes(a.Kp),
                                st, tab, a);
@@ -660,6 +705,15 @@ int run_host_table(const uint8_t* const* wp_tab, const uint8_t* const* ws_tab, i
         }
         a.T = n;
         a.t0 = c0;
+        // A_SILU: column blocks per workgroup so that the groups' workgroups
+        // come to at most 512 (about one round, two per CU, and no fewer than 256)
+        a.ncb = 1;
+        if (amode == A_SILU) {
+            int groups = 0;
+            for (int i = 0; i < n; ++i) groups += tab.info[i] != 0;
+            const int64_t total = (int64_t)groups * ((a.N + 63) / 64);
+            while (a.ncb < 8 && total / a.ncb > 512) a.ncb *= 2;
+        }
         const int rc = launch_gemv(tab, a, amode, st);
         if (rc != MXFP4_OK) return rc;
     }
