@@ -120,10 +120,10 @@ __host__ __device__ constexpr int64_t buf_words(int H, int Mi) {
     return (int64_t)kXcds * (gu_words(Mi) + part_words(H) + x_words(H));
 }
 
-struct Route {
-    int32_t ids[kLdsLayers];            // this slot's expert per layer
-    float w[kLdsLayers][kMaxE];         // every slot's combine weight per layer
-    const uint8_t* ptr[kLdsLayers][6];  // the layer's six stacked weight pointers
+struct Route {                                   // rows read as 16-byte words
+    alignas(16) int32_t ids[kLdsLayers];           // this slot's expert per layer
+    alignas(16) float w[kLdsLayers][kMaxE];        // every slot's combine weight per layer
+    alignas(16) const uint8_t* ptr[kLdsLayers][6];  // the layer's six stacked weight pointers
 };
 
 union Smem {
@@ -320,14 +320,33 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         if (threadIdx.x == 2) sm.code127[0] = 0x7F7F7F7Fu;
         __syncthreads();
     }
-    auto route_id = [&](int l) -> int {
-        int e = __builtin_amdgcn_readfirstlane(l < kLdsLayers ? sm.rt.ids[l] : ld_const(a.ids, l * E + s));
-        return e < 0 ? 0 : (e >= a.n_experts ? a.n_experts - 1 : e);   // memory safety only
+    // layer l's six weight pointers and this slot's expert: from LDS with three 16-byte reads
+    // under one wave-uniform branch (a select per field compiles to a branch and an LDS
+    // round trip each, ~0.3 us per layer in series)
+    struct LayerRoute {
+        const uint8_t* p[6];
+        int e;
     };
-    auto route_w = [&](int l, int t) -> float { return l < kLdsLayers ? sm.rt.w[l][t] : ld_const(a.w, l * E + t); };
-    auto route_ptr = [&](int l, int k) -> const uint8_t* {
-        return l < kLdsLayers ? sm.rt.ptr[l][k]
-                              : ld_const(reinterpret_cast<const uint8_t* const*>(a.layers), 6 * l + k);
+    auto route = [&](int l) -> LayerRoute {
+        LayerRoute r;
+        int e;
+        if (l < kLdsLayers) {
+            const uint4* q = reinterpret_cast<const uint4*>(&sm.rt.ptr[l][0]);
+            const uint4 v[3] = {q[0], q[1], q[2]};
+#pragma unroll
+            for (int k = 0; k < 3; ++k) {
+                r.p[2 * k] = reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)v[k].y << 32) | v[k].x));
+                r.p[2 * k + 1] = reinterpret_cast<const uint8_t*>((uintptr_t)(((uint64_t)v[k].w << 32) | v[k].z));
+            }
+            e = sm.rt.ids[l];
+        } else {
+#pragma unroll
+            for (int k = 0; k < 6; ++k) r.p[k] = ld_const(reinterpret_cast<const uint8_t* const*>(a.layers), 6 * l + k);
+            e = ld_const(a.ids, l * E + s);
+        }
+        e = __builtin_amdgcn_readfirstlane(e);
+        r.e = e < 0 ? 0 : (e >= a.n_experts ? a.n_experts - 1 : e);   // memory safety only
+        return r;
     };
 
     const int hb = H >> 5;                     // 32-blocks along H
@@ -364,13 +383,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
     }
     // valid = false: a zero-extent descriptor, so the loads return zeros
     // without touching memory
-    auto load_gu = [&](int l, bool valid) {
-        const int e = route_id(l);
+    auto load_gu = [&](const LayerRoute& rt, bool valid) {
+        const int e = rt.e;
         const int wbytes = valid ? Mi * (H >> 1) : 0, sbytes = valid ? Mi * hb : 0;
-        const __amdgpu_buffer_rsrc_t rw[2] = {rsrc(route_ptr(l, 0) + (int64_t)e * a.wp_stride_gu, wbytes),
-                                              rsrc(route_ptr(l, 1) + (int64_t)e * a.wp_stride_gu, wbytes)};
-        const __amdgpu_buffer_rsrc_t rs[2] = {rsrc(route_ptr(l, 3) + (int64_t)e * a.ws_stride_gu, sbytes),
-                                              rsrc(route_ptr(l, 4) + (int64_t)e * a.ws_stride_gu, sbytes)};
+        const __amdgpu_buffer_rsrc_t rw[2] = {rsrc(rt.p[0] + (int64_t)e * a.wp_stride_gu, wbytes),
+                                              rsrc(rt.p[1] + (int64_t)e * a.wp_stride_gu, wbytes)};
+        const __amdgpu_buffer_rsrc_t rs[2] = {rsrc(rt.p[3] + (int64_t)e * a.ws_stride_gu, sbytes),
+                                              rsrc(rt.p[4] + (int64_t)e * a.ws_stride_gu, sbytes)};
 #pragma unroll
         for (int m = 0; m < NT; ++m) {
 #pragma unroll
@@ -408,10 +427,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
     }
     uint4 dq[2][MS];
     uint32_t dsc[2][MS];   // scale byte of block 4i + g (KB4: its dword, byte g)
-    auto load_dn = [&](int l, bool valid) {
-        const int e = route_id(l);
-        const __amdgpu_buffer_rsrc_t rw = rsrc(route_ptr(l, 2) + (int64_t)e * a.wp_stride_dn, valid ? H * (Mi >> 1) : 0);
-        const __amdgpu_buffer_rsrc_t rs = rsrc(route_ptr(l, 5) + (int64_t)e * a.ws_stride_dn, valid ? H * kb : 0);
+    auto load_dn = [&](const LayerRoute& rt, bool valid) {
+        const int e = rt.e;
+        const __amdgpu_buffer_rsrc_t rw = rsrc(rt.p[2] + (int64_t)e * a.wp_stride_dn, valid ? H * (Mi >> 1) : 0);
+        const __amdgpu_buffer_rsrc_t rs = rsrc(rt.p[5] + (int64_t)e * a.ws_stride_dn, valid ? H * kb : 0);
 #pragma unroll
         for (int k = 0; k < 2; ++k) {
 #pragma unroll
@@ -428,9 +447,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
     };
 
     if (!STRICT) {
-        const int l0 = min(par, L - 1);
-        load_gu(l0, par < L);
-        load_dn(l0, par < L);
+        const LayerRoute rt = route(min(par, L - 1));
+        load_gu(rt, par < L);
+        load_dn(rt, par < L);
     }
     bool live = true;
     for (int l = par; l < L; l += 2) {
@@ -438,8 +457,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         const int b = (int)((c0 + (uint32_t)l) % kNBuf);
         // combine weights of every slot (read now, used after the y poll)
         float wt[kMaxE];
+        if (l < kLdsLayers) {   // two 16-byte reads (the LDS copy holds 0 for t >= E)
+            const float4 w0 = *reinterpret_cast<const float4*>(&sm.rt.w[l][0]);
+            const float4 w1 = *reinterpret_cast<const float4*>(&sm.rt.w[l][4]);
+            wt[0] = w0.x, wt[1] = w0.y, wt[2] = w0.z, wt[3] = w0.w;
+            wt[4] = w1.x, wt[5] = w1.y, wt[6] = w1.z, wt[7] = w1.w;
+        } else {
 #pragma unroll
-        for (int t = 0; t < kMaxE; ++t) wt[t] = t < E ? route_w(l, t) : 0.0f;
+            for (int t = 0; t < kMaxE; ++t) wt[t] = t < E ? ld_const(a.w, l * E + t) : 0.0f;
+        }
         // ---- 1. x_l for the wave's K quarter (columns cw*H/4 ..) into E4M3 term records (LDS)
         // and, for the combine, bf16 (LDS)
         {
@@ -500,8 +526,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own records, read below
         }
         if (STRICT) {
-            load_gu(l, true);
-            load_dn(l, true);
+            const LayerRoute rt = route(l);
+            load_gu(rt, true);
+            load_dn(rt, true);
         }
         // ---- 2. gate/up MFMAs: A = x_l terms (rows 0..2), B = the tile's weight rows
         {
@@ -669,9 +696,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         lds_barrier();                                                   // B5: every poll of the layer done
         if (!STRICT) {
             // layer l+2 streams while the other set computes layer l+1
-            const int ln = l + 2 < L ? l + 2 : l;
-            load_gu(ln, l + 2 < L);
-            load_dn(ln, l + 2 < L);
+            const LayerRoute rt = route(l + 2 < L ? l + 2 : l);
+            load_gu(rt, l + 2 < L);
+            load_dn(rt, l + 2 < L);
         }
     }
     if (!live) set_error(a);
