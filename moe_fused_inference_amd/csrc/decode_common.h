@@ -2,11 +2,14 @@
 // fused decode kernels (one layer per launch, and several layers per launch).
 //
 // There is no bf16 x FP4 MFMA, so a bf16 (or fp32) activation is split into
-// kTerms E4M3 terms hi + mid + lo, each with its own E8M0 32-block scale.  The
-// terms sum back to the value with an error of at most about 2^-12 of the
-// block's largest magnitude: a value far below its block's amax (more than
-// ~2^17 below it) can fall under every term's scale and drop out.  The terms
-// are rows 0..2 of the A operand of v_mfma_scale_f32_16x16x128_f8f6f4.
+// kTerms E4M3 terms hi + mid + lo with E8M0 32-block scales s0 (the smallest
+// power of two with amax <= 448 s0), s1 = s0 / 16 and s2 = s1 / 32: each term
+// is the E4M3 rounding of what the terms before it left over.  Term 0 leaves
+// at most 16 s0 (half its widest spacing, 32), i.e. <= 256 s1, which E4M3
+// holds; term 1 then leaves at most 8 s1 = 256 s2, and term 2 at most
+// 8 s2 = s0 / 64 <= 2^-13.8 of the block amax.  Only term 0's scale needs the
+// block maximum (one cross-lane reduction per split).  The terms are rows 0..2
+// of the A operand of v_mfma_scale_f32_16x16x128_f8f6f4.
 #pragma once
 #include "mx_device.h"
 
@@ -42,6 +45,13 @@ __device__ __forceinline__ float e8m0_value(uint32_t code) {
     return code > 0u ? __uint_as_float(code << 23) : __uint_as_float(0x00400000u);
 }
 
+// E8M0 codes of the three terms' scales from term 0's: s1 = s0 / 2^4, s2 = s0 / 2^9
+// (clamped at the smallest code, which only makes a scale coarser, never overflowing).
+constexpr int kTermShift[kTerms] = {0, 4, 9};
+__device__ __forceinline__ uint32_t term_code(uint32_t code0, int t) {
+    return code0 > (uint32_t)kTermShift[t] ? code0 - (uint32_t)kTermShift[t] : 0u;
+}
+
 // max over the 4 lanes of a quad (DPP quad permutes: no LDS round trip)
 __device__ __forceinline__ float quad_max(float v) {
     const float a = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // xor 1
@@ -54,16 +64,16 @@ __device__ __forceinline__ float quad_max(float v) {
 // aligned) into kTerms E4M3 terms: word8[t] receives the 8 E4M3 bytes of term
 // t and codes (byte t) the term's E8M0 scale code.  Each term is the E4M3
 // rounding of what the previous terms left over, so the terms sum to the value
-// up to the last term's rounding, relative to the block amax (about 2^-12 of it).
+// up to the last term's rounding (at most 2^-13.8 of the block amax).
 __device__ __forceinline__ void split8(float v[8], uint64_t word8[kTerms], uint32_t& codes) {
     codes = 0;
+    float am = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
+    const uint32_t code0 = e4m3_block_code(quad_max(am));
 #pragma unroll
     for (int t = 0; t < kTerms; ++t) {
-        float am = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) am = fmaxf(am, __builtin_fabsf(v[i]));
-        am = quad_max(am);
-        const uint32_t code = e4m3_block_code(am);
+        const uint32_t code = term_code(code0, t);
         const float sc = e8m0_value(code);
         uint32_t word[2];
 #pragma unroll
@@ -97,12 +107,12 @@ __device__ __forceinline__ float oct_max(float v) {
 // the 4 E4M3 bytes of term t and codes (byte t) the term's E8M0 scale code.
 __device__ __forceinline__ void split4(float v[4], uint32_t word4[kTerms], uint32_t& codes) {
     codes = 0;
+    const float am = fmaxf(fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1])),
+                           fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
+    const uint32_t code0 = e4m3_block_code(oct_max(am));
 #pragma unroll
     for (int t = 0; t < kTerms; ++t) {
-        float am = fmaxf(fmaxf(__builtin_fabsf(v[0]), __builtin_fabsf(v[1])),
-                         fmaxf(__builtin_fabsf(v[2]), __builtin_fabsf(v[3])));
-        am = oct_max(am);
-        const uint32_t code = e4m3_block_code(am);
+        const uint32_t code = term_code(code0, t);
         const float sc = e8m0_value(code);
         mx::v2s p = {0, 0};
         p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v[0], v[1], sc, false);
@@ -137,9 +147,10 @@ __device__ __forceinline__ float max32(float v) {
 __device__ __forceinline__ uint32_t split32(float v, uint32_t& codes) {
     uint32_t bytes = 0;
     codes = 0;
+    const uint32_t code0 = e4m3_block_code(max32(__builtin_fabsf(v)));
 #pragma unroll
     for (int t = 0; t < kTerms; ++t) {
-        const uint32_t code = e4m3_block_code(max32(__builtin_fabsf(v)));
+        const uint32_t code = term_code(code0, t);
         const float sc = e8m0_value(code);
         mx::v2s p = {0, 0};
         p = __builtin_amdgcn_cvt_scalef32_pk_fp8_f32(p, v, 0.0f, sc, false);

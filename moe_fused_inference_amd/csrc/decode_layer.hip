@@ -59,9 +59,10 @@
 // reads of a phase issue back to back ahead of the MFMA chain.
 //
 // Activations on the MFMA: there is no bf16 x FP4 MFMA, so the bf16 x (and the
-// fp32 h) is split into three E4M3 terms hi + mid + lo, each with its own E8M0
-// 32-block scale, that sum back to the value to about 12 significant bits
-// (exactly, for bf16 x).  The three terms are rows 0..2 of the 16-row A
+// fp32 h) is split into three E4M3 terms hi + mid + lo with E8M0 32-block
+// scales s0, s0 / 16 and s0 / 512 (decode_common.h), that sum back to the
+// value to within 2^-13.8 of its block's amax (exactly, for a bf16 x not far
+// below its block's amax).  The three terms are rows 0..2 of the 16-row A
 // operand of v_mfma_scale_f32_16x16x128_f8f6f4 (A = E4M3, B = E2M1), so one
 // MFMA yields all three partial products and y = D[0] + D[1] + D[2]; the other
 // 13 rows are zero and cost nothing in an HBM-bound kernel.

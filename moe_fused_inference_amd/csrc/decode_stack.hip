@@ -549,13 +549,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                 const uint32_t c = sm.xr[(base + g) * kRecBytes + 96 + rr];
                 asc[i] = ok ? c : 127u;
             }
+            // K step outer, tiles inner, held in that order (sched_barrier): NT independent
+            // accumulations in flight.  Left to itself the scheduler emits each tile's four
+            // steps back to back, and a dependent MFMA waits out its predecessor (~60 clocks
+            // issue to issue against ~37 for independent ones)
             mx::v4f acc[NT];
 #pragma unroll
-            for (int m = 0; m < NT; ++m) {
-                acc[m] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
+            for (int m = 0; m < NT; ++m) acc[m] = (mx::v4f){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+                for (int m = 0; m < NT; ++m)
                     acc[m] = mx::mfma16_fp8a_fp4b(av[i], bq[m][i], acc[m], asc[i], (bs[m][i] >> (8 * g)) & 0xFFu);
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int m = 0; m < NT; ++m) mx::pin(acc[m]);
@@ -618,7 +624,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         // accumulations interleaved); publish y_s
         {
             const uint8_t* h8 = sm.hr + 32 * rr;   // term rr of block 0
-            mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+            // all A operands first, then the two tiles' steps interleaved and held in that
+            // order (sched_barrier), as for gate/up
+            mx::v8i av[MS];
+            uint32_t asc[MS];
 #pragma unroll
             for (int i = 0; i < MS; ++i) {
                 // step i, blocks 4i + gb (see the gate/up operands)
@@ -632,21 +641,31 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                                                      : &sm.zero[1];
                 const uint8_t* pc = (rok && bown < kb) ? sm.hr + bown * kRecBytes + 96 + rr
                                                        : reinterpret_cast<const uint8_t*>(&sm.code127[0]);
-                const mx::v8i av = cat8(*plo, *phi);
-                const uint32_t asc = *pc;
+                av[i] = cat8(*plo, *phi);
+                asc[i] = *pc;
+            }
+            mx::v4f acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+            for (int i = 0; i < MS; ++i) {
 #pragma unroll
                 for (int k = 0; k < 2; ++k) {
                     const uint32_t bsc = KB4 ? (dsc[k][i] >> (8 * g)) & 0xFFu : dsc[k][i] & 0xFFu;
-                    acc[k] = mx::mfma16_fp8a_fp4b(av, dq[k][i], acc[k], asc, bsc);
+                    acc[k] = mx::mfma16_fp8a_fp4b(av[i], dq[k][i], acc[k], asc[i], bsc);
                 }
+                __builtin_amdgcn_sched_barrier(0);
             }
+            // both tiles' sums before either (conditional) store: with a sum inside the store's
+            // branch the compiler sinks the second tile's MFMA chain behind the first store
+            float ysum[2];
 #pragma unroll
             for (int k = 0; k < 2; ++k) {
                 mx::pin(acc[k]);
-                if (dok[k] && lane < 16)
-                    put_device(part_base(b, s) + c0d + 16 * (cw + 4 * k) + lane,
-                               __float_as_uint(acc[k][0] + acc[k][1] + acc[k][2]), tag);
+                ysum[k] = acc[k][0] + acc[k][1] + acc[k][2];
             }
+#pragma unroll
+            for (int k = 0; k < 2; ++k)
+                if (dok[k] && lane < 16)
+                    put_device(part_base(b, s) + c0d + 16 * (cw + 4 * k) + lane, __float_as_uint(ysum[k]), tag);
         }
         // ---- 5. y of every slot for block cb = 4 jj + cw (lanes 0..31 = its columns); x_{l+1};
         // its E4M3 terms, published with the bf16 value for the other set's next layer

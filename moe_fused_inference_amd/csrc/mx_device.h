@@ -235,7 +235,7 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 // silu_mul on the hardware exp2 and reciprocal (a few ulp from silu_mul):
 // for the fused decode kernels, whose h is split into three E4M3 terms (a
-// relative resolution of 2^-12), and the prefill MoE, whose h is rounded to
+// resolution of 2^-13.8 of the block amax), and the prefill MoE, whose h is rounded to
 // fp16 and then to 4-bit codes, which a few-ulp change moves only for an h
 // within ~1e-6 (relative) of a rounding threshold.
 __device__ __forceinline__ float silu_mul_fast(float g, float u) {
