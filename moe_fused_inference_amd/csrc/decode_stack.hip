@@ -502,24 +502,27 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                     }
                 v2u xw[8];
                 live = poll_words<8, 16>(a, rs, off, ok, tag16(tag - 1u), xw, live);
+                // byte selects (v_perm_b32: selector byte k < 4 takes byte k of the second
+                // operand, 4..7 byte k - 4 of the first, 0x0c a zero): columns 0, 1 and 2, 3
+                // interleaved first, then term t's four bytes, the block's codes and the bf16 pairs
 #pragma unroll
                 for (int i = 0; i < 2; ++i) {
                     if (256 * i + 4 * lane < nq) {
                         const int c0 = q0 + 256 * i + 4 * lane;
                         uint8_t* rec = sm.xr + (c0 >> 5) * kRecBytes;
-#pragma unroll
-                        for (int t = 0; t < kTerms; ++t) {
-                            uint32_t d = 0;
-#pragma unroll
-                            for (int c = 0; c < 4; ++c) d |= ((xw[4 * i + c].x >> (8 * t)) & 0xFFu) << (8 * c);
-                            *reinterpret_cast<uint32_t*>(rec + 32 * t + (c0 & 31)) = d;
-                        }
-                        if ((c0 & 31) == 0)
-                            *reinterpret_cast<uint32_t*>(rec + 96) =
-                                (xw[4 * i].x >> 24) | ((xw[4 * i + 1].x >> 24) << 8) | ((xw[4 * i + 2].x >> 24) << 16);
+                        const uint32_t w0 = xw[4 * i].x, w1 = xw[4 * i + 1].x, w2 = xw[4 * i + 2].x, w3 = xw[4 * i + 3].x;
+                        const uint32_t q01 = __builtin_amdgcn_perm(w1, w0, 0x05010400u);   // w0.0 w1.0 w0.1 w1.1
+                        const uint32_t q23 = __builtin_amdgcn_perm(w3, w2, 0x05010400u);
+                        const uint32_t r01 = __builtin_amdgcn_perm(w1, w0, 0x07030602u);   // w0.2 w1.2 w0.3 w1.3
+                        const uint32_t r23 = __builtin_amdgcn_perm(w3, w2, 0x07030602u);
+                        *reinterpret_cast<uint32_t*>(rec + (c0 & 31)) = __builtin_amdgcn_perm(q23, q01, 0x05040100u);
+                        *reinterpret_cast<uint32_t*>(rec + 32 + (c0 & 31)) = __builtin_amdgcn_perm(q23, q01, 0x07060302u);
+                        *reinterpret_cast<uint32_t*>(rec + 64 + (c0 & 31)) = __builtin_amdgcn_perm(r23, r01, 0x05040100u);
+                        if ((c0 & 31) == 0)   // codes of terms 0..2: byte 3 of the block's columns 0..2
+                            *reinterpret_cast<uint32_t*>(rec + 96) = __builtin_amdgcn_perm(r23, r01, 0x0c060302u);
                         *reinterpret_cast<uint2*>(&sm.xb[c0]) =
-                            make_uint2((xw[4 * i].y & 0xFFFFu) | (xw[4 * i + 1].y << 16),
-                                       (xw[4 * i + 2].y & 0xFFFFu) | (xw[4 * i + 3].y << 16));
+                            make_uint2(__builtin_amdgcn_perm(xw[4 * i + 1].y, xw[4 * i].y, 0x05040100u),
+                                       __builtin_amdgcn_perm(xw[4 * i + 3].y, xw[4 * i + 2].y, 0x05040100u));
                     }
                 }
             }
