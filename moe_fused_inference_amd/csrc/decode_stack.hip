@@ -438,10 +438,26 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                 const v4u q = __builtin_amdgcn_raw_buffer_load_b128(rw, woffd[k] + 16 * min(4 * i + g, kb - 1), 0, 0);
                 dq[k][i] = make_uint4(q.x, q.y, q.z, q.w);
             }
+            if (KB4 && kb == 4 * MS) {
+                // the row's MS scale dwords are contiguous: 16-byte loads and an 8-byte tail
+                // (fewer load instructions in the layer's burst)
 #pragma unroll
-            for (int i = 0; i < MS; ++i) {
-                if (KB4) dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + 4 * min(i, (kb >> 2) - 1), 0, 0);
-                else dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b8(rs, soffd[k] + min(4 * i + g, kb - 1), 0, 0);
+                for (int i = 0; i + 4 <= MS; i += 4) {
+                    const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs, soffd[k] + 4 * i, 0, 0);
+                    dsc[k][i] = v.x, dsc[k][i + 1] = v.y, dsc[k][i + 2] = v.z, dsc[k][i + 3] = v.w;
+                }
+#pragma unroll
+                for (int i = MS & ~3; i + 2 <= MS; i += 2) {
+                    const v2u v = __builtin_amdgcn_raw_buffer_load_b64(rs, soffd[k] + 4 * i, 0, 0);
+                    dsc[k][i] = v.x, dsc[k][i + 1] = v.y;
+                }
+                if (MS & 1) dsc[k][MS - 1] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + 4 * (MS - 1), 0, 0);
+            } else {
+#pragma unroll
+                for (int i = 0; i < MS; ++i) {
+                    if (KB4) dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b32(rs, soffd[k] + 4 * min(i, (kb >> 2) - 1), 0, 0);
+                    else dsc[k][i] = __builtin_amdgcn_raw_buffer_load_b8(rs, soffd[k] + min(4 * i + g, kb - 1), 0, 0);
+                }
             }
         }
     };
