@@ -76,6 +76,7 @@ constexpr int kGrid = kXcds * kPerXcd;
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kMaxNT = 8;             // gate/up tiles per workgroup (Mi <= 1024)
+static_assert(kMaxNT <= 2 * kWaves, "the g/u publish takes at most two tiles per wave");
 constexpr int kLdsLayers = 128;       // layers whose routing and weight pointers are staged in LDS
 constexpr int kRecBytes = 112;        // LDS record of 32 values: 3 x 32 term bytes, codes at 96..98
 
@@ -590,14 +591,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             }
         }
         lds_barrier();                                                   // B2: gate/up partial sums
-        // publish the g/u values of tile m (wave m % 4): lane r = row r
-        for (int m = cw; m < NT; m += kWaves) {
+        // publish the g/u values of tiles cw and cw + 4 in one pass: lane 16 i + r = row r of
+        // tile cw + 4 i (NT <= 8: at most two tiles per wave)
+        {
+            const int m = cw + kWaves * (lane >> 4);
             const int t = jj + kPerSet * m;
-            if (lane < 16 && t < ntile) {
+            if (lane < 32 && m < NT && t < ntile) {
                 float v = 0.0f;
 #pragma unroll
-                for (int w = 0; w < kWaves; ++w) v += sm.red[w][m][lane];
-                put_local(gu_base(b) + t * 16 + lane, __float_as_uint(v), tag);
+                for (int w = 0; w < kWaves; ++w) v += sm.red[w][m][lane & 15];
+                put_local(gu_base(b) + t * 16 + (lane & 15), __float_as_uint(v), tag);
             }
         }
         // ---- 3. the slot's g/u for this wave's 32-blocks of h (rows r0 .. r0 + nr), row 64k + lane
