@@ -239,6 +239,13 @@ __device__ __forceinline__ bool poll_tagged(const StackArgs& a, __amdgpu_buffer_
     return r;
 }
 
+// Word position of column col's x word within the XCD's x buffer: inside each
+// 256-column block, column 4 j + c sits at 64 c + j, so the x poll of lane j
+// (columns 4 j .. 4 j + 3 of a block) issues four lane-contiguous loads (4
+// cache lines each instead of 16).  A permutation of each block (H is a
+// multiple of 512).
+__device__ __forceinline__ int xpos(int col) { return (col & ~255) | ((col & 3) << 6) | ((col >> 2) & 63); }
+
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t region(const uint64_t* p, int words) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(p), (short)0, words * 8, 0x00020000);
 }
@@ -506,7 +513,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             } else {
                 // published (already split) in layer l-1 by the other set: one word per column,
                 // [term bytes 0..2 | code of term (column % 32) for columns 0..2 of a block |
-                //  bf16 | tag16]; lane -> columns q0 + 256 i + 4 lane .. +3
+                //  bf16 | tag16] at word xpos(column); lane -> columns q0 + 256 i + 4 lane .. +3
                 const __amdgpu_buffer_rsrc_t rs = region(x_base((b + kNBuf - 1) % kNBuf), H);
                 uint32_t off[8];
                 bool ok[8];
@@ -515,7 +522,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
 #pragma unroll
                     for (int c = 0; c < 4; ++c) {
                         ok[4 * i + c] = 256 * i + 4 * lane < nq;
-                        off[4 * i + c] = (uint32_t)((q0 + min(256 * i + 4 * lane, nq - 4) + c) * 8);
+                        off[4 * i + c] = (uint32_t)(xpos(q0 + min(256 * i + 4 * lane, nq - 4) + c) * 8);
                     }
                 v2u xw[8];
                 live = poll_words<8, 16>(a, rs, off, ok, tag16(tag - 1u), xw, live);
@@ -724,7 +731,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                     uint32_t codes;
                     const uint32_t bytes = split32(mx::bf16_to_f32(xn), codes);   // over lanes 0..31
                     const uint32_t code = (lane & 31) < kTerms ? (codes >> (8 * (lane & 31))) & 0xFFu : 0u;
-                    if (ccol) put_word(x_base(b) + col, bytes | (code << 24), (uint32_t)xn | (tag16(tag) << 16));
+                    if (ccol) put_word(x_base(b) + xpos(col), bytes | (code << 24), (uint32_t)xn | (tag16(tag) << 16));
                 } else if (s == 0 && ccol) {
                     a.x_out[col] = xn;
                 }
