@@ -618,20 +618,22 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             const int blo = min(cw * bph, kb), bhi = min(blo + bph, kb);
             const int r0 = 32 * blo, nr = 32 * (bhi - blo);
             const __amdgpu_buffer_rsrc_t rs = region(gu_base(b), 2 * Mi);
-            uint32_t off[8];
-            bool ok[8];
-            uint32_t gv[8];
+            // KG groups of 64 rows: bph <= MS blocks, so nr <= 32 MS rows
+            constexpr int KG = (MS + 1) / 2;
+            uint32_t off[2 * KG];
+            bool ok[2 * KG];
+            uint32_t gv[2 * KG];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < KG; ++k) {
                 const int row = r0 + min(64 * k + lane, max(nr - 1, 0));
-                ok[k] = ok[4 + k] = 64 * k + lane < nr;
+                ok[k] = ok[KG + k] = 64 * k + lane < nr;
                 off[k] = (uint32_t)(min(row, Mi - 1) * 8);
-                off[4 + k] = (uint32_t)((Mi + min(row, Mi - 1)) * 8);
+                off[KG + k] = (uint32_t)((Mi + min(row, Mi - 1)) * 8);
             }
-            live = poll_tagged<8>(a, rs, off, ok, tag, gv, live);
+            live = poll_tagged<2 * KG>(a, rs, off, ok, tag, gv, live);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float h = mx::silu_mul_fast(__uint_as_float(gv[k]), __uint_as_float(gv[4 + k]));
+            for (int k = 0; k < KG; ++k) {
+                const float h = mx::silu_mul_fast(__uint_as_float(gv[k]), __uint_as_float(gv[KG + k]));
                 if (64 * k < nr && ok[k]) sm.hs[r0 + 64 * k + lane] = h;   // 64k < nr: wave-uniform
             }
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the wave's own h values, read below
