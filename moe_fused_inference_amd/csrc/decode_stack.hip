@@ -705,27 +705,41 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             if (cb < hb) {
                 const bool ccol = lane < 32;
                 const int col = 32 * cb + (lane & 31);
-                // slot t's y at word t*part_q + col of the y region
+                // slot t's y at word t*part_q + col of the y region; lanes 0..31 poll slots
+                // 0..3 and lanes 32..63 slots 4..7 of the same 32 columns (four loads a lane)
+                static_assert(kMaxE == 8, "the y poll splits the slots over the two wave halves");
+                const int hf = lane >> 5;
                 const __amdgpu_buffer_rsrc_t rs = region(part_base(b, 0), E * a.part_q);
-                uint32_t off[kMaxE];
-                bool ok[kMaxE];
-                uint32_t yv[kMaxE];
+                uint32_t off[4];
+                bool ok[4];
+                uint32_t yv[4];
 #pragma unroll
-                for (int t = 0; t < kMaxE; ++t) {
-                    ok[t] = ccol && t < E;
-                    off[t] = (uint32_t)((min(t, E - 1) * a.part_q + col) * 8);
+                for (int j = 0; j < 4; ++j) {
+                    const int t = 4 * hf + j;
+                    ok[j] = t < E;
+                    off[j] = (uint32_t)((min(t, E - 1) * a.part_q + col) * 8);
                 }
-                live = poll_tagged<kMaxE>(a, rs, off, ok, tag, yv, live);
+                live = poll_tagged<4>(a, rs, off, ok, tag, yv, live);
                 // the one-layer kernel's order: per slot pair (2w, 2w+1) a fused
-                // multiply-add chain from 0, then the four pair sums left to right
-                float y = 0.0f;
+                // multiply-add chain from 0, then the four pair sums left to right;
+                // pairs 2, 3 come from the upper half (permlane32 swap: lane i < 32
+                // reads lane i + 32 in element 1)
+                float pr[2];
 #pragma unroll
-                for (int w = 0; w < kMaxE / 2; ++w) {
+                for (int u = 0; u < 2; ++u) {
+                    const int t0 = 4 * hf + 2 * u;
+                    const float w0 = hf ? wt[4 + 2 * u] : wt[2 * u], w1 = hf ? wt[5 + 2 * u] : wt[1 + 2 * u];
                     float part = 0.0f;
-                    if (2 * w < E) part = fmaf(wt[2 * w], __uint_as_float(yv[2 * w]), part);
-                    if (2 * w + 1 < E) part = fmaf(wt[2 * w + 1], __uint_as_float(yv[2 * w + 1]), part);
-                    y = w == 0 ? part : y + part;
+                    if (t0 < E) part = fmaf(w0, __uint_as_float(yv[2 * u]), part);
+                    if (t0 + 1 < E) part = fmaf(w1, __uint_as_float(yv[2 * u + 1]), part);
+                    pr[u] = part;
                 }
+                const auto up0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pr[0]), __float_as_uint(pr[0]), false, false);
+                const auto up1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(pr[1]), __float_as_uint(pr[1]), false, false);
+                float y = pr[0];
+                y = y + pr[1];
+                y = y + __uint_as_float(up0[1]);
+                y = y + __uint_as_float(up1[1]);
                 // runtime/model_runner_v2.py:208: x = x + moe.bfloat16() in bf16
                 const float yb = mx::bf16_to_f32(mx::f32_to_bf16_rne(y));
                 const uint16_t xn = mx::f32_to_bf16_rne(mx::bf16_to_f32(sm.xb[col]) + yb);
