@@ -228,6 +228,30 @@ __device__ __forceinline__ bool poll_words(const StackArgs& a, __amdgpu_buffer_r
     }
 }
 
+// poll_words with 16-byte loads: load i (byte offset off[i], 16-byte aligned)
+// brings words w[2i] and w[2i+1], each single-copy atomic on its own.
+template <int N, int TSH = 0>
+__device__ __forceinline__ bool poll_pairs(const StackArgs& a, __amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[N],
+                                           const bool (&ok)[N], uint32_t tag, v2u (&w)[2 * N], bool live) {
+    int spins = 0;
+    while (true) {
+#pragma unroll
+        for (int i = 0; i < N; ++i) {
+            const v4u v = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], 0, 16);
+            w[2 * i] = v2u{v.x, v.y};
+            w[2 * i + 1] = v2u{v.z, v.w};
+        }
+        bool pending = false;
+#pragma unroll
+        for (int i = 0; i < N; ++i) pending |= ok[i] && ((w[2 * i].y >> TSH) != tag || (w[2 * i + 1].y >> TSH) != tag);
+        if (!live) return false;
+        if (__builtin_amdgcn_ballot_w64(pending) == 0) return true;   // the wave polls as one
+        if (++spins >= kSpinLimit || ((spins & 255) == 0 && error_set(a))) return false;
+        __builtin_amdgcn_s_sleep(1);
+        asm volatile("" ::: "memory");   // the words may change: reload them next round
+    }
+}
+
 // poll_words for (value, 32-bit tag) words: v[i] = the values
 template <int N>
 __device__ __forceinline__ bool poll_tagged(const StackArgs& a, __amdgpu_buffer_rsrc_t rs, const uint32_t (&off)[N],
@@ -240,11 +264,13 @@ __device__ __forceinline__ bool poll_tagged(const StackArgs& a, __amdgpu_buffer_
 }
 
 // Word position of column col's x word within the XCD's x buffer: inside each
-// 256-column block, column 4 j + c sits at 64 c + j, so the x poll of lane j
-// (columns 4 j .. 4 j + 3 of a block) issues four lane-contiguous loads (4
-// cache lines each instead of 16).  A permutation of each block (H is a
-// multiple of 512).
-__device__ __forceinline__ int xpos(int col) { return (col & ~255) | ((col & 3) << 6) | ((col >> 2) & 63); }
+// 256-column block, column 4 j + c sits at 128 (c >> 1) + 2 j + (c & 1), so the
+// x poll of lane j (columns 4 j .. 4 j + 3 of a block) is two lane-contiguous
+// 16-byte loads, each bringing two of its columns (8 cache lines a load).  A
+// permutation of each block (H is a multiple of 512).
+__device__ __forceinline__ int xpos(int col) {
+    return (col & ~255) | ((col & 2) << 6) | (((col >> 2) & 63) << 1) | (col & 1);
+}
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t region(const uint64_t* p, int words) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(p), (short)0, words * 8, 0x00020000);
@@ -515,17 +541,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
                 // [term bytes 0..2 | code of term (column % 32) for columns 0..2 of a block |
                 //  bf16 | tag16] at word xpos(column); lane -> columns q0 + 256 i + 4 lane .. +3
                 const __amdgpu_buffer_rsrc_t rs = region(x_base((b + kNBuf - 1) % kNBuf), H);
-                uint32_t off[8];
-                bool ok[8];
+                uint32_t off[4];
+                bool ok[4];
 #pragma unroll
                 for (int i = 0; i < 2; ++i)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) {
-                        ok[4 * i + c] = 256 * i + 4 * lane < nq;
-                        off[4 * i + c] = (uint32_t)(xpos(q0 + min(256 * i + 4 * lane, nq - 4) + c) * 8);
+                    for (int j = 0; j < 2; ++j) {   // columns 2j, 2j+1 of the lane's four (adjacent words)
+                        ok[2 * i + j] = 256 * i + 4 * lane < nq;
+                        off[2 * i + j] = (uint32_t)(xpos(q0 + min(256 * i + 4 * lane, nq - 4) + 2 * j) * 8);
                     }
-                v2u xw[8];
-                live = poll_words<8, 16>(a, rs, off, ok, tag16(tag - 1u), xw, live);
+                v2u xw[8];   // xw[4 i + c]: column c of the lane's four in group i
+                live = poll_pairs<4, 16>(a, rs, off, ok, tag16(tag - 1u), xw, live);
                 // byte selects (v_perm_b32: selector byte k < 4 takes byte k of the second
                 // operand, 4..7 byte k - 4 of the first, 0x0c a zero): columns 0, 1 and 2, 3
                 // interleaved first, then term t's four bytes, the block's codes and the bf16 pairs
