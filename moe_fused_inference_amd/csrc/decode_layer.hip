@@ -239,6 +239,13 @@ __device__ __forceinline__ uint64_t* oproj_words(const LayerArgs& a) {
 }
 __device__ __forceinline__ uint64_t* qkv_words(const LayerArgs& a) { return oproj_words(a) + kMaxH; }
 
+// Word position of o_proj element e among the o_proj words (H = 2048, thread t
+// of 256 holding elements 8t .. 8t+7): element 8t + i sits at 512 (i >> 1) +
+// 2t + (i & 1), so a thread's elements are four adjacent word pairs and each of
+// load_oproj's four 16-byte loads is lane-contiguous (8 cache lines a load
+// instead of 32 for eight 8-byte loads at a 64-byte lane stride).
+__device__ __forceinline__ int opos(int e) { return ((e & 6) << 8) | ((e >> 3) << 1) | (e & 1); }
+
 // o_proj output elements 8t .. 8t+7 of thread t: from `oproj`, or with the
 // front from this launch's o_proj words -- one probe word per wave (the first
 // column of the wave's last thread), then the thread's words until all carry
@@ -256,7 +263,8 @@ __device__ __forceinline__ bool load_oproj(const LayerArgs& a, uint32_t tag, flo
     int spins = 0;
     bool ok = true;
     while (true) {
-        const uint64_t w0 = __hip_atomic_load(words + 8 * (64 * wave + 63), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t w0 = __hip_atomic_load(words + opos(8 * (64 * wave + 63)), __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane((uint32_t)(w0 >> 32)) == tag) break;
         if (++spins >= kSpinLimit) {
             ok = false;
@@ -264,13 +272,17 @@ __device__ __forceinline__ bool load_oproj(const LayerArgs& a, uint32_t tag, flo
         }
         __builtin_amdgcn_s_sleep(2);
     }
+    // agent-scope (sc1) 16-byte loads of two (value, tag) words each
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint64_t*>(words), (short)0, kMaxH * 8, 0x00020000);
     while (ok) {
         bool pending = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint64_t w = __hip_atomic_load(words + k0 + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            of[i] = __uint_as_float((uint32_t)w);
-            pending |= (uint32_t)(w >> 32) != tag;
+        for (int j = 0; j < 4; ++j) {
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(rs, (uint32_t)((opos(k0 + 2 * j)) * 8), 0, 16);
+            of[2 * j] = __uint_as_float(w.x);
+            of[2 * j + 1] = __uint_as_float(w.z);
+            pending |= w.y != tag || w.w != tag;
         }
         if (!pending) break;
         if (++spins >= kSpinLimit) {
@@ -576,7 +588,7 @@ __device__ __forceinline__ void oproj_wg(const LayerArgs& a, Smem& sm, int oi) {
         float t = sm.o.red[0][tid];
 #pragma unroll
         for (int p = 1; p < 8; ++p) t += sm.o.red[p][tid];
-        __hip_atomic_store(oproj_words(a) + 16 * oi + tid, (uint64_t)__float_as_uint(t) | ((uint64_t)tag << 32),
+        __hip_atomic_store(oproj_words(a) + opos(16 * oi + tid), (uint64_t)__float_as_uint(t) | ((uint64_t)tag << 32),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (a.oproj_out) a.oproj_out[16 * oi + tid] = t;
     }
