@@ -239,11 +239,11 @@ __device__ __forceinline__ uint64_t* oproj_words(const LayerArgs& a) {
 }
 __device__ __forceinline__ uint64_t* qkv_words(const LayerArgs& a) { return oproj_words(a) + kMaxH; }
 
-// Word position of o_proj element e among the o_proj words (H = 2048, thread t
-// of 256 holding elements 8t .. 8t+7): element 8t + i sits at 512 (i >> 1) +
-// 2t + (i & 1), so a thread's elements are four adjacent word pairs and each of
-// load_oproj's four 16-byte loads is lane-contiguous (8 cache lines a load
-// instead of 32 for eight 8-byte loads at a 64-byte lane stride).
+// Word position of element e among the o_proj words and the MoE output words
+// (H = 2048, thread t of 256 reading elements 8t .. 8t+7): element 8t + i sits
+// at 512 (i >> 1) + 2t + (i & 1), so a thread's elements are four adjacent word
+// pairs and each of its four 16-byte loads is lane-contiguous (8 cache lines a
+// load instead of 32 for eight 8-byte loads at a 64-byte lane stride).
 __device__ __forceinline__ int opos(int e) { return ((e & 6) << 8) | ((e >> 3) << 1) | (e & 1); }
 
 // o_proj output elements 8t .. 8t+7 of thread t: from `oproj`, or with the
@@ -713,8 +713,10 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
     const int k0 = 8 * tid;
     const uint4 q = *reinterpret_cast<const uint4*>(a.xres + k0);
     const uint4 wn = *reinterpret_cast<const uint4*>(a.qnw + k0);
-    // this launch's MoE output of columns k0 .. k0+7
-    const uint64_t* yw = out_words(a) + k0;
+    // this launch's MoE output of columns k0 .. k0+7 (out words at opos(column): four
+    // lane-contiguous 16-byte loads)
+    const __amdgpu_buffer_rsrc_t yrs =
+        __builtin_amdgcn_make_buffer_rsrc(out_words(a), (short)0, kMaxH * 8, 0x00020000);
     const uint32_t tag = (uint32_t)(launch + 1);
     float of[8], yo[8];
     // one probe word per wave first (the first column of the wave's last
@@ -723,7 +725,7 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
     bool ok = cfg == a.cfg && load_oproj(a, tag, of);
     int spins = 0;
     while (ok) {
-        const uint64_t w0 = __hip_atomic_load(out_words(a) + 8 * (64 * wave + 63), __ATOMIC_RELAXED,
+        const uint64_t w0 = __hip_atomic_load(out_words(a) + opos(8 * (64 * wave + 63)), __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_AGENT);
         if (__builtin_amdgcn_readfirstlane((uint32_t)(w0 >> 32)) == tag) break;
         if (++spins >= kSpinLimit) {
@@ -735,10 +737,11 @@ __device__ __forceinline__ void qkv_wg(const LayerArgs& a, Smem& sm, float* nred
     while (ok) {
         bool pending = false;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const uint64_t w = __hip_atomic_load(yw + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            yo[i] = __uint_as_float((uint32_t)w);
-            pending |= (uint32_t)(w >> 32) != tag;
+        for (int j = 0; j < 4; ++j) {
+            const v4u w = __builtin_amdgcn_raw_buffer_load_b128(yrs, (uint32_t)(opos(k0 + 2 * j) * 8), 0, 16);
+            yo[2 * j] = __uint_as_float(w.x);
+            yo[2 * j + 1] = __uint_as_float(w.z);
+            pending |= w.y != tag || w.w != tag;
         }
         if (!pending) break;
         if (++spins >= kSpinLimit) {
@@ -1253,7 +1256,8 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
                         sm.b.red[3][threadIdx.x];
         a.out[c] = y;
         if (ROUTE == ROUTE_FUSED && a.nq > 0)   // for the q|k|v tail: (value, this launch's tag)
-            __hip_atomic_store(out_words(a) + c, (uint64_t)__float_as_uint(y) | ((uint64_t)(uint32_t)(launch + 1) << 32),
+            __hip_atomic_store(out_words(a) + opos(c),
+                               (uint64_t)__float_as_uint(y) | ((uint64_t)(uint32_t)(launch + 1) << 32),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (a.resid) {
             // runtime/model_runner_v2.py:208: x = x + moe.bfloat16() in bf16
