@@ -498,8 +498,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
 
     if (!STRICT) {
         const LayerRoute rt = route(min(par, L - 1));
-        load_gu(rt, par < L);
         load_dn(rt, par < L);
+        load_gu(rt, par < L);
     }
     bool live = true;
     for (int l = par; l < L; l += 2) {
@@ -580,8 +580,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         }
         if (STRICT) {
             const LayerRoute rt = route(l);
-            load_gu(rt, true);
             load_dn(rt, true);
+            load_gu(rt, true);
         }
         // ---- 2. gate/up MFMAs: A = x_l terms (rows 0..2), B = the tile's weight rows
         {
@@ -787,8 +787,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
         if (!STRICT) {
             // layer l+2 streams while the other set computes layer l+1
             const LayerRoute rt = route(l + 2 < L ? l + 2 : l);
-            load_gu(rt, l + 2 < L);
             load_dn(rt, l + 2 < L);
+            load_gu(rt, l + 2 < L);
         }
     }
     if (!live) set_error(a);
