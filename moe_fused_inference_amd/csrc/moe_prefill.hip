@@ -214,9 +214,10 @@ __device__ __forceinline__ uint64_t same_id_lanes(int id, bool valid, int bits) 
 __device__ __forceinline__ int id_bits(int n_exp) { return 32 - __clz(max(n_exp - 1, 1)); }
 
 __global__ __launch_bounds__(64 * kRtWaves) void route_count_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
-                                                                   int* __restrict__ hist) {
+                                                                   int* __restrict__ hist, int* __restrict__ qctr) {
     __shared__ int h[kMaxExperts];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (qctr && blockIdx.x == 0 && tid < 16) qctr[tid] = 0;   // the grouped GEMMs' tile queues (8 each)
     for (int e = tid; e < n_exp; e += 64 * kRtWaves) h[e] = 0;
     const int bits = id_bits(n_exp);
     int id[kRtGroups];
@@ -833,7 +834,7 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_dma_kernel(GArgs g, W w) 
 // mostly hit L2, in a 2-stage ring: during step k the copies of the token
 // rows of step k+1 and of the weight rows of step k+2 are in flight, in that
 // order, so the wait at the top of step k+1 leaves the last five copies (the
-// weights of step k+2) outstanding.  One workgroup per CU (153 KB of LDS).
+// weights of step k+2) outstanding.  One workgroup per CU (156 KB of LDS).
 //  * The token tile is sized to the expert's count in 64-row steps (only
 //    ceil(rows / 64) * 64 token rows are copied), and a wave issues the MFMAs
 //    of only those of its 32-token blocks that hold routed tokens, so an
@@ -841,9 +842,9 @@ __global__ __launch_bounds__(256, 2) void grouped_gemm_dma_kernel(GArgs g, W w) 
 //    wave (wm, wn) is tile block 2i + wm: the two waves of a SIMD share the
 //    routed rows, so each one's MFMAs run while the other waits on its
 //    operand reads, which are issued one MFMA substep ahead.
-//  * All tiles of one expert take workgroup numbers of one residue mod 8,
-//    i.e. run on one XCD (workgroups are dealt to the 8 XCDs round-robin),
-//    so the expert's gathered token rows are fetched into one L2.
+//  * All tiles of one expert run on workgroups of one residue mod 8, i.e.
+//    on one XCD (workgroups are dealt to the 8 XCDs round-robin), so the
+//    expert's gathered token rows are fetched into one L2.
 // Requires Kp % 256 == 0.
 constexpr int X_BM = 192, X_BN = 256;
 constexpr int X_ROWB = 128;                           // bytes per row per K step
@@ -853,10 +854,9 @@ constexpr int X_AST = X_A + X_BM * 8;                 // token stage: rows + 8 s
 constexpr int X_WST = X_W + X_BN * 8;                 // weight stage
 constexpr int X_ARING = 3 * X_WST;                    // the token ring follows the 3-stage weight ring
 constexpr int X_THREADS = 512;
-constexpr int X_TROW = 144;                           // down transpose: bytes per row (128 + 16 of pad)
 constexpr int X_PP = X_ARING + 2 * X_AST;             // the down tile's pair indices and weights
 constexpr int X_LDS = X_PP + 8 * X_BM;
-static_assert(8 * 96 * X_TROW <= X_PP && X_LDS <= 160 * 1024, "x8 LDS layout");
+static_assert(X_LDS <= 160 * 1024, "x8 LDS layout");
 
 // Per-tile copy plan of one wave: na token-row blocks (8 rows of 128 bytes
 // each), 4 weight-row blocks, one weight-scale copy (32 rows x 8 bytes) and,
@@ -867,21 +867,33 @@ struct XCopies {
     int na;
 };
 
-template <int MODE, class W>
-__device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, int e, int n0, int off, int mt,
-                                        int mrows, int wave, int lane) {
-    const uint32_t cbytes = (uint32_t)g.Kp >> 1, nch = (uint32_t)g.Kp >> 5;
-    const int slot = lane & 7, lrow = lane >> 3;
-    c.na = (mrows + 63) >> 6;
-    auto src_row = [&](int r) {   // token (gate/up) or sorted h row (down) of tile row r
+// Source rows of a wave's copies of one token tile: the rows of its three
+// token-row blocks (64j + 8*wave + lane/8) and of its token-scale copy
+// (32*wave + lane/2), clamped to the tile.  Gate/up: the sorted pair index
+// (the token is it / topk, taken by x8_plan_rows); down: the sorted h row.
+template <int MODE>
+__device__ __forceinline__ void x8_rows(int (&rw)[4], const GArgs& g, int off, int mt, int mrows, int wave, int lane) {
+    auto src = [&](int r) {
         const int rc = min(r, mrows - 1);
-        return MODE == MODE_GATEUP ? g.pairs[off + mt + rc] / g.topk : off + mt + rc;
+        return MODE == MODE_GATEUP ? g.pairs[off + mt + rc] : off + mt + rc;
     };
+#pragma unroll
+    for (int j = 0; j < 3; ++j) rw[j] = src(64 * j + 8 * wave + (lane >> 3));
+    rw[3] = src(32 * wave + (lane >> 1));
+}
+
+template <int MODE, class W>
+__device__ __forceinline__ void x8_plan_rows(XCopies& c, const GArgs& g, const W& w, int e, int n0, int mrows,
+                                             const int (&rw)[4], int wave, int lane) {
+    const uint32_t cbytes = (uint32_t)g.Kp >> 1, nch = (uint32_t)g.Kp >> 5;
+    const int slot = lane & 7;
+    c.na = (mrows + 63) >> 6;
+    auto row_of = [&](int v) { return MODE == MODE_GATEUP ? v / g.topk : v; };
     c.ars = mx::buf_rsrc(g.aq, (int64_t)g.a_rows * cbytes);
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
-        const int r = 64 * j + 8 * wave + lrow;   // block 8j + wave
-        c.avo[j] = (uint32_t)src_row(r) * cbytes + ((slot ^ mx::swz_key128(r)) << 4);
+        const int r = 64 * j + 8 * wave + (lane >> 3);   // block 8j + wave
+        c.avo[j] = (uint32_t)row_of(rw[j]) * cbytes + ((slot ^ mx::swz_key128(r)) << 4);
     }
     // weight blocks 4*wave + j: rows 32*wave .. +31, one projection
     int proj;
@@ -890,7 +902,7 @@ __device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, 
     c.swrs = mx::buf_rsrc(w.s(e, proj), (int64_t)g.Nw * nch);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int rho = 32 * wave + 8 * j + lrow;
+        const int rho = 32 * wave + 8 * j + (lane >> 3);
         int pj;
         const int rr = min(weight_row<MODE>(rho, n0, pj), g.Nw - 1);
         c.wvo[j] = (uint32_t)rr * cbytes + ((slot ^ mx::swz_key128(rho)) << 4);
@@ -901,7 +913,7 @@ __device__ __forceinline__ void x8_plan(XCopies& c, const GArgs& g, const W& w, 
         const int rr = min(weight_row<MODE>(row, n0, pj), g.Nw - 1);
         c.swvo = (uint32_t)rr * nch + 4 * (lane & 1);
         c.sars = mx::buf_rsrc(g.as, (int64_t)g.a_rows * nch);
-        c.savo = (uint32_t)src_row(row) * nch + 4 * (lane & 1);
+        c.savo = (uint32_t)row_of(rw[3]) * nch + 4 * (lane & 1);
     }
 }
 
@@ -927,11 +939,122 @@ __device__ __forceinline__ void x8_issue_w(const XCopies& c, uint32_t wbuf, int 
     if (part == 2) mx::dma4(c.swvo, c.swrs, (uint32_t)s * 8, wbuf + X_W + 256 * wave);
 }
 
-// K loop and epilogue of one wave on one token tile; NB = the wave's 32-token
-// blocks holding routed tokens (0..3).
-template <int MODE, int NB>
-__device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_t* smem, uint32_t ring, int n0,
-                                        int off, int mt, int mrows, int wave, int lane) {
+// ------------------------------------------------------------------ persistent 192 x 256 tiles
+// grouped_gemm_xp_kernel<MODE>: the tiles above, with one workgroup per CU
+// that takes tiles from its group's queue until the queue is empty.  A
+// tile's plan and first copies (weights of steps 0 and 1, tokens of step 0)
+// are issued during the previous tile's epilogue, so they land while that
+// epilogue runs instead of after one workgroup has exited and the next has
+// started (a workgroup per tile, one per CU: 140 us per config-3b call
+// against 133 us).
+//  * Groups: workgroup b is in group b % 8, i.e. on XCD b % 8 (workgroups
+//    are dealt to the XCDs round-robin), and group x computes the experts
+//    e = x, x+8, ..., so an expert's token rows are fetched into one L2.
+//  * Units: a group's tiles are (expert j, token tile, weight-row tile),
+//    expert-major, then token tile, then weight-row tile, so the weight-row
+//    tiles of an expert run at about the same time and share its token rows.
+//    At the start every workgroup counts its group's units from the expert
+//    counts (a prefix over the group's experts, in LDS); a unit index names
+//    its tile by a ballot over the prefix.  Workgroup k of a group (of P)
+//    takes units k and k + P first; the group's queue (an atomic counter the
+//    route kernel zeroes) hands out the rest from 2P on, one per tile and a
+//    tile ahead, so the next tile is known when a tile starts and its source
+//    rows load during the K loop.
+//  * The weight ring is used from stage 1 on (K step s in stage (s+1) % 3):
+//    the down epilogue transposes its blocks in stage 0, which the next tile
+//    first refills during its step 0, after the barrier every wave reaches
+//    only past its epilogue.  The next tile's copies go to stages 1 and 2
+//    and token stage 0, read by no wave once all are past the last K step.
+//  * Waits: the copies are invisible to the compiler (inline asm), so a load
+//    whose value is used while copies are in flight would make it wait for
+//    all of them.  The loads of a tile (the next tile's source rows, the
+//    queue atomic, the down tile's pair indices and weights) are issued at
+//    its start and used only after its K loop, where no copy is in flight.
+constexpr int XP_TROW = 136;                                // down transpose: 128 B + 8 per row
+static_assert(8 * 32 * XP_TROW <= X_WST, "the down transposes fit weight stage 0");
+constexpr int XP_MAXJ = kMaxExperts / 8;                    // experts per group
+constexpr int XP_UCUM = X_LDS;                              // int[XP_MAXJ + 1]: units of the experts below j
+constexpr int XP_ECNT = XP_UCUM + 4 * (XP_MAXJ + 1);        // int[XP_MAXJ]: expert counts
+constexpr int XP_EOFF = XP_ECNT + 4 * XP_MAXJ;              // int[XP_MAXJ]: expert offsets
+constexpr int XP_SLOT = XP_EOFF + 4 * XP_MAXJ;              // int: the unit the queue handed out
+constexpr int XP_LDS = XP_SLOT + 16;
+static_assert(XP_LDS <= 160 * 1024 && XP_MAXJ <= 128, "xp LDS layout (two experts per lane in the prefix)");
+
+struct XpTile {
+    int e, n0, off, mt, mrows;
+};
+
+// The tile of unit u (uniform): the expert j of the group with
+// ucum[j] <= u < ucum[j+1], found by a ballot over the group's experts.
+template <int MODE>
+__device__ __forceinline__ XpTile xp_tile_of(const uint8_t* smem, int grp, int nj, int ntiles, int u, int lane) {
+    const int* ucum = reinterpret_cast<const int*>(smem + XP_UCUM);
+    int j = 0;
+    for (int b = 0; b < nj; b += 64) {
+        const int jj = b + lane;
+        const bool hit = jj < nj && ucum[jj] <= u && u < ucum[jj + 1];
+        const uint64_t m = __ballot(hit);
+        if (m) {
+            j = b + __ffsll((unsigned long long)m) - 1;
+            break;
+        }
+    }
+    j = __builtin_amdgcn_readfirstlane(j);
+    const int local = u - ucum[j];
+    const int mti = local / ntiles;
+    const int nt = local - mti * ntiles;
+    XpTile t;
+    t.e = grp + 8 * j;
+    t.off = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(smem + XP_EOFF)[j]);
+    const int cnt = __builtin_amdgcn_readfirstlane(reinterpret_cast<const int*>(smem + XP_ECNT)[j]);
+    t.mt = __builtin_amdgcn_readfirstlane(mti * X_BM);
+    t.mrows = min(X_BM, cnt - t.mt);
+    t.n0 = __builtin_amdgcn_readfirstlane(nt * (MODE == MODE_GATEUP ? X_BN / 2 : X_BN));
+    return t;
+}
+
+// A tile's first copies in three parts, in the order the K loop's waits
+// count on: 0, the weights of step 0 (stage 1); 1, the tokens of step 0;
+// 2, the weights of step 1 (stage 2).  Before part 0 the plan's offsets and
+// descriptors pass through an empty asm, so that they (and the compiler's
+// waits for the plan's loads) are complete before the first copy is
+// issued: a wait placed after a copy would also wait for the copy, which
+// the compiler does not count.
+__device__ __forceinline__ void xp_prologue_part(XCopies& c, uint32_t ring, int nsteps, int wave, int part) {
+    if (part == 0) {
+        asm volatile("" : "+v"(c.avo[0]), "+v"(c.avo[1]), "+v"(c.avo[2]), "+v"(c.savo), "+v"(c.wvo[0]),
+                     "+v"(c.wvo[1]), "+v"(c.wvo[2]), "+v"(c.wvo[3]), "+v"(c.swvo), "+s"(c.ars), "+s"(c.wrs),
+                     "+s"(c.sars), "+s"(c.swrs) :: "memory");
+        x8_issue_w(c, ring + X_WST, 0, 2, wave);
+        x8_issue_w(c, ring + X_WST, 0, 3, wave);
+    } else if (part == 1) {
+        x8_issue_a(c, ring + X_ARING, 0, 0, wave);
+        x8_issue_a(c, ring + X_ARING, 0, 1, wave);
+    } else if (nsteps > 1) {
+        x8_issue_w(c, ring + 2 * X_WST, 1, 2, wave);
+        x8_issue_w(c, ring + 2 * X_WST, 1, 3, wave);
+    }
+}
+
+__device__ __forceinline__ void xp_prologue(XCopies& c, uint32_t ring, int nsteps, int wave) {
+    for (int part = 0; part < 3; ++part) xp_prologue_part(c, ring, nsteps, wave, part);
+}
+
+template <int MODE, int NB, class Issue>
+__device__ __forceinline__ void xp_epilogue(mx::v16f (&acc)[3][2], const GArgs& g, uint8_t* smem, const XpTile& t,
+                                            int wave, int lane, Issue&& issue);
+
+// K loop of one wave on tile t (its prologue already issued), then
+// `sync()` (every wave past the K loop, the tile's pair rows in LDS), then
+// the epilogue with the next tile's plan and first copies (`issue(part)`)
+// issued before it and between its blocks: the copies' latency hides under
+// the epilogue, and the epilogue's VALU work fills the time a wave waits
+// for the memory pipeline to accept them.  (All copies after the epilogue
+// measured slower: their latency is then exposed.)
+// NB = the wave's 32-token blocks holding routed tokens (0..3).
+template <int MODE, int NB, class Sync, class Issue>
+__device__ __forceinline__ void xp_tile(const XCopies& c, const GArgs& g, uint8_t* smem, uint32_t ring,
+                                        const XpTile& t, int wave, int lane, Sync&& sync, Issue&& issue) {
     const int wm = wave >> 2, wn = wave & 3;
     const int lr = lane & 31, h = lane >> 5;
     const int key = mx::swz_key128(lr);
@@ -944,25 +1067,6 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
 #pragma unroll
             for (int q = 0; q < 16; ++q) acc[i][j][q] = 0.0f;
 
-    // down: the tile's pair indices and routing weights, loaded before the
-    // first copies and put in LDS after the K loop (a use of a loaded value
-    // makes the compiler wait for every load in flight)
-    int rp = 0;
-    float rs = 0.0f;
-    const int trow = wave * 64 + lane;
-    if (MODE == MODE_DOWN && trow < mrows) {
-        rp = g.pairs[off + mt + trow];
-        rs = g.sscore[off + mt + trow];
-    }
-    // prologue: weights of step 0, tokens of step 0, weights of step 1
-    x8_issue_w(c, ring, 0, 2, wave);
-    x8_issue_w(c, ring, 0, 3, wave);
-    x8_issue_a(c, ring + X_ARING, 0, 0, wave);
-    x8_issue_a(c, ring + X_ARING, 0, 1, wave);
-    if (nsteps > 1) {
-        x8_issue_w(c, ring + X_WST, 1, 2, wave);
-        x8_issue_w(c, ring + X_WST, 1, 3, wave);
-    }
     for (int it = 0; it < nsteps; ++it) {
         // this wave's copies of step it have landed (the weights of step
         // it+1, issued last, may still be in flight) and its reads of step
@@ -972,11 +1076,10 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
         const bool more_a = it + 1 < nsteps, more_w = it + 2 < nsteps;
-        const uint8_t* wst = smem + (it % 3) * X_WST;
+        const uint8_t* wst = smem + ((it + 1) % 3) * X_WST;
         const uint8_t* ast = smem + X_ARING + (it & 1) * X_AST;
         const uint32_t anxt = ring + X_ARING + ((it + 1) & 1) * X_AST;
-        const uint32_t wnxt = ring + ((it + 2) % 3) * X_WST;
-        // token block i of wave (wm, wn) is tile block 2i + wm
+        const uint32_t wnxt = ring + (it % 3) * X_WST;   // step it+2: stage (it+3) % 3, step it-1's
         const uint8_t* la = ast + (32 * wm + lr) * X_ROWB;
         const uint8_t* lw = wst + (wn * 64 + lr) * X_ROWB;
         const uint8_t* lsa = ast + X_A + (32 * wm + lr) * 8;
@@ -986,7 +1089,6 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
         for (int i = 0; i < NB; ++i) sa[i] = scale_word(lsa + i * 64 * 8, h);
 #pragma unroll
         for (int j = 0; j < 2; ++j) sb[j] = scale_word(lsw + j * 32 * 8, h);
-        // operands of substep ks+1 are read before the MFMAs of substep ks
         uint4 af[2][3], bf[2][2];
         auto load = [&](int ks, int r) {
             const int koff = ((2 * ks + h) ^ key) << 4;
@@ -1007,7 +1109,6 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
             if (NB > 0) {
                 if (ks + 1 < 4) load(ks + 1, (ks + 1) & 1);
                 const int r = ks & 1;
-                // D[weight row][token]: the weight tile is the MFMA A operand
 #pragma unroll
                 for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -1024,21 +1125,39 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
     for (int i = 0; i < 3; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) mx::pin(acc[i][j]);
+    sync();
+    issue(0);
+    xp_epilogue<MODE, NB>(acc, g, smem, t, wave, lane, issue);
+}
+
+// Epilogue of one wave's token blocks (NB of them) of tile t; issues parts 1
+// and 2 of the next tile's first copies between its blocks.
+template <int MODE, int NB, class Issue>
+__device__ __forceinline__ void xp_epilogue(mx::v16f (&acc)[3][2], const GArgs& g, uint8_t* smem, const XpTile& t,
+                                            int wave, int lane, Issue&& issue) {
+    const int wm = wave >> 2, wn = wave & 3;
+    const int lr = lane & 31, h = lane >> 5;
+    if (NB == 0) {
+        issue(1);
+        issue(2);
+        return;
+    }
     if (MODE == MODE_DOWN) {
-        // bf16(bf16(y) * score) goes through LDS, so that each store
-        // instruction writes 8 whole 128-byte row segments instead of 16
-        // bytes of 32 rows: wave w transposes its 96 x 64 block in its own
-        // X_TROW-pitched buffer, over the rings (free once every wave is past
-        // its last MFMA)
-        if (trow < X_BM) {
-            reinterpret_cast<int*>(smem + X_PP)[trow] = rp;
-            reinterpret_cast<float*>(smem + X_PP + 4 * X_BM)[trow] = rs;
-        }
-        __syncthreads();
-        if (NB == 0) return;
-        uint8_t* tb = smem + wave * 96 * X_TROW;
+        // bf16(bf16(y) * score) through LDS, one 32-token block at a time in
+        // the wave's own 32-row buffer of weight stage 0, so that a store
+        // writes 8 whole 128-byte row segments; rows 136 bytes apart make
+        // the 8-byte writes of 32 lanes (one row each) hit distinct banks
+        uint8_t* tb = smem + wave * 32 * XP_TROW;
         const int* lp = reinterpret_cast<const int*>(smem + X_PP);
         const float* ls = reinterpret_cast<const float*>(smem + X_PP + 4 * X_BM);
+        // lane: buffer row 8*st + lane/8 (tile row 64*i + 32*wm + 8*st +
+        // lane/8), 16 bytes at column chunk lane%8
+        const int ch = lane & 7;
+        const int col = t.n0 + wn * 64 + 8 * ch;
+        const int lim = col < g.Nw ? t.mrows - 32 * wm - (lane >> 3) : 0;   // tile rows < lim + 32*wm + lane/8 are routed
+        const uint8_t* tr = tb + (lane >> 3) * XP_TROW + 16 * ch;
+        const int* pr = lp + 32 * wm + (lane >> 3);
+        uint16_t* yc = g.yd + col;
 #pragma unroll
         for (int i = 0; i < NB; ++i) {
             const float sc = ls[64 * i + 32 * wm + lr];
@@ -1053,77 +1172,146 @@ __device__ __forceinline__ void x8_tile(const XCopies& c, const GArgs& g, uint8_
                         b[r] = mx::f32x2_to_bf16x2(__uint_as_float(y2 << 16) * sc, __uint_as_float(y2 & 0xFFFF0000u) * sc);
                     }
                     // element q of block j: column 32j + 8(q/4) + 4h + q%4
-                    *reinterpret_cast<uint2*>(tb + (32 * i + lr) * X_TROW + (32 * j + 8 * q4 + 4 * h) * 2) =
-                        make_uint2(b[0], b[1]);
+                    *reinterpret_cast<uint2*>(tb + lr * XP_TROW + (32 * j + 8 * q4 + 4 * h) * 2) = make_uint2(b[0], b[1]);
                 }
-        }
-        // lane: buffer row 8*st + lane/8 (tile row 64*(st/4) + 32*wm +
-        // 8*(st%4) + lane/8), 16 bytes at column chunk lane%8; per-lane
-        // bases, so each step's LDS reads take immediate offsets
-        const int ch = lane & 7;
-        const int col = n0 + wn * 64 + 8 * ch;
-        const int lim = col < g.Nw ? mrows - 32 * wm - (lane >> 3) : 0;   // tile rows r < lim + 32*wm + lane/8 are routed
-        const uint8_t* tr = tb + (lane >> 3) * X_TROW + 16 * ch;
-        const int* pr = lp + 32 * wm + (lane >> 3);
-        uint16_t* yc = g.yd + col;
 #pragma unroll
-        for (int st = 0; st < 4 * NB; ++st) {
-            const int toff = 64 * (st >> 2) + 8 * (st & 3);   // tile row - (32*wm + lane/8)
-            if (toff < lim) {
-                const uint4 v = *reinterpret_cast<const uint4*>(tr + 8 * st * X_TROW);
-                *reinterpret_cast<uint4*>(yc + (int64_t)pr[toff] * g.Nw) = v;
+            for (int st = 0; st < 4; ++st) {
+                const int toff = 64 * i + 8 * st;   // tile row - (32*wm + lane/8)
+                if (toff < lim) {
+                    const uint4 v = *reinterpret_cast<const uint4*>(tr + 8 * st * XP_TROW);
+                    *reinterpret_cast<uint4*>(yc + (int64_t)pr[toff] * g.Nw) = v;
+                }
             }
+            if (i < 2) issue(i + 1);
         }
+        if (NB == 1) issue(2);
         return;
     }
-    if (NB == 0) return;
-    // gate/up: the wave's token blocks (tile rows 64*i + 32*wm + lane%32)
-    // through the 128 x 128 epilogue, in pairs, the last one alone when NB
-    // is odd (the epilogue is VALU-bound: no work on empty blocks)
     const int pp[2] = {0, 0};
     const float ss[2] = {0.0f, 0.0f};
     if (NB >= 2) {
         mx::v16f sub[2][2] = {{acc[0][0], acc[0][1]}, {acc[1][0], acc[1][1]}};
-        tile_epilogue<MODE, 2>(sub, g, n0, off, mt, mrows, 32 * wm, wn, lr, h, pp, ss, 64);
+        tile_epilogue<MODE, 2>(sub, g, t.n0, t.off, t.mt, t.mrows, 32 * wm, wn, lr, h, pp, ss, 64);
+        issue(1);
     }
     if (NB == 1 || NB == 3) {
         mx::v16f sub[2][2] = {{acc[NB - 1][0], acc[NB - 1][1]}, {acc[NB - 1][0], acc[NB - 1][1]}};
-        tile_epilogue<MODE, 1>(sub, g, n0, off, mt, mrows, 64 * (NB - 1) + 32 * wm, wn, lr, h, pp, ss, 64);
+        tile_epilogue<MODE, 1>(sub, g, t.n0, t.off, t.mt, t.mrows, 64 * (NB - 1) + 32 * wm, wn, lr, h, pp, ss, 64);
+        if (NB == 1) issue(1);
     }
+    issue(2);
 }
 
 template <int MODE, class W>
-__global__ __launch_bounds__(X_THREADS, 1) void grouped_gemm_x8_kernel(GArgs g, W w, int ntiles, int n_exp) {
+__global__ __launch_bounds__(X_THREADS, 1) void grouped_gemm_xp_kernel(GArgs g, W w, int ntiles, int n_exp,
+                                                                       int* __restrict__ qctr) {
     extern __shared__ __align__(16) uint8_t smem[];
-    const int bid = blockIdx.x;
-    const int e = (bid & 7) + 8 * ((bid >> 3) / ntiles);
-    const int nt = (bid >> 3) % ntiles;
-    if (e >= n_exp) return;
-    const int cnt = g.counts[e];
-    if (cnt == 0) return;
-    const int off = g.offs[e];
-    const int n0 = nt * (MODE == MODE_GATEUP ? X_BN / 2 : X_BN);
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int grp = blockIdx.x & 7;
+    const int kw = blockIdx.x >> 3;              // workgroup of the group
+    const int per = gridDim.x >> 3;              // workgroups per group
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t ring = __builtin_amdgcn_readfirstlane(mx::lds_addr(smem));
-    for (int mt = 0; mt < cnt; mt += X_BM) {
-        const int mrows = min(X_BM, cnt - mt);
-        XCopies c;
-        x8_plan<MODE>(c, g, w, e, n0, off, mt, mrows, wave, lane);
+    int* ucum = reinterpret_cast<int*>(smem + XP_UCUM);
+    int* ecnt = reinterpret_cast<int*>(smem + XP_ECNT);
+    int* eoff = reinterpret_cast<int*>(smem + XP_EOFF);
+    int* slot = reinterpret_cast<int*>(smem + XP_SLOT);
+    const int nj = n_exp > grp ? (n_exp - grp + 7) / 8 : 0;
+    if (nj == 0) return;
+    for (int j = tid; j < nj; j += X_THREADS) {
+        ecnt[j] = g.counts[grp + 8 * j];
+        eoff[j] = g.offs[grp + 8 * j];
+    }
+    __syncthreads();
+    if (wave == 0) {   // units below expert j: exclusive prefix, two experts per lane
+        const int j0 = 2 * lane;
+        const int u0 = j0 < nj ? (ecnt[j0] + X_BM - 1) / X_BM * ntiles : 0;
+        const int u1 = j0 + 1 < nj ? (ecnt[j0 + 1] + X_BM - 1) / X_BM * ntiles : 0;
+        int v = u0 + u1;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const int o = __shfl_up(v, d);
+            if (lane >= d) v += o;
+        }
+        const int ex = v - u0 - u1;
+        ucum[j0] = ex;
+        ucum[j0 + 1] = ex + u0;
+        if (lane == 63) ucum[128] = v;
+    }
+    __syncthreads();
+    const int nunits = __builtin_amdgcn_readfirstlane(ucum[nj]);
+    // units kw and kw + per are this workgroup's first two; the queue hands
+    // out the rest, from 2 * per on
+    if (kw >= nunits) return;
+    const int nsteps = g.Kp / 256;
+    XpTile t = xp_tile_of<MODE>(smem, grp, nj, ntiles, kw, lane);
+    XCopies c;
+    {
+        int rw[4];
+        x8_rows<MODE>(rw, g, t.off, t.mt, t.mrows, wave, lane);
+        x8_plan_rows<MODE>(c, g, w, t.e, t.n0, t.mrows, rw, wave, lane);
+    }
+    xp_prologue(c, ring, nsteps, wave);
+    int un1 = kw + per;                          // the next tile's unit (uniform)
+    const int trow = wave * 64 + lane;
+    for (;;) {
+        // Issued now, used only after the K loop: the next tile's source
+        // rows, the queue's unit for the tile after it, and the down tile's
+        // pair indices and weights.  No loaded value is merged with a
+        // default (a merge is a use, and the compiler's wait for it would
+        // also wait for the copies in flight, which it does not count): the
+        // atomic's result is read only by the lane that issued it, every
+        // load is unconditional (clamped rows).  atomicInc, because the
+        // compiler's wave aggregation of atomic adds uses the result at once.
+        const bool more = un1 < nunits;
+        XpTile tn = t;
+        int rwn[4];
+        if (more) {
+            tn = xp_tile_of<MODE>(smem, grp, nj, ntiles, un1, lane);
+            x8_rows<MODE>(rwn, g, tn.off, tn.mt, tn.mrows, wave, lane);
+        }
+        int uq;
+        if (tid == 0) uq = (int)atomicInc(reinterpret_cast<unsigned*>(qctr + grp), 0xFFFFFFFFu);
+        int rp = 0;
+        float rs = 0.0f;
+        if (MODE == MODE_DOWN) {
+            const int r = t.off + t.mt + min(trow, t.mrows - 1);
+            rp = g.pairs[r];
+            rs = g.sscore[r];
+        }
+        XCopies cn = c;
+        auto sync = [&]() {
+            if (MODE == MODE_DOWN && trow < t.mrows) {
+                reinterpret_cast<int*>(smem + X_PP)[trow] = rp;
+                reinterpret_cast<float*>(smem + X_PP + 4 * X_BM)[trow] = rs;
+            }
+            if (tid == 0) *slot = uq;
+            // every wave is past its last operand read of this tile (the
+            // next tile's copies may overwrite the stages), the pair rows
+            // and the queue's unit are in LDS
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        };
+        auto issue = [&](int part) {
+            if (more) {
+                if (part == 0) x8_plan_rows<MODE>(cn, g, w, tn.e, tn.n0, tn.mrows, rwn, wave, lane);
+                xp_prologue_part(cn, ring, nsteps, wave, part);
+            }
+        };
         // the wave's token blocks 2i + wm (i < nb) holding routed rows
-        const int nb = min(((mrows + 31) / 32 - (wave >> 2) + 1) >> 1, 3);
+        const int nb = min(((t.mrows + 31) / 32 - (wave >> 2) + 1) >> 1, 3);
         switch (nb) {
-            case 3: x8_tile<MODE, 3>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
-            case 2: x8_tile<MODE, 2>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
-            case 1: x8_tile<MODE, 1>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
-            default: x8_tile<MODE, 0>(c, g, smem, ring, n0, off, mt, mrows, wave, lane); break;
+            case 3: xp_tile<MODE, 3>(c, g, smem, ring, t, wave, lane, sync, issue); break;
+            case 2: xp_tile<MODE, 2>(c, g, smem, ring, t, wave, lane, sync, issue); break;
+            case 1: xp_tile<MODE, 1>(c, g, smem, ring, t, wave, lane, sync, issue); break;
+            default: xp_tile<MODE, 0>(c, g, smem, ring, t, wave, lane, sync, issue); break;
         }
-        // every wave is done with the rings before the next token tile
-        // refills them (and its vmcnt counts only the new copies)
-        if (mt + X_BM < cnt) {
-            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            __syncthreads();
-        }
+        if (!more) break;
+        un1 = 2 * per + __builtin_amdgcn_readfirstlane(*slot);
+        t = tn;
+        c = cn;
     }
 }
 
@@ -1159,10 +1347,24 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(const uint16_t* __
 
 // ------------------------------------------------------------------ host
 struct WsLayout {
-    size_t counts, offs, pairs, sscore, hist, xq, xs, hq, hs, yd, total;
+    size_t counts, offs, pairs, sscore, hist, qctr, xq, xs, hq, hs, yd, total;
 };
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// CUs per XCD of the current device (its CU count / 8), cached per device:
+// the persistent grouped GEMMs launch one workgroup per CU.
+int cus_per_xcd() {
+    static int cache[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 32;
+    if (cache[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 8) n = 256;
+        cache[dev] = n / 8;
+    }
+    return cache[dev];
+}
 
 WsLayout ws_layout(int T, int topk, int n_exp, int H, int Mi) {
     const size_t P = (size_t)T * topk;
@@ -1173,6 +1375,7 @@ WsLayout ws_layout(int T, int topk, int n_exp, int H, int Mi) {
     L.pairs = o;  o = align256(o + sizeof(int) * P);
     L.sscore = o; o = align256(o + sizeof(float) * P);
     L.hist = o;   o = align256(o + sizeof(int) * ((P + kRtChunk - 1) / kRtChunk) * n_exp);
+    L.qctr = o;   o = align256(o + sizeof(int) * 16);
     L.xq = o;     o = align256(o + (size_t)T * (H / 2));
     L.xs = o;     o = align256(o + (size_t)T * (H / 32));
     L.hq = o;     o = align256(o + P * (Mi / 2));
@@ -1204,9 +1407,9 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
                               reinterpret_cast<const void*>(grouped_gemm_kernel<MODE_DOWN, W>),
                               reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_GATEUP, W>),
                               reinterpret_cast<const void*>(grouped_gemm_dma_kernel<MODE_DOWN, W>),
-                              reinterpret_cast<const void*>(grouped_gemm_x8_kernel<MODE_GATEUP, W>),
-                              reinterpret_cast<const void*>(grouped_gemm_x8_kernel<MODE_DOWN, W>)};
-        const int bytes = m < 2 ? 2 * BUF_BYTES : m < 4 ? D_NST * D_STAGE : X_LDS;
+                              reinterpret_cast<const void*>(grouped_gemm_xp_kernel<MODE_GATEUP, W>),
+                              reinterpret_cast<const void*>(grouped_gemm_xp_kernel<MODE_DOWN, W>)};
+        const int bytes = m < 2 ? 2 * BUF_BYTES : m < 4 ? D_NST * D_STAGE : XP_LDS;
         hipError_t e = hipFuncSetAttribute(fns[m], hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         MXH_REQUIRE(e == hipSuccess, "moe_prefill: cannot reserve %d B of LDS: %s", bytes, hipGetErrorString(e));
         attr_set[tw][m] = true;
@@ -1220,7 +1423,8 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     float* sscore = reinterpret_cast<float*>(ws + L.sscore);
     int* hist = reinterpret_cast<int*>(ws + L.hist);
     const int nchunk = (P + kRtChunk - 1) / kRtChunk;
-    hipLaunchKernelGGL(route_count_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist);
+    int* qctr = reinterpret_cast<int*>(ws + L.qctr);
+    hipLaunchKernelGGL(route_count_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist, qctr);
     hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist, counts,
                        offs, pairs, scores, sscore);
     int rc = mxh::launch_status("moe_prefill route");
@@ -1246,11 +1450,11 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     // the copy kernels address operands with 32-bit byte offsets
     const bool fit_gu = (int64_t)T * (H / 2) < (1ll << 32) && (int64_t)Mi * (H / 2) < (1ll << 32);
     const bool fit_dn = (int64_t)P * (Mi / 2) < (1ll << 32) && (int64_t)H * (Mi / 2) < (1ll << 32);
-    const int xgroups = (n_exp + 7) / 8;
+    const int xp_grid = 8 * cus_per_xcd();   // one persistent workgroup per CU
     if (H % 256 == 0 && fit_gu) {
         const int ntiles = (Mi + X_BN / 2 - 1) / (X_BN / 2);
-        hipLaunchKernelGGL((grouped_gemm_x8_kernel<MODE_GATEUP, W>), dim3(8 * xgroups * ntiles), dim3(X_THREADS),
-                           X_LDS, st, g, w, ntiles, n_exp);
+        hipLaunchKernelGGL((grouped_gemm_xp_kernel<MODE_GATEUP, W>), dim3(xp_grid), dim3(X_THREADS), XP_LDS, st, g,
+                           w, ntiles, n_exp, qctr);
     } else if (H % DK == 0 && fit_gu)
         hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_GATEUP, W>), dim3((Mi + 63) / 64, n_exp), dim3(256),
                            D_NST * D_STAGE, st, g, w);
@@ -1267,8 +1471,8 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     g.a_rows = P;
     if (Mi % 256 == 0 && fit_dn) {
         const int ntiles = (H + X_BN - 1) / X_BN;
-        hipLaunchKernelGGL((grouped_gemm_x8_kernel<MODE_DOWN, W>), dim3(8 * xgroups * ntiles), dim3(X_THREADS),
-                           X_LDS, st, g, w, ntiles, n_exp);
+        hipLaunchKernelGGL((grouped_gemm_xp_kernel<MODE_DOWN, W>), dim3(xp_grid), dim3(X_THREADS), XP_LDS, st, g,
+                           w, ntiles, n_exp, qctr + 8);
     } else if (Mi % DK == 0 && fit_dn)
         hipLaunchKernelGGL((grouped_gemm_dma_kernel<MODE_DOWN, W>), dim3((H + BN - 1) / BN, n_exp), dim3(256),
                            D_NST * D_STAGE, st, g, w);
