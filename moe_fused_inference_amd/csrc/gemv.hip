@@ -627,9 +627,19 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     if (c >= N) return;
     const float* yb = yd + (int64_t)m * E * ystride;
     const float* wb = w + (int64_t)m * E;
-    float acc = 0.0f;
     const int ee = E < 8 ? E : 8;  // src/ext/mxfp4_decode.cu:296 caps at 8 slots
-    for (int e = 0; e < ee; ++e) acc = fmaf(wb[e], yb[(int64_t)e * ystride + c], acc);
+    // every load issued before the first use (a use inside the loop made each
+    // slot wait for the previous one's load), then the fmas in slot order
+    float yv[8], wv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        yv[e] = e < ee ? yb[(int64_t)e * ystride + c] : 0.0f;
+        wv[e] = e < ee ? wb[e] : 0.0f;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+        if (e < ee) acc = fmaf(wv[e], yv[e], acc);
     out[(int64_t)m * N + c] = acc;
 }
 
