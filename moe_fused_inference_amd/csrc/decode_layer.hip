@@ -80,18 +80,20 @@ constexpr int kCfgOff = 0;            // int32 config word written by reset
 constexpr int kErrOff = 256;          // int32 error flag
 constexpr int kMemoAOff = 1024;       // int32 launch count of gate/up workgroup (s, jb): [8][32]
 constexpr int kMemoBOff = 2048;       // int32 launch count of down workgroup cb: [128]
-constexpr int kMemoROff = 2560;       // int32 launch count of router workgroup r (fused router): [16]
+constexpr int kMemoROff = 2560;       // int32 launch count of router workgroup r (fused router): [128]
 constexpr int kMemoQOff = 3072;       // int32 launch count of q|k|v workgroup q (fused router tail): [128]
-constexpr int kLogOff = 4096;         // fused router: (logit, tag) 64-bit words, n_experts <= 256
 constexpr int kMemoMOff = 6144;       // int32 launch count of attention-merge workgroup h (front): [64]
 constexpr int kMemoOOff = 6400;       // int32 launch count of o_proj workgroup o (front): [128]
 constexpr int kMemoTOff = 8192;       // int32 launch count of attention chunk workgroup t (next layer): [512]
-constexpr int kHOff = 16384;          // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
+constexpr int kLogOff = 16384;        // fused router: 8 copies (one per XCD) of (logit, tag) 64-bit words,
+                                      // kLogCopy words apart, n_experts <= 256
+constexpr int kLogCopy = 256;
+constexpr int kHOff = 32768;          // two h buffers of (E, Mi/32, kRecWords) uint32, bufwords apart,
                                       // then (out[c], tag) 64-bit words, c < H, for the q|k|v tail,
                                       // then the front's words: kAttnWords per head of the attention
                                       // output, and (o_proj[c], tag), c < H; then (q|k|v[r], tag)
                                       // for the next layer's attention, r < 8192
-constexpr int kMaxRouterWg = 16;      // fused router: 16 logits per workgroup
+constexpr int kMaxRouterWg = 128;     // fused router: 16 logits per workgroup, all logits once per XCD
 constexpr int kMaxQkvWg = 128;        // q|k|v tail: 64 rows per workgroup, up to 8192 rows
 constexpr int kMaxH = 2048;
 constexpr int kMaxHq = 32;            // front: query heads (o_proj K = 4096)
@@ -341,9 +343,12 @@ __device__ __forceinline__ void fused_norm_row(const LayerArgs& a, float* nred, 
 
 // The router logits of this launch from the workspace: element i*64 + lane
 // into lv[i], waiting (bounded) until every word carries this launch's tag.
+// The copy read is the one the router workgroups of this workgroup's XCD
+// write (blockIdx.x % 8: workgroups are dealt to the 8 XCDs round-robin), so
+// the hand-off stays in one L2; any copy holds every logit.
 template <int NPL>
 __device__ __forceinline__ bool poll_logits(const LayerArgs& a, uint32_t tag, float (&lv)[NPL]) {
-    const uint64_t* words = reinterpret_cast<const uint64_t*>(a.ws + kLogOff);
+    const uint64_t* words = reinterpret_cast<const uint64_t*>(a.ws + kLogOff) + (blockIdx.x & 7) * kLogCopy;
     const int lane = threadIdx.x & 63;
     int spins = 0;
     // the last logit first, one request per wave and round
@@ -372,21 +377,25 @@ __device__ __forceinline__ bool poll_logits(const LayerArgs& a, uint32_t tag, fl
     }
 }
 
-// Router workgroup r (fused router): logits [16r, 16r + 16) of the normed
-// row -- its MXFP4 (the reference quantizes the bf16 row, prequant) times
-// the router's MXFP4 rows on v_mfma_scale_f32_16x16x128_f8f6f4 (row 0 of A is
-// the row, rows 1..15 zero), K split over the four waves, partial sums
-// added in wave order -- published as (value, tag) words for every other
-// workgroup of the launch.  Workgroup 0 also writes x_out / y_out.
+// Router workgroup ri (fused router): logits [16c, 16c + 16), c = ri / 8, of
+// the normed row -- its MXFP4 (the reference quantizes the bf16 row,
+// prequant) times the router's MXFP4 rows on v_mfma_scale_f32_16x16x128_f8f6f4
+// (row 0 of A is the row, rows 1..15 zero), K split over the four waves,
+// partial sums added in wave order -- published as (value, tag) words into
+// the logit copy of its XCD (blockIdx.x % 8), read by that XCD's gate/up and
+// down workgroups: every XCD computes all logits (8 x 16 router rows of
+// 1 KB each), so the hand-off to the routing stays in one L2.  Router
+// workgroup 0 also writes x_out / y_out.
 __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* nred, int ri) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
+    const int chunk = ri >> 3;
     int* memo = reinterpret_cast<int*>(a.ws + kMemoROff) + ri;
     const int launch = *memo;
     const int cfg = *reinterpret_cast<const int*>(a.ws + kCfgOff);
-    // weights first: row 16ri + r, blocks 16*wave + 4g .. +3 (64 contiguous bytes) and their scales
+    // weights first: row 16c + r, blocks 16*wave + 4g .. +3 (64 contiguous bytes) and their scales
     const int blk0 = 16 * wave + 4 * g;
-    const int row = min(16 * ri + r, a.n_experts - 1);
+    const int row = min(16 * chunk + r, a.n_experts - 1);
     const uint8_t* wr = a.rwp + (int64_t)row * 1024 + blk0 * 16;
     uint4 wq[4];
 #pragma unroll
@@ -431,19 +440,17 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
     __syncthreads();
     if (tid < 16) {
         const float lg = (sm.r.red[0][tid] + sm.r.red[1][tid]) + (sm.r.red[2][tid] + sm.r.red[3][tid]);
-        const int idx = 16 * ri + tid;
+        const int idx = 16 * chunk + tid;
         if (idx < a.n_experts) {
-            uint64_t* words = reinterpret_cast<uint64_t*>(a.ws + kLogOff);
+            uint64_t* words = reinterpret_cast<uint64_t*>(a.ws + kLogOff) + (blockIdx.x & 7) * kLogCopy;
             __hip_atomic_store(words + idx, (uint64_t)__float_as_uint(lg) | ((uint64_t)(uint32_t)(launch + 1) << 32),
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if (a.logits_out) a.logits_out[idx] = lg;
+            if (a.logits_out && (ri & 7) == 0) a.logits_out[idx] = lg;
         }
     }
     if (tid == 0) {
-        // launch counts of the router slots this launch has no workgroup for
-        // move on with it (workgroup 0), so every count stays in step
-        if (ri == 0)
-            for (int k = a.nr; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
+        // (the launch counts of the router slots this launch has no
+        // workgroup for move on with gate/up workgroup 0)
         *memo = launch + 1;
         if (cfg != a.cfg) set_error(a);
     }
@@ -1046,17 +1053,16 @@ __global__ __launch_bounds__(256) void decode_layer_kernel(LayerArgs a) {
             if (lane == 0) {
                 *memo = launch + 1;
                 if (!cfg_ok) set_error(a);
-                // launches without router workgroups move the router launch
-                // counts on (workgroup 0), so a later fused launch agrees
-                if (ROUTE != ROUTE_FUSED && bid == 0)
-                    for (int k = 0; k < kMaxRouterWg; ++k) reinterpret_cast<int*>(a.ws + kMemoROff)[k] += 1;
             }
         }
-        // likewise the slots of the q|k|v tail, the front and the next
-        // layer's attention this launch has no workgroup for (workgroup 0,
-        // all threads: one memory round trip)
+        // the launch counts of the router slots, the q|k|v tail, the front
+        // and the next layer's attention this launch has no workgroup for
+        // move on with it, so a later fused launch agrees (workgroup 0, all
+        // threads: one memory round trip)
         if (bid == 0) {
             const int t = threadIdx.x;
+            const int nr = ROUTE == ROUTE_FUSED ? a.nr : 0;
+            if (t < kMaxRouterWg && t >= nr) reinterpret_cast<int*>(a.ws + kMemoROff)[t] += 1;
             const int nq = ROUTE == ROUTE_FUSED ? a.nq : 0;
             const int nm = ROUTE == ROUTE_FUSED ? a.nm : 0;
             const int no = ROUTE == ROUTE_FUSED ? a.no : 0;
@@ -1421,9 +1427,9 @@ int fused_router_args(LayerArgs& a, const void* x, const float* resid, const voi
     if (rc != MXFP4_OK) return rc;
     MXH_REQUIRE(resid && norm_w && router_wp && router_ws, "moe_decode_layer_fused_router: null pointer");
     MXH_REQUIRE(H == 2048, "moe_decode_layer_fused_router: H=%d (the fused norm is built for 2048)", H);
-    MXH_REQUIRE(n_experts % 16 == 0 && n_experts <= 16 * kMaxRouterWg,
+    MXH_REQUIRE(n_experts % 16 == 0 && n_experts <= 2 * kMaxRouterWg,
                 "moe_decode_layer_fused_router: n_experts=%d must be a multiple of 16 up to %d", n_experts,
-                16 * kMaxRouterWg);
+                2 * kMaxRouterWg);
     MXH_REQUIRE((ids_out != nullptr) == (w_out != nullptr),
                 "moe_decode_layer_fused_router: give ids_out and w_out both or neither");
     MXH_REQUIRE(((uintptr_t)resid & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && ((uintptr_t)router_wp & 15) == 0 &&
@@ -1442,7 +1448,7 @@ int fused_router_args(LayerArgs& a, const void* x, const float* resid, const voi
     a.logits_out = logits_out;
     a.ids_out = ids_out;
     a.w_out = w_out;
-    a.nr = n_experts / 16;
+    a.nr = 8 * (n_experts / 16);   // every XCD's copy of the logits
     return MXFP4_OK;
 }
 }  // namespace
