@@ -63,6 +63,7 @@
 // flag, a wave stops waiting, the results are garbage and the flag stays set
 // until the workspace is reset.
 #include "decode_common.h"
+#include "lds_dma.h"
 #include "mx_host.h"
 
 namespace {
@@ -140,6 +141,8 @@ union Smem {
     } s;
     uint8_t one_per_cu[84 * 1024];              // more than half of a CU's LDS: one workgroup per CU
 };
+constexpr int kSinkOff = 80 * 1024;             // strict prefetch: LDS sink of 256 bytes, past Smem::s
+static_assert(sizeof(decltype(Smem::s)) <= kSinkOff, "the prefetch sink lies past the kernel's LDS data");
 
 // Error flag bits: a bounded wait expired, the workspace belongs to another shape.
 constexpr int kErrWait = 1, kErrCfg = 2;
@@ -444,6 +447,25 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
             }
         }
     };
+    // STRICT: the gate/up rows load_gu would read, touched with 4-byte LDS-DMA
+    // loads into a sink (no registers held, nothing the compiler waits on), so
+    // the lines come into this XCD's L2 for the workgroup of the other set
+    // that computes the layer
+    auto prefetch_gu = [&](const LayerRoute& rt) {
+        const int e = rt.e;
+        const uint32_t sink = __builtin_amdgcn_readfirstlane(mx::lds_addr(smu.one_per_cu + kSinkOff));
+        const mx::v4u rw[2] = {mx::buf_rsrc(rt.p[0] + (int64_t)e * a.wp_stride_gu, (int64_t)Mi * (H >> 1)),
+                               mx::buf_rsrc(rt.p[1] + (int64_t)e * a.wp_stride_gu, (int64_t)Mi * (H >> 1))};
+        const mx::v4u rs[2] = {mx::buf_rsrc(rt.p[3] + (int64_t)e * a.ws_stride_gu, (int64_t)Mi * hb),
+                               mx::buf_rsrc(rt.p[4] + (int64_t)e * a.ws_stride_gu, (int64_t)Mi * hb)};
+#pragma unroll
+        for (int m = 0; m < NT; ++m) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (i < sa) mx::dma4(woff[m] + 64 * i, tup[m] ? rw[1] : rw[0], 0, sink);
+            mx::dma4(soff[m], tup[m] ? rs[1] : rs[0], 0, sink);
+        }
+    };
     // ---- down weights: column tiles cw and cw + 4 (16 columns each) of the
     // workgroup's columns.  Step i takes blocks 4i .. 4i + 3 of the Mi row,
     // lane group g block 4i + g (64 contiguous bytes per row and load);
@@ -505,6 +527,32 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stack_kernel(StackArgs a) 
     for (int l = par; l < L; l += 2) {
         const uint32_t tag = c0 + (uint32_t)l + 1u;          // this layer's tag (never 0)
         const int b = (int)((c0 + (uint32_t)l) % kNBuf);
+        if (STRICT && l >= 1) {
+            // the other set computes layer l-1 now: once x_{l-1} is complete
+            // (that layer's routing known) this workgroup pulls its partner's
+            // gate/up rows of layer l-1 (the workgroup of the same index in
+            // the other set, on this XCD) into their L2, so the partner's own
+            // loads of them, issued after its down rows, find them there
+            const int m = l - 1;
+            if (m >= 1) {
+                const int bm = (int)((c0 + (uint32_t)m) % kNBuf);
+                const __amdgpu_buffer_rsrc_t rs = region(x_base((bm + kNBuf - 1) % kNBuf), H);
+                const int nq = H >> 2;
+                const int q0 = cw * nq;
+                uint32_t off[4];
+                bool ok[4];
+#pragma unroll
+                for (int i = 0; i < 2; ++i)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        ok[2 * i + j] = 256 * i + 4 * lane < nq;
+                        off[2 * i + j] = (uint32_t)(xpos(q0 + min(256 * i + 4 * lane, nq - 4) + 2 * j) * 8);
+                    }
+                v2u xw[8];
+                live = poll_pairs<4, 16>(a, rs, off, ok, tag16(c0 + (uint32_t)m), xw, live);
+            }
+            prefetch_gu(route(m));
+        }
         // combine weights of every slot (read now, used after the y poll)
         float wt[kMaxE];
         if (l < kLdsLayers) {   // two 16-byte reads (the LDS copy holds 0 for t >= E)
