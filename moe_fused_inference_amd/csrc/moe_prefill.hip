@@ -41,6 +41,7 @@
 #include "lds_dma.h"
 #include "mx_device.h"
 #include "mx_host.h"
+#include "quant_rows.h"
 
 namespace mxh {
 int quantize_rows_impl(const void* x, int src_dtype, int round_to_f16, int64_t ldx, int M, int K, int Kp,
@@ -213,10 +214,30 @@ __device__ __forceinline__ uint64_t same_id_lanes(int id, bool valid, int bits) 
 
 __device__ __forceinline__ int id_bits(int n_exp) { return 32 - __clz(max(n_exp - 1, 1)); }
 
+// The token rows' quantization (x -> fp16 -> MXFP4) rides in the route
+// count launch as the workgroups past its chunks: it does not depend on the
+// routing, and the count's few latency-bound workgroups leave the CUs free.
+struct XQuant {
+    const void* x;      // (T, H) bf16
+    int T, H;
+    int lt, gx;         // quantize_rows_kernel's layout: 2^lt threads per row, gx row groups
+    uint8_t* q;         // (T, H/2)
+    uint8_t* s;         // (T, H/32)
+};
+
 __global__ __launch_bounds__(64 * kRtWaves) void route_count_kernel(const int64_t* __restrict__ topi, int P, int n_exp,
-                                                                   int* __restrict__ hist, int* __restrict__ qctr) {
+                                                                   int* __restrict__ hist, int* __restrict__ qctr,
+                                                                   int nchunk, XQuant xq) {
     __shared__ int h[kMaxExperts];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if ((int)blockIdx.x >= nchunk) {
+        const int local = (int)blockIdx.x - nchunk;
+        const int bx = local % xq.gx, by = local / xq.gx;
+        const int64_t row = (int64_t)bx * (256 >> xq.lt) + (tid >> xq.lt);
+        const int u = by * (1 << xq.lt) + (tid & ((1 << xq.lt) - 1));
+        mxq::quantize_unit<MXFP4_DT_BF16, 1>(xq.x, xq.H, xq.T, xq.H, xq.H, true, row, u, xq.q, xq.s);
+        return;
+    }
     if (qctr && blockIdx.x == 0 && tid < 16) qctr[tid] = 0;   // the grouped GEMMs' tile queues (8 each)
     for (int e = tid; e < n_exp; e += 64 * kRtWaves) h[e] = 0;
     const int bits = id_bits(n_exp);
@@ -1424,12 +1445,18 @@ int run_prefill(const void* x, const int64_t* topi, const uint16_t* scores, W w,
     int* hist = reinterpret_cast<int*>(ws + L.hist);
     const int nchunk = (P + kRtChunk - 1) / kRtChunk;
     int* qctr = reinterpret_cast<int*>(ws + L.qctr);
-    hipLaunchKernelGGL(route_count_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist, qctr);
+    // x -> fp16 -> MXFP4 once per token (the reference quantizes each gathered
+    // copy; the bytes are identical), in the same launch: quantize_rows_kernel's
+    // layout (x is 16-byte aligned and H a multiple of 32, so the vector path)
+    XQuant xqa{x, T, H, 2, 0, ws + L.xq, ws + L.xs};
+    while ((1 << xqa.lt) < H / 8 && xqa.lt < 8) ++xqa.lt;
+    xqa.gx = (T + (256 >> xqa.lt) - 1) / (256 >> xqa.lt);
+    const int xq_gy = (H / 8 + (1 << xqa.lt) - 1) >> xqa.lt;
+    hipLaunchKernelGGL(route_count_kernel, dim3(nchunk + xqa.gx * xq_gy), dim3(64 * kRtWaves), 0, st, topi, P, n_exp,
+                       hist, qctr, nchunk, xqa);
     hipLaunchKernelGGL(route_scatter_kernel, dim3(nchunk), dim3(64 * kRtWaves), 0, st, topi, P, n_exp, hist, counts,
                        offs, pairs, scores, sscore);
     int rc = mxh::launch_status("moe_prefill route");
-    if (rc != MXFP4_OK) return rc;
-    rc = mxh::quantize_rows_impl(x, MXFP4_DT_BF16, 1, H, T, H, H, ws + L.xq, ws + L.xs, st);
     if (rc != MXFP4_OK) return rc;
 
     GArgs g{};
