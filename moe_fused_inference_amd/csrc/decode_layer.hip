@@ -384,8 +384,13 @@ __device__ __forceinline__ bool poll_logits(const LayerArgs& a, uint32_t tag, fl
 // partial sums added in wave order -- published as (value, tag) words into
 // the logit copy of its XCD (blockIdx.x % 8), read by that XCD's gate/up and
 // down workgroups: every XCD computes all logits (8 x 16 router rows of
-// 1 KB each), so the hand-off to the routing stays in one L2.  Router
-// workgroup 0 also writes x_out / y_out.
+// 1 KB each), so the hand-off to the routing stays in one L2.  The words are
+// workgroup-scope stores (they stay in this XCD's L2, where the readers'
+// agent-scope polls find them): that relies on the round-robin dispatch of
+// workgroups to XCDs, which the copy index assumes; under another placement
+// a reader sees only an older tag, its bounded wait expires and the error
+// flag is set -- it never takes a stale logit.  Router workgroup 0 also
+// writes x_out / y_out.
 __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* nred, int ri) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -444,7 +449,7 @@ __device__ __forceinline__ void router_wg(const LayerArgs& a, Smem& sm, float* n
         if (idx < a.n_experts) {
             uint64_t* words = reinterpret_cast<uint64_t*>(a.ws + kLogOff) + (blockIdx.x & 7) * kLogCopy;
             __hip_atomic_store(words + idx, (uint64_t)__float_as_uint(lg) | ((uint64_t)(uint32_t)(launch + 1) << 32),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
             if (a.logits_out && (ri & 7) == 0) a.logits_out[idx] = lg;
         }
     }
